@@ -1,0 +1,512 @@
+// capi.cpp -- the extern "C" boundary declared in include/ferrum_gpu.h.
+//
+// Every entry point converts C++ exceptions into an FG_ERR_* status plus a
+// thread-local message, the C-ABI shape of the reference's Result<_, Error> ->
+// PyValueError mapping (crates/ferrum-gpu-py/src/lib.rs:404-406, 497, 577).
+#include <hip/hip_runtime_api.h>
+#include <string.h>
+
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <tuple>
+
+#include "device.hpp"
+#include "fft_plan.hpp"
+#include "ferrum_gpu.h"
+#include "hip_backend.hpp"
+
+using fg::Buffer;
+using fg::Cf32;
+using fg::Direction;
+using fg::Error;
+using fg::FftPlan;
+using fg::HipBackend;
+using fg::HipDevice;
+
+struct fg_device {
+    std::unique_ptr<HipDevice> dev;
+    HipBackend::Module fft_module;
+    std::mutex mu;  // guards the plan cache and the staging buffer of the host path
+    std::map<std::tuple<int, uint32_t, size_t>, std::unique_ptr<FftPlan>> plans;
+    Buffer<Cf32, HipBackend> staging;
+};
+
+struct fg_module {
+    HipBackend::Module mod;
+    HipBackend::DeviceHandle dev;
+    bool borrowed = false;  // the device's own FFT module: not unloaded by the caller
+};
+
+struct fg_kernel {
+    HipBackend::KernelHandle fn = nullptr;
+    HipBackend::Module keep;  // a kernel keeps its module loaded
+};
+
+struct fg_event {
+    hipEvent_t ev = nullptr;
+    int ordinal = 0;
+};
+
+struct fg_fft_plan {
+    std::unique_ptr<FftPlan> plan;
+    fg_device* dev = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        f();
+        g_last_error.clear();
+        return FG_OK;
+    } catch (const Error& e) {
+        g_last_error = e.what();
+        return e.code();
+    } catch (const std::bad_alloc&) {
+        g_last_error = "host allocation failed";
+        return FG_ERR_OUT_OF_MEMORY;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return FG_ERR_INTERNAL;
+    } catch (...) {
+        g_last_error = "unknown error";
+        return FG_ERR_INTERNAL;
+    }
+}
+
+void need(const void* p, const char* what) {
+    if (!p) fg::invalid(std::string(what) + " is null");
+}
+
+fg_device* open_device(int ordinal) {
+    auto h = HipBackend::open(ordinal);
+    std::unique_ptr<fg_device> d(new fg_device);
+    d->dev.reset(new HipDevice(h));
+    d->fft_module = d->dev->load_or_cache(fg::fft_code_object());
+    return d.release();
+}
+
+// The one-shot path's device (crates/ferrum-gpu-py/src/lib.rs:254-264 builds a
+// transient context per call; this keeps one per process instead).
+fg_device* default_device() {
+    static std::once_flag once;
+    static fg_device* dev = nullptr;
+    static std::string err;
+    static int code = 0;
+    std::call_once(once, [] {
+        try {
+            dev = open_device(0);
+        } catch (const Error& e) {
+            err = e.what();
+            code = e.code();
+        }
+    });
+    if (!dev) fg::fail(code ? code : FG_ERR_NO_DEVICE, err);
+    return dev;
+}
+
+FftPlan& cached_plan(fg_device* d, int dims, uint32_t log_n, size_t batch) {
+    auto key = std::make_tuple(dims, log_n, batch);
+    auto it = d->plans.find(key);
+    if (it != d->plans.end()) return *it->second;
+    auto p = dims == 1 ? FftPlan::make_1d(*d->dev, d->fft_module, log_n, batch)
+                       : FftPlan::make_2d(*d->dev, d->fft_module, log_n, batch);
+    FftPlan& ref = *p;
+    d->plans.emplace(key, std::move(p));
+    return ref;
+}
+
+Direction parse_dir(int direction) {
+    if (direction == FG_FORWARD) return Direction::Forward;
+    if (direction == FG_INVERSE) return Direction::Inverse;
+    fg::invalid("direction must be 1 (forward) or -1 (inverse), got " + std::to_string(direction));
+}
+
+// Host path shared by the 1D and 2D entry points: stage through one device
+// buffer (grown on demand, kept per device), run in place, copy back.
+void run_host(fg_device* d, int dims, uint32_t log_n, size_t batch, size_t total, const float* in, float* out,
+              Direction dir, bool normalize) {
+    std::lock_guard<std::mutex> g(d->mu);
+    FftPlan& plan = cached_plan(d, dims, log_n, batch);
+    if (d->staging.len() < total) {
+        d->staging.reset();
+        d->staging = d->dev->alloc<Cf32>(total);
+    }
+    const auto& h = d->dev->handle();
+    HipBackend::copy_async(h, d->staging.data(), in, total * sizeof(Cf32), hipMemcpyHostToDevice, nullptr);
+    plan.exec(d->staging.data(), d->staging.data(), dir, normalize, nullptr);
+    HipBackend::copy_async(h, out, d->staging.data(), total * sizeof(Cf32), hipMemcpyDeviceToHost, nullptr);
+    d->dev->sync();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fg_last_error(void) { return g_last_error.c_str(); }
+const char* fg_version(void) { return "0.3.0"; }
+int fg_backend_id(void) { return (int)HipBackend::id(); }
+
+int fg_device_count(int* count) {
+    return guarded([&] {
+        need(count, "count");
+        *count = HipBackend::device_count();
+    });
+}
+
+int fg_device_open(int ordinal, fg_device_t* out) {
+    return guarded([&] {
+        need(out, "out");
+        *out = nullptr;
+        *out = open_device(ordinal);
+    });
+}
+
+int fg_device_close(fg_device_t dev) {
+    return guarded([&] {
+        if (!dev) return;
+        try {
+            dev->dev->sync();
+        } catch (...) {
+        }
+        delete dev;
+    });
+}
+
+int fg_device_sync(fg_device_t dev) {
+    return guarded([&] {
+        need(dev, "device");
+        dev->dev->sync();
+    });
+}
+
+int fg_device_default_stream(fg_device_t dev, fg_stream_t* out) {
+    return guarded([&] {
+        need(dev, "device");
+        need(out, "out");
+        *out = (fg_stream_t)dev->dev->default_stream();
+    });
+}
+
+int fg_device_info(fg_device_t dev, char* arch, size_t arch_cap, int* cu_count, size_t* total_mem_bytes,
+                   int* clock_khz) {
+    return guarded([&] {
+        need(dev, "device");
+        const auto& h = dev->dev->handle();
+        if (arch && arch_cap) {
+            strncpy(arch, h->arch.c_str(), arch_cap - 1);
+            arch[arch_cap - 1] = 0;
+        }
+        if (cu_count) *cu_count = h->cu_count;
+        if (total_mem_bytes) *total_mem_bytes = h->total_mem;
+        if (clock_khz) *clock_khz = h->clock_khz;
+    });
+}
+
+int fg_alloc_zeros(fg_device_t dev, size_t bytes, void** dptr) {
+    return guarded([&] {
+        need(dev, "device");
+        need(dptr, "dptr");
+        *dptr = HipBackend::alloc_zeros(dev->dev->handle(), bytes);
+    });
+}
+
+int fg_free(fg_device_t dev, void* dptr) {
+    return guarded([&] {
+        need(dev, "device");
+        HipBackend::free(dev->dev->handle(), dptr);
+    });
+}
+
+int fg_copy_h2d(fg_device_t dev, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        need(dev, "device");
+        if (bytes) {
+            need(dst, "dst");
+            need(src, "src");
+        }
+        HipBackend::copy_h2d(dev->dev->handle(), dst, src, bytes);
+    });
+}
+
+int fg_copy_d2h(fg_device_t dev, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        need(dev, "device");
+        if (bytes) {
+            need(dst, "dst");
+            need(src, "src");
+        }
+        HipBackend::copy_d2h(dev->dev->handle(), dst, src, bytes);
+    });
+}
+
+static int copy_async(fg_device_t dev, void* dst, const void* src, size_t bytes, fg_stream_t stream,
+                      hipMemcpyKind kind) {
+    return guarded([&] {
+        need(dev, "device");
+        if (bytes) {
+            need(dst, "dst");
+            need(src, "src");
+        }
+        HipBackend::copy_async(dev->dev->handle(), dst, src, bytes, kind, (hipStream_t)stream);
+    });
+}
+
+int fg_copy_h2d_async(fg_device_t dev, void* dst, const void* src, size_t bytes, fg_stream_t stream) {
+    return copy_async(dev, dst, src, bytes, stream, hipMemcpyHostToDevice);
+}
+int fg_copy_d2h_async(fg_device_t dev, void* dst, const void* src, size_t bytes, fg_stream_t stream) {
+    return copy_async(dev, dst, src, bytes, stream, hipMemcpyDeviceToHost);
+}
+int fg_copy_d2d_async(fg_device_t dev, void* dst, const void* src, size_t bytes, fg_stream_t stream) {
+    return copy_async(dev, dst, src, bytes, stream, hipMemcpyDeviceToDevice);
+}
+
+int fg_module_load(fg_device_t dev, int backend_id, const void* image, size_t size, fg_module_t* out) {
+    return guarded([&] {
+        need(dev, "device");
+        need(out, "out");
+        *out = nullptr;
+        fg::KernelArtifact a;
+        a.backend = (fg::BackendId)backend_id;
+        a.name = "user";
+        a.image = image;
+        a.size = size;
+        std::unique_ptr<fg_module> m(new fg_module);
+        m->dev = dev->dev->handle();
+        m->mod = HipBackend::load_module(m->dev, a);
+        *out = m.release();
+    });
+}
+
+int fg_module_unload(fg_module_t mod) {
+    return guarded([&] {
+        if (!mod) return;
+        delete mod;  // the module itself unloads once no kernel holds it
+    });
+}
+
+int fg_device_fft_module(fg_device_t dev, fg_module_t* out) {
+    return guarded([&] {
+        need(dev, "device");
+        need(out, "out");
+        std::unique_ptr<fg_module> m(new fg_module);
+        m->dev = dev->dev->handle();
+        m->mod = dev->fft_module;
+        m->borrowed = true;
+        *out = m.release();
+    });
+}
+
+int fg_kernel_get(fg_module_t mod, const char* name, fg_kernel_t* out) {
+    return guarded([&] {
+        need(mod, "module");
+        need(name, "name");
+        need(out, "out");
+        *out = nullptr;
+        std::unique_ptr<fg_kernel> k(new fg_kernel);
+        k->fn = HipBackend::get_kernel(mod->mod, name);
+        k->keep = mod->mod;
+        *out = k.release();
+    });
+}
+
+int fg_launch(fg_device_t dev, fg_stream_t stream, fg_kernel_t kernel, const uint32_t grid[3],
+              const uint32_t block[3], uint32_t shared_bytes, void** args) {
+    return guarded([&] {
+        need(dev, "device");
+        need(kernel, "kernel");
+        need(grid, "grid");
+        need(block, "block");
+        HipBackend::launch(dev->dev->handle(), (hipStream_t)stream, kernel->fn, fg::Dim3(grid[0], grid[1], grid[2]),
+                           fg::Dim3(block[0], block[1], block[2]), shared_bytes, args);
+    });
+}
+
+int fg_stream_create(fg_device_t dev, fg_stream_t* out) {
+    return guarded([&] {
+        need(dev, "device");
+        need(out, "out");
+        *out = (fg_stream_t)HipBackend::create_stream(dev->dev->handle());
+    });
+}
+
+int fg_stream_destroy(fg_device_t dev, fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        HipBackend::destroy_stream(dev->dev->handle(), (hipStream_t)stream);
+    });
+}
+
+int fg_stream_sync(fg_device_t dev, fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        HipBackend::sync_stream(dev->dev->handle(), (hipStream_t)stream);
+    });
+}
+
+int fg_event_create(fg_device_t dev, fg_event_t* out) {
+    return guarded([&] {
+        need(dev, "device");
+        need(out, "out");
+        HipBackend::bind(dev->dev->handle());
+        std::unique_ptr<fg_event> e(new fg_event);
+        e->ordinal = dev->dev->handle()->ordinal;
+        fg::hip_check(hipEventCreate(&e->ev), "hipEventCreate");
+        *out = e.release();
+    });
+}
+
+int fg_event_destroy(fg_event_t ev) {
+    return guarded([&] {
+        if (!ev) return;
+        (void)hipSetDevice(ev->ordinal);
+        (void)hipEventDestroy(ev->ev);
+        delete ev;
+    });
+}
+
+int fg_event_record(fg_event_t ev, fg_stream_t stream) {
+    return guarded([&] {
+        need(ev, "event");
+        fg::hip_check(hipSetDevice(ev->ordinal), "hipSetDevice");
+        fg::hip_check(hipEventRecord(ev->ev, (hipStream_t)stream), "hipEventRecord");
+    });
+}
+
+int fg_event_sync(fg_event_t ev) {
+    return guarded([&] {
+        need(ev, "event");
+        fg::hip_check(hipEventSynchronize(ev->ev), "hipEventSynchronize");
+    });
+}
+
+int fg_event_elapsed_ms(fg_event_t start, fg_event_t end, float* ms) {
+    return guarded([&] {
+        need(start, "start");
+        need(end, "end");
+        need(ms, "ms");
+        fg::hip_check(hipEventElapsedTime(ms, start->ev, end->ev), "hipEventElapsedTime");
+    });
+}
+
+int fg_fft_plan_1d(fg_device_t dev, uint32_t log_n, size_t batch, fg_fft_plan_t* out) {
+    return guarded([&] {
+        need(dev, "device");
+        need(out, "out");
+        *out = nullptr;
+        std::unique_ptr<fg_fft_plan> p(new fg_fft_plan);
+        p->dev = dev;
+        p->plan = FftPlan::make_1d(*dev->dev, dev->fft_module, log_n, batch);
+        *out = p.release();
+    });
+}
+
+int fg_fft_plan_2d(fg_device_t dev, uint32_t log_n, size_t batch, fg_fft_plan_t* out) {
+    return guarded([&] {
+        need(dev, "device");
+        need(out, "out");
+        *out = nullptr;
+        std::unique_ptr<fg_fft_plan> p(new fg_fft_plan);
+        p->dev = dev;
+        p->plan = FftPlan::make_2d(*dev->dev, dev->fft_module, log_n, batch);
+        *out = p.release();
+    });
+}
+
+int fg_fft_plan_destroy(fg_fft_plan_t plan) {
+    return guarded([&] { delete plan; });
+}
+
+int fg_fft_exec(fg_fft_plan_t plan, const void* d_in, void* d_out, int direction, int normalize,
+                fg_stream_t stream) {
+    return guarded([&] {
+        need(plan, "plan");
+        need(d_in, "d_in");
+        need(d_out, "d_out");
+        plan->plan->exec(d_in, d_out, parse_dir(direction), normalize != 0, (hipStream_t)stream);
+    });
+}
+
+int fg_fft_plan_describe(fg_fft_plan_t plan, int* launches, char* main_kernel, size_t cap,
+                         size_t* workspace_bytes) {
+    return guarded([&] {
+        need(plan, "plan");
+        if (launches) *launches = plan->plan->launches();
+        if (main_kernel && cap) {
+            strncpy(main_kernel, plan->plan->main_kernel().c_str(), cap - 1);
+            main_kernel[cap - 1] = 0;
+        }
+        if (workspace_bytes) *workspace_bytes = plan->plan->workspace_bytes();
+    });
+}
+
+int fg_fft_1d_c2c_pow2_host(fg_device_t dev, const float* in, float* out, size_t total_complex, uint32_t log_n,
+                            int direction, int normalize) {
+    return guarded([&] {
+        // Argument checks and messages of crates/ferrum-gpu-py/src/lib.rs:455-477,
+        // with the log_n range widened to the two-pass limit.
+        if (log_n < fg::kMinLogN1D || log_n > fg::kMaxLogN1D)
+            fg::invalid("log_n must be in [" + std::to_string(fg::kMinLogN1D) + ", " +
+                        std::to_string(fg::kMaxLogN1D) + "], got " + std::to_string(log_n));
+        const size_t n = size_t(1) << log_n;
+        if (total_complex == 0 || total_complex % n != 0)
+            fg::invalid("arr len " + std::to_string(total_complex) + " must be a positive multiple of N = " +
+                        std::to_string(n));
+        Direction dir = parse_dir(direction);
+        need(in, "in");
+        need(out, "out");
+        fg_device* d = dev ? dev : default_device();
+        run_host(d, 1, log_n, total_complex / n, total_complex, in, out, dir, normalize != 0);
+    });
+}
+
+int fg_fft_2d_c2c_pow2_host(fg_device_t dev, const float* in, float* out, uint32_t log_n, size_t batch,
+                            int direction, int normalize) {
+    return guarded([&] {
+        // crates/ferrum-gpu-py/src/lib.rs:537-541
+        if (log_n < fg::kMinLogN2D || log_n > fg::kMaxLogN2D)
+            fg::invalid("2D requires log_n in [" + std::to_string(fg::kMinLogN2D) + ", " +
+                        std::to_string(fg::kMaxLogN2D) + "]; got " + std::to_string(log_n));
+        if (batch == 0) fg::invalid("batch must be positive");
+        Direction dir = parse_dir(direction);
+        need(in, "in");
+        need(out, "out");
+        fg_device* d = dev ? dev : default_device();
+        const size_t total = (size_t(1) << (2 * log_n)) * batch;
+        run_host(d, 2, log_n, batch, total, in, out, dir, normalize != 0);
+    });
+}
+
+int fg_stream_copy(fg_device_t dev, const void* d_in, void* d_out, size_t bytes, fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        need(d_in, "d_in");
+        need(d_out, "d_out");
+        if (bytes % 16) fg::invalid("fg_stream_copy: bytes must be a multiple of 16");
+        static thread_local HipBackend::KernelHandle k = nullptr;
+        static thread_local const void* k_mod = nullptr;
+        if (!k || k_mod != dev->fft_module.get()) {
+            k = HipBackend::get_kernel(dev->fft_module, "fg_copy_f4");
+            k_mod = dev->fft_module.get();
+        }
+        uint64_t n4 = bytes / 16;
+        const uint32_t block = 256;
+        uint64_t blocks = (n4 + block - 1) / block;
+        const uint64_t cap = (uint64_t)dev->dev->handle()->cu_count * 64;  // grid-stride beyond this
+        if (blocks > cap) blocks = cap;
+        if (blocks == 0) return;
+        const void* src = d_in;
+        void* dst = d_out;
+        void* args[] = {(void*)&src, &dst, &n4};
+        HipBackend::launch(dev->dev->handle(), (hipStream_t)stream, k, fg::Dim3((uint32_t)blocks),
+                           fg::Dim3(block), 0, args);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,163 @@
+// hip_backend.cpp -- HipBackend over libamdhip64 (the replacement of the
+// reference's cudarc-based `impl Backend for Cuda`,
+// crates/ferrum-gpu-cuda/src/backend_impl.rs:20-184).
+#include "hip_backend.hpp"
+
+#include <string.h>
+
+namespace fg {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return;
+    int code = FG_ERR_DRIVER;
+    if (e == hipErrorOutOfMemory) code = FG_ERR_OUT_OF_MEMORY;
+    else if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) code = FG_ERR_NO_DEVICE;
+    else if (e == hipErrorNotFound) code = FG_ERR_KERNEL_NOT_FOUND;
+    else if (e == hipErrorNoBinaryForGpu || e == hipErrorInvalidImage) code = FG_ERR_TARGET_MISMATCH;
+    fail(code, std::string(what) + " failed: " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+}
+
+HipDeviceState::~HipDeviceState() {
+    if (stream) {
+        (void)hipSetDevice(ordinal);
+        (void)hipStreamSynchronize(stream);
+        (void)hipStreamDestroy(stream);
+    }
+}
+
+HipModuleState::~HipModuleState() {
+    if (module) {
+        (void)hipSetDevice(ordinal);
+        (void)hipModuleUnload(module);
+    }
+}
+
+int HipBackend::device_count() {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice) return 0;
+    hip_check(e, "hipGetDeviceCount");
+    return n;
+}
+
+HipBackend::DeviceHandle HipBackend::open(int ordinal) {
+    int n = device_count();
+    if (n == 0) fail(FG_ERR_NO_DEVICE, "no HIP device is visible");
+    if (ordinal < 0 || ordinal >= n)
+        fail(FG_ERR_NO_DEVICE, "device ordinal " + std::to_string(ordinal) + " out of range (" +
+                                   std::to_string(n) + " visible)");
+    auto dev = std::make_shared<HipDeviceState>();
+    dev->ordinal = ordinal;
+    hip_check(hipSetDevice(ordinal), "hipSetDevice");
+    hipDeviceProp_t p;
+    hip_check(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
+    std::string arch = p.gcnArchName;
+    dev->arch = arch.substr(0, arch.find(':'));
+    dev->cu_count = p.multiProcessorCount;
+    dev->clock_khz = p.clockRate;
+    dev->total_mem = p.totalGlobalMem;
+    // Default priority on purpose: streams of different priorities are never mixed.
+    hip_check(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    return dev;
+}
+
+void HipBackend::bind(const DeviceHandle& dev) { hip_check(hipSetDevice(dev->ordinal), "hipSetDevice"); }
+
+void* HipBackend::alloc_zeros(const DeviceHandle& dev, size_t bytes) {
+    bind(dev);
+    void* p = nullptr;
+    if (bytes == 0) return nullptr;
+    hip_check(hipMalloc(&p, bytes), "hipMalloc");
+    hipError_t e = hipMemsetAsync(p, 0, bytes, dev->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        hip_check(e, "zero-fill of a new buffer");
+    }
+    return p;
+}
+
+void HipBackend::free(const DeviceHandle& dev, void* ptr) {
+    if (!ptr) return;
+    bind(dev);
+    hip_check(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+    hip_check(hipFree(ptr), "hipFree");
+}
+
+void HipBackend::copy_h2d(const DeviceHandle& dev, void* dst, const void* src, size_t bytes) {
+    if (!bytes) return;
+    bind(dev);
+    hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream), "hipMemcpyAsync(H2D)");
+    hip_check(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+}
+
+void HipBackend::copy_d2h(const DeviceHandle& dev, void* dst, const void* src, size_t bytes) {
+    if (!bytes) return;
+    bind(dev);
+    hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream), "hipMemcpyAsync(D2H)");
+    hip_check(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+}
+
+void HipBackend::copy_async(const DeviceHandle& dev, void* dst, const void* src, size_t bytes,
+                            hipMemcpyKind kind, Stream stream) {
+    if (!bytes) return;
+    bind(dev);
+    hip_check(hipMemcpyAsync(dst, src, bytes, kind, stream ? stream : dev->stream), "hipMemcpyAsync");
+}
+
+HipBackend::Module HipBackend::load_module(const DeviceHandle& dev, const KernelArtifact& art) {
+    // crates/ferrum-gpu-cuda/src/backend_impl.rs:79-81: refuse foreign artifacts.
+    if (art.backend != BackendId::Hip)
+        fail(FG_ERR_BACKEND_MISMATCH, "backend mismatch: expected " + std::to_string((int)BackendId::Hip) +
+                                          ", got " + std::to_string((int)art.backend));
+    if (!art.image || art.size == 0) invalid("module image is empty");
+    if (!art.target.empty() && art.target != dev->arch)
+        fail(FG_ERR_TARGET_MISMATCH, "code object targets " + art.target + " but device " +
+                                         std::to_string(dev->ordinal) + " is " + dev->arch);
+    bind(dev);
+    auto m = std::make_shared<HipModuleState>();
+    m->ordinal = dev->ordinal;
+    m->name = art.name;
+    hip_check(hipModuleLoadData(&m->module, art.image), "hipModuleLoadData");
+    return m;
+}
+
+HipBackend::KernelHandle HipBackend::get_kernel(const Module& mod, const char* name) {
+    hipFunction_t f = nullptr;
+    hip_check(hipSetDevice(mod->ordinal), "hipSetDevice");
+    hipError_t e = hipModuleGetFunction(&f, mod->module, name);
+    if (e != hipSuccess || !f) fail(FG_ERR_KERNEL_NOT_FOUND, std::string("kernel not found: ") + name);
+    return f;
+}
+
+void HipBackend::launch(const DeviceHandle& dev, Stream stream, KernelHandle k, Dim3 grid, Dim3 block,
+                        uint32_t shared_bytes, void** args) {
+    if (!k) invalid("launch of a null kernel");
+    if (grid.product() == 0 || block.product() == 0) invalid("launch with an empty grid or block");
+    if (block.product() > 1024) invalid("block of " + std::to_string(block.product()) + " threads exceeds 1024");
+    bind(dev);
+    hip_check(hipModuleLaunchKernel(k, grid.x, grid.y, grid.z, block.x, block.y, block.z, shared_bytes,
+                                    stream ? stream : dev->stream, args, nullptr),
+              "hipModuleLaunchKernel");
+}
+
+void HipBackend::sync_stream(const DeviceHandle& dev, Stream stream) {
+    bind(dev);
+    hip_check(hipStreamSynchronize(stream ? stream : dev->stream), "hipStreamSynchronize");
+}
+
+HipBackend::Stream HipBackend::create_stream(const DeviceHandle& dev) {
+    bind(dev);
+    hipStream_t s = nullptr;
+    hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    return s;
+}
+
+void HipBackend::destroy_stream(const DeviceHandle& dev, Stream s) {
+    if (!s) return;
+    bind(dev);
+    hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    hip_check(hipStreamDestroy(s), "hipStreamDestroy");
+}
+
+}  // namespace fg

@@ -1,0 +1,80 @@
+// hip_backend.hpp -- the Backend contract implemented over libamdhip64.
+//
+// Mirrors the reference's `Backend` trait (crates/ferrum-gpu-core/src/backend.rs:12-77)
+// as a C++ traits class: associated handle types plus static operations, so
+// `Device<B>` and `Buffer<T, B>` (device.hpp) stay generic over the backend the
+// way the Rust facade is.  This is the only file that talks to HIP.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <memory>
+#include <string>
+
+#include "backend.hpp"
+
+namespace fg {
+
+// Owned per-device state: the ordinal, the default stream (default priority)
+// and the properties read at open.
+struct HipDeviceState {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    std::string arch;  // gcnArchName up to the first ':' (e.g. "gfx950")
+    int cu_count = 0;
+    int clock_khz = 0;
+    size_t total_mem = 0;
+    ~HipDeviceState();
+};
+
+struct HipModuleState {
+    int ordinal = 0;
+    hipModule_t module = nullptr;
+    std::string name;
+    ~HipModuleState();
+};
+
+struct HipBackend {
+    using DeviceHandle = std::shared_ptr<HipDeviceState>;
+    using Stream = hipStream_t;
+    using Module = std::shared_ptr<HipModuleState>;
+    using KernelHandle = hipFunction_t;
+
+    static BackendId id() { return BackendId::Hip; }
+
+    static int device_count();
+    static DeviceHandle open(int ordinal);
+    // Makes the device current on the calling thread.
+    static void bind(const DeviceHandle& dev);
+
+    // Backend::alloc_zeros (backend.rs:30-33), in bytes.
+    static void* alloc_zeros(const DeviceHandle& dev, size_t bytes);
+    // Drop of the buffer (crates/ferrum-gpu-cuda/src/buffer.rs:45-56).
+    static void free(const DeviceHandle& dev, void* ptr);
+    // Backend::copy_h2d / copy_d2h (backend.rs:35-47): synchronous.
+    static void copy_h2d(const DeviceHandle& dev, void* dst, const void* src, size_t bytes);
+    static void copy_d2h(const DeviceHandle& dev, void* dst, const void* src, size_t bytes);
+    static void copy_async(const DeviceHandle& dev, void* dst, const void* src, size_t bytes,
+                           hipMemcpyKind kind, Stream stream);
+
+    // Backend::load_module (backend.rs:50-53): refuses artifacts of another
+    // backend or gfx target.
+    static Module load_module(const DeviceHandle& dev, const KernelArtifact& art);
+    // Backend::get_kernel (backend.rs:56-59).
+    static KernelHandle get_kernel(const Module& mod, const char* name);
+    // Backend::launch (backend.rs:62-70): args[i] points at argument i's bytes.
+    static void launch(const DeviceHandle& dev, Stream stream, KernelHandle k, Dim3 grid, Dim3 block,
+                       uint32_t shared_bytes, void** args);
+
+    // Backend::default_stream / sync_stream (backend.rs:73-76).
+    static Stream default_stream(const DeviceHandle& dev) { return dev->stream; }
+    static void sync_stream(const DeviceHandle& dev, Stream stream);
+
+    static Stream create_stream(const DeviceHandle& dev);
+    static void destroy_stream(const DeviceHandle& dev, Stream s);
+};
+
+// Throws fg::Error(FG_ERR_DRIVER or a closer code) naming the failed call.
+void hip_check(hipError_t e, const char* what);
+
+}  // namespace fg

@@ -1,0 +1,133 @@
+// fft_common.hpp -- device-side building blocks shared by every FFT kernel:
+// complex helpers and in-register forward DFTs of size 2, 4, 8 and 16.
+//
+// Complex values are float2 (x = re, y = im), the interleaved complex64 layout
+// of the reference's Complex32 (crates/ferrum-gpu-fft/src/complex.rs:10-53).
+// All butterflies compute the forward transform X_k = sum_n x_n W^{nk} with
+// W = exp(-2 pi i / R); the inverse is obtained by conjugating on load and on
+// store, the same identity the reference applies on the host
+// (crates/ferrum-gpu-fft/src/cpu.rs:106-121).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fg {
+
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+    return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+__device__ __forceinline__ float2 cconj(float2 a) { return make_float2(a.x, -a.y); }
+__device__ __forceinline__ float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
+// a * (-i)
+__device__ __forceinline__ float2 cmul_negi(float2 a) { return make_float2(a.y, -a.x); }
+
+// cos/sin of multiples of pi/8 (exact mathematics, not library constants).
+constexpr float kC8 = 0.92387953251128675613f;  // cos(pi/8)
+constexpr float kS8 = 0.38268343236508977173f;  // sin(pi/8)
+constexpr float kR2 = 0.70710678118654752440f;  // cos(pi/4) = sin(pi/4)
+
+template <int R>
+struct Dft;
+
+template <>
+struct Dft<1> {
+    __device__ __forceinline__ static void run(float2*) {}
+};
+
+template <>
+struct Dft<2> {
+    __device__ __forceinline__ static void run(float2* v) {
+        float2 a = v[0], b = v[1];
+        v[0] = cadd(a, b);
+        v[1] = csub(a, b);
+    }
+};
+
+template <>
+struct Dft<4> {
+    // X0 = (x0+x2)+(x1+x3); X2 = (x0+x2)-(x1+x3);
+    // X1 = (x0-x2) - i(x1-x3); X3 = (x0-x2) + i(x1-x3).
+    __device__ __forceinline__ static void run(float2* v) {
+        float2 a = cadd(v[0], v[2]), b = csub(v[0], v[2]);
+        float2 c = cadd(v[1], v[3]), d = csub(v[1], v[3]);
+        v[0] = cadd(a, c);
+        v[2] = csub(a, c);
+        v[1] = make_float2(b.x + d.y, b.y - d.x);
+        v[3] = make_float2(b.x - d.y, b.y + d.x);
+    }
+};
+
+template <>
+struct Dft<8> {
+    // Decimation in time: E = DFT4(even), O = DFT4(odd),
+    // X_q = E_q + W8^q O_q, X_{q+4} = E_q - W8^q O_q.
+    __device__ __forceinline__ static void run(float2* v) {
+        float2 e[4] = {v[0], v[2], v[4], v[6]};
+        float2 o[4] = {v[1], v[3], v[5], v[7]};
+        Dft<4>::run(e);
+        Dft<4>::run(o);
+        float2 w1 = make_float2(kR2 * (o[1].x + o[1].y), kR2 * (o[1].y - o[1].x));   // W8^1 = (r,-r)
+        float2 w2 = cmul_negi(o[2]);                                                  // W8^2 = -i
+        float2 w3 = make_float2(kR2 * (o[3].y - o[3].x), -kR2 * (o[3].x + o[3].y));  // W8^3 = (-r,-r)
+        v[0] = cadd(e[0], o[0]);
+        v[4] = csub(e[0], o[0]);
+        v[1] = cadd(e[1], w1);
+        v[5] = csub(e[1], w1);
+        v[2] = cadd(e[2], w2);
+        v[6] = csub(e[2], w2);
+        v[3] = cadd(e[3], w3);
+        v[7] = csub(e[3], w3);
+    }
+};
+
+template <>
+struct Dft<16> {
+    // 16 = 4 x 4: n = 4*n1 + n2, k = k1 + 4*k2.
+    //   Y[n2][k1] = DFT4_{n1} x[4 n1 + n2];  Y[n2][k1] *= W16^{n2 k1};
+    //   X[k1 + 4 k2] = DFT4_{n2} Y[n2][k1].
+    __device__ __forceinline__ static void run(float2* v) {
+        float2 y[4][4];
+#pragma unroll
+        for (int n2 = 0; n2 < 4; ++n2) {
+            y[n2][0] = v[n2];
+            y[n2][1] = v[4 + n2];
+            y[n2][2] = v[8 + n2];
+            y[n2][3] = v[12 + n2];
+            Dft<4>::run(y[n2]);
+        }
+        // n2 = 1: W16^1, W16^2, W16^3
+        y[1][1] = cmul(y[1][1], make_float2(kC8, -kS8));
+        y[1][2] = make_float2(kR2 * (y[1][2].x + y[1][2].y), kR2 * (y[1][2].y - y[1][2].x));
+        y[1][3] = cmul(y[1][3], make_float2(kS8, -kC8));
+        // n2 = 2: W16^2, W16^4, W16^6
+        y[2][1] = make_float2(kR2 * (y[2][1].x + y[2][1].y), kR2 * (y[2][1].y - y[2][1].x));
+        y[2][2] = cmul_negi(y[2][2]);
+        y[2][3] = make_float2(kR2 * (y[2][3].y - y[2][3].x), -kR2 * (y[2][3].x + y[2][3].y));
+        // n2 = 3: W16^3, W16^6, W16^9
+        y[3][1] = cmul(y[3][1], make_float2(kS8, -kC8));
+        y[3][2] = make_float2(kR2 * (y[3][2].y - y[3][2].x), -kR2 * (y[3][2].x + y[3][2].y));
+        y[3][3] = cmul(y[3][3], make_float2(-kC8, kS8));
+#pragma unroll
+        for (int k1 = 0; k1 < 4; ++k1) {
+            float2 z[4] = {y[0][k1], y[1][k1], y[2][k1], y[3][k1]};
+            Dft<4>::run(z);
+            v[k1] = z[0];
+            v[k1 + 4] = z[1];
+            v[k1 + 8] = z[2];
+            v[k1 + 12] = z[3];
+        }
+    }
+};
+
+// Wave-scope ordering of LDS traffic: a wave's LDS operations execute in
+// program order, so a compiler-level barrier plus wavefront-scope fences is
+// enough between one wave's LDS writes and its own later reads.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace fg

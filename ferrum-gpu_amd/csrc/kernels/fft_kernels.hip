@@ -1,0 +1,61 @@
+// fft_kernels.hip -- the gfx950 code object loaded by the HIP backend.
+//
+// Every kernel has an unmangled extern "C" name so the host looks it up with
+// hipModuleGetFunction, the way the reference's host runner looks up the
+// kernels of its embedded module (crates/ferrum-gpu-py/src/lib.rs:54-79).
+//
+// Built by ferrum-gpu_amd/csrc/Makefile with
+//   hipcc --genco --offload-arch=gfx950 -O3 -Xclang -target-feature -Xclang -packed-fp32-ops
+#include "fft_stockham.hpp"
+
+using namespace fg;
+
+// Launch geometry is fixed per kernel and mirrored on the host in
+// fft_plan.cpp (kStockhamTable): LOGE = min(4, LOGN); FPB transforms per
+// workgroup of FPB * (N / E) threads.
+#define FG_STOCKHAM(LOGN, LOGE, FPB)                                                        \
+    extern "C" __global__ __launch_bounds__(FPB * ((1 << LOGN) >> LOGE)) void                \
+        fg_fft_n##LOGN##_fwd(const float2* __restrict__ in, float2* __restrict__ out,        \
+                             const float2* __restrict__ tw, uint64_t batch, float scale) {  \
+        fft_stockham_body<LOGN, LOGE, FPB, false>(in, out, tw, batch, scale);               \
+    }                                                                                        \
+    extern "C" __global__ __launch_bounds__(FPB * ((1 << LOGN) >> LOGE)) void                \
+        fg_fft_n##LOGN##_inv(const float2* __restrict__ in, float2* __restrict__ out,        \
+                             const float2* __restrict__ tw, uint64_t batch, float scale) {  \
+        fft_stockham_body<LOGN, LOGE, FPB, true>(in, out, tw, batch, scale);                \
+    }
+
+FG_STOCKHAM(2, 2, 64)    // N=4:    1 thread  / transform, 64 per wave
+FG_STOCKHAM(3, 3, 64)    // N=8:    1 thread  / transform
+FG_STOCKHAM(4, 4, 64)    // N=16:   1 thread  / transform
+FG_STOCKHAM(5, 4, 32)    // N=32:   2 threads / transform
+FG_STOCKHAM(6, 4, 16)    // N=64:   4 threads
+FG_STOCKHAM(7, 4, 8)     // N=128:  8 threads
+FG_STOCKHAM(8, 4, 4)     // N=256:  16 threads
+FG_STOCKHAM(9, 4, 2)     // N=512:  32 threads
+FG_STOCKHAM(10, 4, 1)    // N=1024: 64 threads (one wave per transform)
+FG_STOCKHAM(11, 4, 1)    // N=2048: 128 threads
+FG_STOCKHAM(12, 4, 1)    // N=4096: 256 threads
+
+// ---------------------------------------------------------------- utilities
+
+// Streaming copy, 16 bytes per lane: the bandwidth yardstick the bench
+// reports beside the FFT, and the known-size kernel used to scale rocprof's
+// FETCH_SIZE / WRITE_SIZE counters.
+extern "C" __global__ __launch_bounds__(256) void fg_copy_f4(const float4* __restrict__ in,
+                                                             float4* __restrict__ out,
+                                                             uint64_t n4) {
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (; i < n4; i += stride) out[i] = in[i];
+}
+
+// c = a + b over n floats: the substrate smoke kernel (the reference's
+// hand-written vector_add, examples/vector-add/src/main.rs:17-60).
+extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __restrict__ a,
+                                                                const float* __restrict__ b,
+                                                                float* __restrict__ c,
+                                                                uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) c[i] = a[i] + b[i];
+}

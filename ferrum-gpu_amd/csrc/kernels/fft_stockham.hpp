@@ -1,0 +1,172 @@
+// fft_stockham.hpp -- LDS-resident batched power-of-two C2C FFT for
+// N = 2^LOGN <= 4096, one (or several) transforms per workgroup.
+//
+// Algorithm: mixed-radix Stockham autosort, the same stage recurrence as the
+// reference's radix-4/radix-8 specs (crates/ferrum-gpu-fft/src/cpu_radix4.rs:6-9,
+// cpu_radix8.rs:11-15) generalised to a radix list (E, E, ..., E, r) with
+// E = 2^LOGE elements held in VGPRs per thread:
+//   stage s, radix R, L = product of earlier radices, butterfly b = j*L + k:
+//     gather  src[b + p*(N/R)]              p in [0, R)
+//     twiddle t_p = W_{L*R}^{p*k} * src_p    (table; none when L == 1)
+//     DFT-R   X = DFT_R(t)
+//     scatter dst[j*L*R + k + q*L] = X_q    q in [0, R)
+// Thread t of a transform always gathers positions t + T*m (m in [0, E)), so
+// the first stage reads global memory coalesced; the last stage has j == 0 and
+// scatters to positions t + T*m as well, so it writes global memory coalesced.
+// Intermediate stages exchange through LDS with one pad slot per 16 entries,
+// which breaks the stride-E pattern of the first scatter across LDS banks.
+//
+// Inverse: conjugate on load, conjugate (and scale) on store.
+#pragma once
+#include "fft_common.hpp"
+
+namespace fg {
+
+template <int LOGN, int LOGE>
+struct StockhamShape {
+    static constexpr int N = 1 << LOGN;
+    static constexpr int E = 1 << LOGE;                  // elements per thread
+    static constexpr int T = N / E;                      // threads per transform
+    static constexpr int NFULL = LOGN / LOGE;            // radix-E stages
+    static constexpr int REM = LOGN % LOGE;              // log2 of the tail radix
+    static constexpr int NSTAGES = NFULL + (REM ? 1 : 0);
+    static constexpr int LDS_ELEMS = N + N / 16;         // padded transform
+    static_assert(LOGE <= LOGN, "more elements per thread than points");
+};
+
+// Padded LDS slot of logical position p.
+__device__ __forceinline__ int lds_pos(int p) { return p + (p >> 4); }
+
+// Offset (in complex entries) of stage s's block in the twiddle table built by
+// the host for this radix list; stage 0 has no block.  Block of stage s holds
+// L*R entries [k][p] = W_{L*R}^{p*k}.
+template <int LOGN, int LOGE>
+__host__ __device__ constexpr int stockham_tw_offset(int s) {
+    int off = 0;
+    for (int i = 1; i < s; ++i) {
+        int logl = i * LOGE;
+        int logr = (i < LOGN / LOGE) ? LOGE : (LOGN % LOGE);
+        off += 1 << (logl + logr);
+    }
+    return off;
+}
+
+// Processes one stage's butterflies for a thread: x holds the E gathered
+// elements (position t + T*m at index m); on return x holds the outputs laid
+// out so that output q of butterfly i sits at index i + NB*q.
+template <int LOGN, int LOGE, int S>
+__device__ __forceinline__ void stockham_stage_regs(float2* x, int t, const float2* __restrict__ tw) {
+    using Sh = StockhamShape<LOGN, LOGE>;
+    constexpr int LOGR = (S < Sh::NFULL) ? LOGE : Sh::REM;
+    constexpr int R = 1 << LOGR;
+    constexpr int NB = Sh::E / R;       // butterflies per thread
+    constexpr int LOGL = S * LOGE;
+    constexpr int L = 1 << LOGL;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        float2 u[R];
+#pragma unroll
+        for (int p = 0; p < R; ++p) u[p] = x[i + NB * p];
+        if constexpr (L > 1) {
+            const int b = t + Sh::T * i;
+            const int k = b & (L - 1);
+            const float2* w = tw + stockham_tw_offset<LOGN, LOGE>(S) + k * R;
+            if constexpr (R >= 2 && (R % 2) == 0) {
+                // Rows are R-aligned, so pairs of entries load as 16-byte vectors.
+                const float4* w4 = reinterpret_cast<const float4*>(w);
+#pragma unroll
+                for (int p2 = 0; p2 < R / 2; ++p2) {
+                    float4 ww = w4[p2];
+                    if (p2 > 0) u[2 * p2] = cmul(u[2 * p2], make_float2(ww.x, ww.y));
+                    u[2 * p2 + 1] = cmul(u[2 * p2 + 1], make_float2(ww.z, ww.w));
+                }
+            }
+        }
+        Dft<R>::run(u);
+#pragma unroll
+        for (int q = 0; q < R; ++q) x[i + NB * q] = u[q];
+    }
+}
+
+// Destination position of output (i, q) of stage S for thread t.
+template <int LOGN, int LOGE, int S>
+__device__ __forceinline__ int stockham_dst(int t, int i, int q) {
+    using Sh = StockhamShape<LOGN, LOGE>;
+    constexpr int LOGR = (S < Sh::NFULL) ? LOGE : Sh::REM;
+    constexpr int R = 1 << LOGR;
+    constexpr int L = 1 << (S * LOGE);
+    const int b = t + Sh::T * i;
+    const int j = b >> (S * LOGE);
+    const int k = b & (L - 1);
+    return j * L * R + k + q * L;
+}
+
+template <int LOGN, int LOGE, int S>
+struct StockhamStages {
+    using Sh = StockhamShape<LOGN, LOGE>;
+    // Runs stage S (already gathered in x) and every later stage.
+    template <bool ONE_WAVE>
+    __device__ __forceinline__ static void run(float2* x, int t, const float2* __restrict__ tw,
+                                               float2* __restrict__ lds) {
+        stockham_stage_regs<LOGN, LOGE, S>(x, t, tw);
+        if constexpr (S + 1 < Sh::NSTAGES) {
+            constexpr int LOGR = (S < Sh::NFULL) ? LOGE : Sh::REM;
+            constexpr int NB = Sh::E >> LOGR;
+            constexpr int R = 1 << LOGR;
+#pragma unroll
+            for (int i = 0; i < NB; ++i)
+#pragma unroll
+                for (int q = 0; q < R; ++q)
+                    lds[lds_pos(stockham_dst<LOGN, LOGE, S>(t, i, q))] = x[i + NB * q];
+            if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
+#pragma unroll
+            for (int m = 0; m < Sh::E; ++m) x[m] = lds[lds_pos(t + Sh::T * m)];
+            if constexpr (S + 2 < Sh::NSTAGES) {
+                if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
+            }
+            StockhamStages<LOGN, LOGE, S + 1>::template run<ONE_WAVE>(x, t, tw, lds);
+        }
+    }
+};
+
+// Kernel body: FPB transforms per workgroup of FPB*T threads.
+template <int LOGN, int LOGE, int FPB, bool INV>
+__device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
+                                                  float2* __restrict__ out,
+                                                  const float2* __restrict__ tw,
+                                                  uint64_t batch, float scale) {
+    using Sh = StockhamShape<LOGN, LOGE>;
+    constexpr bool ONE_WAVE = (Sh::T * FPB) <= 64;
+    __shared__ float2 lds_all[FPB][Sh::LDS_ELEMS];
+    const int tid = threadIdx.x;
+    const int slot = tid / Sh::T;
+    const int t = tid - slot * Sh::T;
+    const uint64_t f = (uint64_t)blockIdx.x * FPB + slot;
+    const bool valid = f < batch;
+    const float2* src = in + f * Sh::N;
+    float2* dst = out + f * Sh::N;
+
+    float2 x[Sh::E];
+    if (valid) {
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = src[t + Sh::T * m];
+    } else {
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = make_float2(0.f, 0.f);
+    }
+    if constexpr (INV) {
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = cconj(x[m]);
+    }
+    StockhamStages<LOGN, LOGE, 0>::template run<ONE_WAVE>(x, t, tw, lds_all[slot]);
+    if (valid) {
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) {
+            float2 v = x[m];
+            if constexpr (INV) v = cscale(cconj(v), scale);
+            dst[t + Sh::T * m] = v;
+        }
+    }
+}
+
+}  // namespace fg

@@ -1,0 +1,182 @@
+"""ferrum_gpu.fft -- batched power-of-two C2C complex64 FFTs on MI355X.
+
+``fft_1d_c2c_pow2`` and ``fft_2d_c2c_pow2`` keep the reference's signatures,
+argument meaning and error messages (crates/ferrum-gpu-py/src/lib.rs:425-588).
+Two deliberate widenings: 1D accepts ``log_n`` up to 24 (the reference stops at
+12, lib.rs:455-459), and 2D also accepts a ``(B, N, N)`` stack of images.
+
+``Plan1D`` / ``Plan2D`` are the device-resident form: plan once, then execute
+on device buffers with no host copies (what the bench measures).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import operator
+
+import numpy as np
+
+from ferrum_gpu import _native as _n
+from ferrum_gpu.hip import Device, DeviceBuffer
+
+__all__ = ["fft_1d_c2c_pow2", "fft_2d_c2c_pow2", "Plan1D", "Plan2D", "MIN_LOG_N", "MAX_LOG_N",
+           "MIN_LOG_N_2D", "MAX_LOG_N_2D"]
+
+MIN_LOG_N, MAX_LOG_N = 2, 24
+MIN_LOG_N_2D, MAX_LOG_N_2D = 4, 12
+
+
+def _as_u32(log_n) -> int:
+    # PyO3 extracts log_n as u32: non-integers raise TypeError, negatives OverflowError.
+    try:
+        v = operator.index(log_n)
+    except TypeError:
+        raise TypeError(f"argument 'log_n': '{type(log_n).__name__}' object cannot be interpreted as an integer")
+    if v < 0 or v > 0xFFFFFFFF:
+        raise OverflowError("argument 'log_n': can't convert to u32")
+    return v
+
+
+def _direction(direction) -> int:
+    if direction == "forward":
+        return _n.FG_FORWARD
+    if direction == "inverse":
+        return _n.FG_INVERSE
+    # Rust formats the offending string with {:?} (double-quoted), lib.rs:472-476.
+    raise ValueError(f"direction must be 'forward' or 'inverse', got \"{direction}\"")
+
+
+def _device_handle(device):
+    if device is None:
+        return None
+    if not isinstance(device, Device):
+        raise TypeError(f"argument 'device': expected ferrum_gpu.hip.Device, got {type(device).__name__}")
+    return device.handle
+
+
+def _complex64_array(arr, ndims: tuple[int, ...]) -> np.ndarray:
+    # PyReadonlyArray{1,2}<Complex32> + as_slice(): a complex64 ndarray of the
+    # right rank, C-contiguous (lib.rs:449, 461, 531, 560).
+    if not isinstance(arr, np.ndarray):
+        raise TypeError(f"argument 'arr': '{type(arr).__name__}' object cannot be converted to 'PyArray'")
+    if arr.dtype != np.complex64:
+        raise TypeError(f"argument 'arr': type mismatch: from={arr.dtype}, to=complex64")
+    if arr.ndim not in ndims:
+        raise TypeError(f"argument 'arr': dimensionality mismatch: from={arr.ndim}, to={ndims[0]}")
+    if not arr.flags.c_contiguous:
+        raise TypeError("The given array is not contiguous")
+    return arr
+
+
+def fft_1d_c2c_pow2(arr, log_n, direction="forward", normalize=False, device=None):
+    """FFT of a 1D ``complex64`` numpy array of length ``batch * 2**log_n``.
+
+    Arguments mirror crates/ferrum-gpu-py/src/lib.rs:425-444: ``direction`` is
+    "forward" (default) or "inverse"; ``normalize`` scales the inverse by 1/N;
+    ``device`` is an optional persistent :class:`ferrum_gpu.hip.Device`.
+    Returns a new ``complex64`` array of the same length.
+    """
+    a = _complex64_array(arr, (1,))
+    log_n = _as_u32(log_n)
+    if not (MIN_LOG_N <= log_n <= MAX_LOG_N):
+        raise ValueError(f"log_n must be in [{MIN_LOG_N}, {MAX_LOG_N}], got {log_n}")
+    n = 1 << log_n
+    total = a.size
+    if total == 0 or total % n != 0:
+        raise ValueError(f"arr len {total} must be a positive multiple of N = {n}")
+    d = _direction(direction)
+    h = _device_handle(device)
+    out = np.empty_like(a)
+    rc = _n.lib.fg_fft_1d_c2c_pow2_host(h, a.ctypes.data, out.ctypes.data, total, log_n, d, int(bool(normalize)))
+    if rc != _n.FG_OK:
+        raise ValueError(f"ferrum-gpu fft error: {_n.last_error()}")
+    return out
+
+
+def fft_2d_c2c_pow2(arr, log_n, direction="forward", normalize=False, device=None):
+    """2D FFT of a square ``complex64`` array of shape ``(N, N)`` (or ``(B, N, N)``).
+
+    Arguments mirror crates/ferrum-gpu-py/src/lib.rs:506-526; ``normalize``
+    scales the inverse by 1/(N*N).  Returns a new array of the same shape.
+    """
+    a = _complex64_array(arr, (2, 3))
+    log_n = _as_u32(log_n)
+    if not (MIN_LOG_N_2D <= log_n <= MAX_LOG_N_2D):
+        raise ValueError(f"2D requires log_n in [{MIN_LOG_N_2D}, {MAX_LOG_N_2D}]; got {log_n}")
+    n = 1 << log_n
+    dims = list(a.shape)
+    if dims[-2:] != [n, n] or (a.ndim == 3 and dims[0] == 0):
+        raise ValueError(f"arr shape {dims} != ({n}, {n})")
+    d = _direction(direction)
+    h = _device_handle(device)
+    batch = 1 if a.ndim == 2 else dims[0]
+    out = np.empty_like(a)
+    rc = _n.lib.fg_fft_2d_c2c_pow2_host(h, a.ctypes.data, out.ctypes.data, log_n, batch, d, int(bool(normalize)))
+    if rc != _n.FG_OK:
+        raise ValueError(f"ferrum-gpu fft 2d error: {_n.last_error()}")
+    return out
+
+
+def _ptr(x) -> ctypes.c_void_p:
+    if isinstance(x, DeviceBuffer):
+        return ctypes.c_void_p(x.ptr)
+    if hasattr(x, "data_ptr"):  # a torch tensor on the GPU
+        return ctypes.c_void_p(x.data_ptr())
+    return ctypes.c_void_p(int(x))
+
+
+class _Plan:
+    def __init__(self, device: Device, handle: ctypes.c_void_p, elems: int, batch: int):
+        self.device = device
+        self._p = handle
+        self.elems = elems
+        self.batch = batch
+
+    @property
+    def nbytes(self) -> int:
+        """Bytes of one input (or output) buffer: batch * elems * 8."""
+        return self.batch * self.elems * 8
+
+    def execute(self, d_in, d_out, direction="forward", normalize=False, stream: int = 0) -> None:
+        """Stream-ordered, asynchronous execution on device buffers (may alias)."""
+        d = _direction(direction)
+        _n.check(_n.lib.fg_fft_exec(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),
+                                    ctypes.c_void_p(stream or None)))
+
+    def describe(self) -> dict:
+        launches = ctypes.c_int()
+        name = ctypes.create_string_buffer(128)
+        ws = ctypes.c_size_t()
+        _n.check(_n.lib.fg_fft_plan_describe(self._p, ctypes.byref(launches), name, 128, ctypes.byref(ws)))
+        return {"launches": launches.value, "main_kernel": name.value.decode(), "workspace_bytes": ws.value}
+
+    def destroy(self) -> None:
+        if getattr(self, "_p", None) is not None and self._p.value:
+            _n.lib.fg_fft_plan_destroy(self._p)
+        self._p = ctypes.c_void_p()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class Plan1D(_Plan):
+    """Plan for ``batch`` transforms of length ``2**log_n`` (Plan::new, plan.rs:57-68)."""
+
+    def __init__(self, log_n: int, batch: int, device: Device):
+        p = ctypes.c_void_p()
+        _n.check(_n.lib.fg_fft_plan_1d(device.handle, int(log_n), int(batch), ctypes.byref(p)))
+        super().__init__(device, p, 1 << int(log_n), int(batch))
+        self.log_n = int(log_n)
+
+
+class Plan2D(_Plan):
+    """Plan for ``batch`` N x N images, N = ``2**log_n`` (Plan2D::new, plan.rs:111-119)."""
+
+    def __init__(self, log_n: int, batch: int, device: Device):
+        p = ctypes.c_void_p()
+        _n.check(_n.lib.fg_fft_plan_2d(device.handle, int(log_n), int(batch), ctypes.byref(p)))
+        super().__init__(device, p, 1 << (2 * int(log_n)), int(batch))
+        self.log_n = int(log_n)

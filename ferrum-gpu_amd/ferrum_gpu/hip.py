@@ -1,0 +1,182 @@
+"""ferrum_gpu.hip -- the device handle and the substrate objects over HIP.
+
+``Device`` is the HIP counterpart of the reference's ``ferrum_gpu.cuda.Device``
+(crates/ferrum-gpu-py/src/lib.rs:389-417, python/ferrum_gpu/cuda.py): construct
+once, pass as ``device=`` to the FFT functions, ``sync()`` the default stream.
+``DeviceBuffer``, ``Event``, ``Module`` and ``Kernel`` expose the rest of the
+Backend contract (crates/ferrum-gpu-core/src/backend.rs:12-77) for
+device-resident work and for the bench.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from ferrum_gpu import _native as _n
+
+__all__ = ["Device", "DeviceBuffer", "Event", "Module", "Kernel", "device_count"]
+
+
+def device_count() -> int:
+    c = ctypes.c_int(0)
+    _n.check(_n.lib.fg_device_count(ctypes.byref(c)))
+    return c.value
+
+
+class Device:
+    """A GPU with its default stream and loaded FFT code object."""
+
+    def __init__(self, ordinal: int = 0):
+        h = ctypes.c_void_p()
+        rc = _n.lib.fg_device_open(int(ordinal), ctypes.byref(h))
+        if rc != _n.FG_OK:
+            # crates/ferrum-gpu-py/src/lib.rs:403-406 reports ValueError.
+            raise ValueError(f"Device::new({ordinal}): {_n.last_error()}")
+        self._h = h
+        self.ordinal = int(ordinal)
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        if self._h is None:
+            raise ValueError("device is closed")
+        return self._h
+
+    def sync(self) -> None:
+        """Synchronise the default stream (lib.rs:410-416)."""
+        rc = _n.lib.fg_device_sync(self.handle)
+        if rc != _n.FG_OK:
+            raise ValueError(f"sync: {_n.last_error()}")
+
+    @property
+    def default_stream(self) -> int:
+        s = ctypes.c_void_p()
+        _n.check(_n.lib.fg_device_default_stream(self.handle, ctypes.byref(s)))
+        return s.value or 0
+
+    def info(self) -> dict:
+        arch = ctypes.create_string_buffer(64)
+        cu, mem, clk = ctypes.c_int(), ctypes.c_size_t(), ctypes.c_int()
+        _n.check(_n.lib.fg_device_info(self.handle, arch, 64, ctypes.byref(cu), ctypes.byref(mem),
+                                       ctypes.byref(clk)))
+        return {"arch": arch.value.decode(), "cu_count": cu.value, "total_mem": mem.value,
+                "clock_khz": clk.value}
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None:
+            _n.lib.fg_device_close(self._h)
+            self._h = None
+
+    def __del__(self):  # pragma: no cover - interpreter teardown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __repr__(self) -> str:
+        return f"ferrum_gpu.hip.Device({self.ordinal})"
+
+
+class DeviceBuffer:
+    """A zero-initialised device allocation (Buffer<T, B>, crates/ferrum-gpu/src/buffer.rs:8-47)."""
+
+    def __init__(self, device: Device, nbytes: int):
+        self.device = device
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        _n.check(_n.lib.fg_alloc_zeros(device.handle, self.nbytes, ctypes.byref(p)))
+        self._p = p
+
+    @property
+    def ptr(self) -> int:
+        return self._p.value or 0
+
+    def copy_from_host(self, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr)
+        if a.nbytes > self.nbytes:
+            raise ValueError("copy_from_host: source longer than the buffer")
+        _n.check(_n.lib.fg_copy_h2d(self.device.handle, self._p, a.ctypes.data, a.nbytes))
+
+    def copy_to_host(self, out: np.ndarray) -> np.ndarray:
+        if not out.flags.c_contiguous or out.nbytes > self.nbytes:
+            raise ValueError("copy_to_host: destination must be contiguous and fit the buffer")
+        _n.check(_n.lib.fg_copy_d2h(self.device.handle, out.ctypes.data, self._p, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if getattr(self, "_p", None) is not None and self._p.value:
+            _n.lib.fg_free(self.device.handle, self._p)
+        self._p = ctypes.c_void_p()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Event:
+    """A HIP event for stream-ordered timing."""
+
+    def __init__(self, device: Device):
+        e = ctypes.c_void_p()
+        _n.check(_n.lib.fg_event_create(device.handle, ctypes.byref(e)))
+        self._e = e
+
+    def record(self, stream: int = 0) -> None:
+        _n.check(_n.lib.fg_event_record(self._e, ctypes.c_void_p(stream or None)))
+
+    def synchronize(self) -> None:
+        _n.check(_n.lib.fg_event_sync(self._e))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        _n.check(_n.lib.fg_event_elapsed_ms(self._e, end._e, ctypes.byref(ms)))
+        return ms.value
+
+    def __del__(self):  # pragma: no cover
+        try:
+            _n.lib.fg_event_destroy(self._e)
+        except Exception:
+            pass
+
+
+class Kernel:
+    def __init__(self, module: "Module", name: str):
+        k = ctypes.c_void_p()
+        _n.check(_n.lib.fg_kernel_get(module._m, name.encode(), ctypes.byref(k)))
+        self._k = k
+        self.module = module
+        self.name = name
+
+    def launch(self, grid, block, args, shared_bytes: int = 0, stream: int = 0) -> None:
+        """Backend::launch: ``args`` is a list of ctypes scalars (c_void_p for pointers)."""
+        g = (ctypes.c_uint32 * 3)(*(list(grid) + [1, 1, 1])[:3])
+        b = (ctypes.c_uint32 * 3)(*(list(block) + [1, 1, 1])[:3])
+        ptrs = (ctypes.c_void_p * len(args))(*[ctypes.cast(ctypes.pointer(a), ctypes.c_void_p) for a in args])
+        _n.check(_n.lib.fg_launch(self.module.device.handle, ctypes.c_void_p(stream or None), self._k, g, b,
+                                  shared_bytes, ptrs))
+
+
+class Module:
+    """A loaded code object (Backend::load_module)."""
+
+    def __init__(self, device: Device, image: bytes | None = None, backend_id: int = _n.FG_BACKEND_HIP):
+        self.device = device
+        m = ctypes.c_void_p()
+        if image is None:
+            _n.check(_n.lib.fg_device_fft_module(device.handle, ctypes.byref(m)))
+        else:
+            self._image = ctypes.create_string_buffer(bytes(image), len(image))
+            _n.check(_n.lib.fg_module_load(device.handle, backend_id, self._image, len(image), ctypes.byref(m)))
+        self._m = m
+
+    def kernel(self, name: str) -> Kernel:
+        return Kernel(self, name)
+
+    def __del__(self):  # pragma: no cover
+        try:
+            _n.lib.fg_module_unload(self._m)
+        except Exception:
+            pass

@@ -1,0 +1,175 @@
+/*
+ * ferrum_gpu.h -- C ABI of the MI355X-native ferrum-gpu FFT backend.
+ *
+ * Plain pointers and sizes only.  Every function returns an int status
+ * (FG_OK = 0, negative on failure) and leaves a thread-local message in
+ * fg_last_error().  Complex data is interleaved complex64 ([re, im] f32
+ * pairs), the layout of the reference's Complex32
+ * (crates/ferrum-gpu-fft/src/complex.rs:10-53) and of numpy complex64.
+ *
+ * Each declaration cites the reference interface it replaces (paths relative
+ * to the reference repository root).
+ */
+#ifndef FERRUM_GPU_H
+#define FERRUM_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define FG_API __attribute__((visibility("default")))
+#else
+#define FG_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+
+/* Error variants of crates/ferrum-gpu-cuda/src/error.rs:9-34 and
+ * crates/ferrum-gpu-core/src/error.rs:11-34, plus argument/memory errors the
+ * Python layer reports as ValueError (crates/ferrum-gpu-py/src/lib.rs:455-477). */
+#define FG_OK 0
+#define FG_ERR_INVALID_ARGUMENT (-1)
+#define FG_ERR_DRIVER (-2)           /* HIP runtime error (CudaBackendError::Driver) */
+#define FG_ERR_BACKEND_MISMATCH (-3) /* FerrumGpuError::BackendMismatch */
+#define FG_ERR_KERNEL_NOT_FOUND (-4) /* FerrumGpuError::KernelNotFound */
+#define FG_ERR_TARGET_MISMATCH (-5)  /* code object built for another gfx target */
+#define FG_ERR_OUT_OF_MEMORY (-6)
+#define FG_ERR_NO_DEVICE (-7)
+#define FG_ERR_INTERNAL (-8)
+
+/* BackendId (crates/ferrum-gpu-core/src/artifact.rs:13-36) with Hip added. */
+#define FG_BACKEND_CUDA 1
+#define FG_BACKEND_VULKAN 2
+#define FG_BACKEND_HIP 3
+
+/* Direction (crates/ferrum-gpu-core/src/dim.rs:52-64). */
+#define FG_FORWARD 1
+#define FG_INVERSE (-1)
+
+/* Thread-local text of the last failure on this thread ("" if none). */
+FG_API const char *fg_last_error(void);
+/* Crate version string, "0.3.0" (crates/ferrum-gpu-py/src/lib.rs:420-423). */
+FG_API const char *fg_version(void);
+/* Backend::id() (crates/ferrum-gpu-core/src/backend.rs:27): FG_BACKEND_HIP. */
+FG_API int fg_backend_id(void);
+
+/* ---------------------------------------------------------------- device */
+
+typedef struct fg_device *fg_device_t;
+typedef struct fg_module *fg_module_t;
+typedef struct fg_kernel *fg_kernel_t;
+typedef struct fg_event *fg_event_t;
+typedef void *fg_stream_t; /* a hipStream_t */
+
+/* Number of visible GPUs (0 on a machine without one). */
+FG_API int fg_device_count(int *count);
+/* Device::new(ordinal) (crates/ferrum-gpu/src/lib.rs:22-40,
+ * crates/ferrum-gpu-py/src/lib.rs:400-408): select the GPU, create its default
+ * stream and load the FFT code object into the device's module cache. */
+FG_API int fg_device_open(int ordinal, fg_device_t *out);
+/* Drop of Device: waits for the default stream, frees what the device owns. */
+FG_API int fg_device_close(fg_device_t dev);
+/* Device::sync (crates/ferrum-gpu/src/device.rs:36-38, py lib.rs:410-416). */
+FG_API int fg_device_sync(fg_device_t dev);
+/* Backend::default_stream (crates/ferrum-gpu-core/src/backend.rs:73). */
+FG_API int fg_device_default_stream(fg_device_t dev, fg_stream_t *out);
+/* Name ("gfx950"...), compute units and total memory of the device. */
+FG_API int fg_device_info(fg_device_t dev, char *arch, size_t arch_cap, int *cu_count,
+                   size_t *total_mem_bytes, int *clock_khz);
+
+/* --------------------------------------------------------------- buffers */
+
+/* Backend::alloc_zeros (backend.rs:30-33): synchronous, zero-filled. */
+FG_API int fg_alloc_zeros(fg_device_t dev, size_t bytes, void **dptr);
+/* Drop of CudaBuffer (crates/ferrum-gpu-cuda/src/buffer.rs:45-56): waits for
+ * the device's default stream, then frees. */
+FG_API int fg_free(fg_device_t dev, void *dptr);
+/* Backend::copy_h2d / copy_d2h (backend.rs:35-47): synchronous. */
+FG_API int fg_copy_h2d(fg_device_t dev, void *dst, const void *src, size_t bytes);
+FG_API int fg_copy_d2h(fg_device_t dev, void *dst, const void *src, size_t bytes);
+/* Stream-ordered variants (the async copies the north star adds). */
+FG_API int fg_copy_h2d_async(fg_device_t dev, void *dst, const void *src, size_t bytes,
+                      fg_stream_t stream);
+FG_API int fg_copy_d2h_async(fg_device_t dev, void *dst, const void *src, size_t bytes,
+                      fg_stream_t stream);
+FG_API int fg_copy_d2d_async(fg_device_t dev, void *dst, const void *src, size_t bytes,
+                      fg_stream_t stream);
+
+/* ------------------------------------------------------ modules, launch */
+
+/* Backend::load_module (backend.rs:50-53, crates/ferrum-gpu-cuda/src/backend_impl.rs:75-87):
+ * loads a gfx950 code object; backend_id must be FG_BACKEND_HIP, otherwise
+ * FG_ERR_BACKEND_MISMATCH. */
+FG_API int fg_module_load(fg_device_t dev, int backend_id, const void *image, size_t size,
+                   fg_module_t *out);
+FG_API int fg_module_unload(fg_module_t mod);
+/* The FFT module the device loaded at open (owned by the device). */
+FG_API int fg_device_fft_module(fg_device_t dev, fg_module_t *out);
+/* Backend::get_kernel (backend.rs:56-59): FG_ERR_KERNEL_NOT_FOUND if absent. */
+FG_API int fg_kernel_get(fg_module_t mod, const char *name, fg_kernel_t *out);
+/* Backend::launch (backend.rs:62-70): args[i] points at the i-th kernel
+ * argument's bytes (device pointers and scalars alike). stream NULL = default. */
+FG_API int fg_launch(fg_device_t dev, fg_stream_t stream, fg_kernel_t kernel, const uint32_t grid[3],
+              const uint32_t block[3], uint32_t shared_bytes, void **args);
+
+/* --------------------------------------------------------- streams/events */
+
+FG_API int fg_stream_create(fg_device_t dev, fg_stream_t *out); /* default priority */
+FG_API int fg_stream_destroy(fg_device_t dev, fg_stream_t stream);
+/* Backend::sync_stream (backend.rs:75-76). NULL = the device default stream. */
+FG_API int fg_stream_sync(fg_device_t dev, fg_stream_t stream);
+FG_API int fg_event_create(fg_device_t dev, fg_event_t *out);
+FG_API int fg_event_destroy(fg_event_t ev);
+FG_API int fg_event_record(fg_event_t ev, fg_stream_t stream);
+FG_API int fg_event_sync(fg_event_t ev);
+FG_API int fg_event_elapsed_ms(fg_event_t start, fg_event_t end, float *ms);
+
+/* -------------------------------------------------------------------- FFT */
+
+typedef struct fg_fft_plan *fg_fft_plan_t;
+
+/* Plan::new(log_n, batch, normalize) (crates/ferrum-gpu-fft/src/plan.rs:57-68)
+ * on a device: builds the twiddle tables in HBM once and picks the kernel(s).
+ * log_n in [2, 24] (the reference stops at 12, plan.rs:58).  batch >= 1. */
+FG_API int fg_fft_plan_1d(fg_device_t dev, uint32_t log_n, size_t batch, fg_fft_plan_t *out);
+/* Plan2D::new(log_n, normalize) (plan.rs:111-119) for `batch` square N x N
+ * row-major images; log_n in [4, 12] (py lib.rs:537-541). */
+FG_API int fg_fft_plan_2d(fg_device_t dev, uint32_t log_n, size_t batch, fg_fft_plan_t *out);
+FG_API int fg_fft_plan_destroy(fg_fft_plan_t plan);
+/* Device-resident execution, stream-ordered and asynchronous: the kernel
+ * launch of the host runner (py lib.rs:142-233, 325-358) with the inverse's
+ * conjugation and 1/N (1/(N*N) for 2D) scaling done inside the kernels.
+ * d_in and d_out each hold batch*N (2D: batch*N*N) complex64 and may be equal.
+ * direction: FG_FORWARD or FG_INVERSE.  stream NULL = device default stream. */
+FG_API int fg_fft_exec(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction, int normalize,
+                fg_stream_t stream);
+/* Number of kernel launches per execution and the name of the kernel that
+ * moves the most bytes (what the bench times and profiles). */
+FG_API int fg_fft_plan_describe(fg_fft_plan_t plan, int *launches, char *main_kernel, size_t cap,
+                         size_t *workspace_bytes);
+
+/* Host-memory convenience path behind ferrum_gpu.fft.fft_1d_c2c_pow2
+ * (crates/ferrum-gpu-py/src/lib.rs:445-504 -> run_fft_flat_with_device,
+ * lib.rs:86-250): validate, copy in, execute, copy out, synchronous.
+ * dev NULL uses a process-wide device 0 (the one-shot path, lib.rs:254-264).
+ * total_complex must be a positive multiple of 2^log_n; log_n in [2, 24]. */
+FG_API int fg_fft_1d_c2c_pow2_host(fg_device_t dev, const float *in, float *out, size_t total_complex,
+                            uint32_t log_n, int direction, int normalize);
+/* Behind ferrum_gpu.fft.fft_2d_c2c_pow2 (py lib.rs:527-588 -> run_fft_2d_flat,
+ * lib.rs:273-375): `batch` images of N x N; log_n in [4, 12]. */
+FG_API int fg_fft_2d_c2c_pow2_host(fg_device_t dev, const float *in, float *out, uint32_t log_n,
+                            size_t batch, int direction, int normalize);
+
+/* Streaming device copy of `bytes` (a multiple of 16) with the code object's
+ * copy kernel: the HBM yardstick reported beside the FFT. */
+FG_API int fg_stream_copy(fg_device_t dev, const void *d_in, void *d_out, size_t bytes,
+                   fg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FERRUM_GPU_H */

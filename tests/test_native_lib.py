@@ -1,0 +1,140 @@
+"""CPU-side checks of the C ABI library and the Python boundary (no GPU needed).
+
+The library must load, export every entry point include/ferrum_gpu.h
+declares, and reject bad arguments with the reference's messages before any
+device is touched (crates/ferrum-gpu-py/src/lib.rs:455-477, 537-558).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import ferrum_gpu
+from ferrum_gpu import _native as N
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ferrum_gpu.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^FG_API\s+[\w\s\*]+?\b(fg_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_boundary():
+    syms = declared_symbols()
+    for must in ("fg_fft_plan_1d", "fg_fft_plan_2d", "fg_fft_exec", "fg_fft_1d_c2c_pow2_host",
+                 "fg_fft_2d_c2c_pow2_host", "fg_module_load", "fg_kernel_get", "fg_launch",
+                 "fg_alloc_zeros", "fg_copy_h2d", "fg_copy_d2h", "fg_event_elapsed_ms"):
+        assert must in syms
+    assert len(syms) >= 37
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(N.LIB_PATH)
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_library_exports_nothing_undeclared():
+    out = os.popen(f"nm -D --defined-only {N.LIB_PATH}").read()
+    exported = sorted(set(re.findall(r" T (fg_\w+)", out)))
+    assert exported == declared_symbols()
+
+
+def test_version_and_backend():
+    assert ferrum_gpu.version() == "0.3.0"          # crates/ferrum-gpu-py/src/lib.rs:420-423
+    assert N.backend_id() == N.FG_BACKEND_HIP == 3  # BackendId with Hip added
+
+
+def test_code_object_is_embedded_for_gfx950():
+    # The .so carries the gfx950 code object (an ELF for amdgcn) in .rodata.
+    data = open(N.LIB_PATH, "rb").read()
+    assert data.count(b"\x7fELF") >= 2
+    assert b"gfx950" in data
+    for k in ("fg_fft_n10_fwd", "fg_fft_n12_inv", "fg_copy_f4", "fg_vector_add"):
+        assert k.encode() in data
+
+
+# --------------------------------------------------- argument validation
+
+
+def test_fft_1d_argument_errors():
+    f = ferrum_gpu.fft.fft_1d_c2c_pow2
+    x = np.zeros(1024, np.complex64)
+    with pytest.raises(ValueError, match=r"^log_n must be in \[2, 24\], got 1$"):
+        f(x, 1)
+    with pytest.raises(ValueError, match=r"^log_n must be in \[2, 24\], got 25$"):
+        f(x, 25)
+    with pytest.raises(ValueError, match=r"^arr len 1000 must be a positive multiple of N = 1024$"):
+        f(np.zeros(1000, np.complex64), 10)
+    with pytest.raises(ValueError, match=r"^arr len 0 must be a positive multiple of N = 4$"):
+        f(np.zeros(0, np.complex64), 2)
+    with pytest.raises(ValueError, match=r"^direction must be 'forward' or 'inverse', got \"sideways\"$"):
+        f(x, 10, direction="sideways")
+    with pytest.raises(TypeError):
+        f(np.zeros(1024, np.complex128), 10)        # PyReadonlyArray1<Complex32> dtype check
+    with pytest.raises(TypeError):
+        f(np.zeros((2, 512), np.complex64), 9)      # rank check
+    with pytest.raises(TypeError):
+        f(np.zeros(2048, np.complex64)[::2], 10)    # as_slice() needs contiguity
+    with pytest.raises(OverflowError):
+        f(x, -1)                                    # u32 extraction
+    with pytest.raises(TypeError):
+        f(x, 10, device="gpu0")
+
+
+def test_fft_2d_argument_errors():
+    f = ferrum_gpu.fft.fft_2d_c2c_pow2
+    with pytest.raises(ValueError, match=r"^2D requires log_n in \[4, 12\]; got 3$"):
+        f(np.zeros((8, 8), np.complex64), 3)
+    with pytest.raises(ValueError, match=r"^2D requires log_n in \[4, 12\]; got 13$"):
+        f(np.zeros((16, 16), np.complex64), 13)
+    with pytest.raises(ValueError, match=r"^arr shape \[16, 8\] != \(16, 16\)$"):
+        f(np.zeros((16, 8), np.complex64), 4)
+    with pytest.raises(ValueError, match=r"^direction must be 'forward' or 'inverse'"):
+        f(np.zeros((16, 16), np.complex64), 4, direction="back")
+
+
+def test_c_abi_validation_without_device():
+    # The host entry points validate before they need a device.
+    x = np.zeros(64, np.complex64)
+    y = np.empty_like(x)
+    rc = N.lib.fg_fft_1d_c2c_pow2_host(None, x.ctypes.data, y.ctypes.data, 64, 30, 1, 0)
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "log_n must be in [2, 24], got 30" in N.last_error()
+    rc = N.lib.fg_fft_1d_c2c_pow2_host(None, x.ctypes.data, y.ctypes.data, 60, 4, 1, 0)
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "arr len 60 must be a positive multiple of N = 16" in N.last_error()
+    rc = N.lib.fg_fft_1d_c2c_pow2_host(None, x.ctypes.data, y.ctypes.data, 64, 4, 2, 0)
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "direction" in N.last_error()
+    rc = N.lib.fg_fft_2d_c2c_pow2_host(None, x.ctypes.data, y.ctypes.data, 2, 1, 1, 0)
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "2D requires log_n in [4, 12]; got 2" in N.last_error()
+    rc = N.lib.fg_fft_exec(None, None, None, 1, 0, None)
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "plan is null" in N.last_error()
+    rc = N.lib.fg_fft_plan_1d(None, 10, 1, ctypes.byref(ctypes.c_void_p()))
+    assert rc == N.FG_ERR_INVALID_ARGUMENT
+
+
+def test_last_error_is_thread_local():
+    import threading
+
+    N.lib.fg_fft_exec(None, None, None, 1, 0, None)
+    assert N.last_error()
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(N.last_error()))
+    t.start()
+    t.join()
+    assert seen == [""]
+
+
+def test_no_device_reports_cleanly():
+    if ferrum_gpu.hip.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    with pytest.raises(ValueError, match=r"^Device::new\(0\): "):
+        ferrum_gpu.hip.Device(0)
+    with pytest.raises(ValueError, match=r"^ferrum-gpu fft error: "):
+        ferrum_gpu.fft.fft_1d_c2c_pow2(np.zeros(16, np.complex64), 4)

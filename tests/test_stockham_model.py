@@ -1,0 +1,118 @@
+"""CPU model of the LDS-resident Stockham kernel's data movement
+(ferrum-gpu_amd/csrc/kernels/fft_stockham.hpp), checked against the oracle.
+
+The model keeps the kernel's register bookkeeping exactly -- thread t holds
+positions t + T*m, butterfly i of stage s reads x[i + NB*p], scatters output q
+to j*L*R + k + q*L, the next stage gathers t + T*m -- and its twiddle table is
+built the way fft_plan.cpp builds it.  Only the in-register DFT-R is replaced
+by numpy's, so this pins the indexing (the part a GPU fault would come from)
+on the CPU before any launch.  It also checks every LDS index stays inside the
+padded allocation the kernel declares.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_l2, uniform_c64
+
+# kStockham in fft_plan.cpp / FG_STOCKHAM in fft_kernels.hip: (log_e, fpb)
+GEOM = {2: (2, 64), 3: (3, 64), 4: (4, 64), 5: (4, 32), 6: (4, 16), 7: (4, 8), 8: (4, 4),
+        9: (4, 2), 10: (4, 1), 11: (4, 1), 12: (4, 1)}
+
+
+def stockham_table(log_n, log_e):
+    nfull, rem = divmod(log_n, log_e)
+    nst = nfull + (1 if rem else 0)
+    out, offs = [], [0, 0]
+    for s in range(1, nst):
+        logl, logr = s * log_e, (log_e if s < nfull else rem)
+        L, R = 1 << logl, 1 << logr
+        k, p = np.meshgrid(np.arange(L), np.arange(R), indexing="ij")
+        e = (p * k) % (L * R)
+        out.append(np.exp(-2j * np.pi * e / (L * R)).astype(np.complex64).reshape(-1))
+        offs.append(offs[-1] + L * R)
+    return (np.concatenate(out) if out else np.ones(1, np.complex64)), offs
+
+
+def lds_pos(p):
+    return p + (p >> 4)
+
+
+def model(x, log_n, log_e):
+    n, e = 1 << log_n, 1 << log_e
+    t_per = n // e
+    nfull, rem = divmod(log_n, log_e)
+    logrs = [log_e] * nfull + ([rem] if rem else [])
+    tw, offs = stockham_table(log_n, log_e)
+    lanes = x.reshape(-1, n)
+    t = np.arange(t_per)
+    regs = lanes[:, t[:, None] + t_per * np.arange(e)[None, :]]   # regs[b, t, m] = x[t + T m]
+    lds_elems = n + n // 16
+    for s, logr in enumerate(logrs):
+        r = 1 << logr
+        nb = e // r
+        L = 1 << (s * log_e)
+        new = np.empty_like(regs)
+        dst_pos = np.empty((t_per, e), dtype=np.int64)
+        for i in range(nb):
+            u = regs[:, :, [i + nb * p for p in range(r)]].astype(np.complex128)   # (B, T, R)
+            b = t + t_per * i
+            k = b & (L - 1)
+            if L > 1:
+                w = tw[offs[s] + k[:, None] * r + np.arange(r)[None, :]]
+                u = u * w[None, :, :]
+            y = np.fft.fft(u, axis=2)
+            j = b >> (s * log_e)
+            for q in range(r):
+                new[:, :, i + nb * q] = y[:, :, q]
+                dst_pos[:, i + nb * q] = j * L * r + k + q * L
+        # every thread writes a distinct position and all N positions are covered
+        assert np.array_equal(np.sort(dst_pos.reshape(-1)), np.arange(n))
+        if s + 1 < len(logrs):
+            lds = np.zeros((lanes.shape[0], lds_elems), np.complex128)
+            assert lds_pos(dst_pos).max() < lds_elems
+            lds[:, lds_pos(dst_pos)] = new
+            gather = lds_pos(t[:, None] + t_per * np.arange(e)[None, :])
+            assert gather.max() < lds_elems
+            regs = lds[:, gather]
+        else:
+            # the last stage's scatter is exactly the coalesced t + T*m store
+            assert np.array_equal(dst_pos, t[:, None] + t_per * np.arange(e)[None, :])
+            regs = new
+    out = np.empty((lanes.shape[0], n), np.complex128)
+    out[:, t[:, None] + t_per * np.arange(e)[None, :]] = regs
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("log_n", list(range(2, 13)))
+def test_model_matches_oracle(log_n):
+    rng = np.random.default_rng(log_n)
+    x = uniform_c64(rng, 3 << log_n)
+    log_e, _ = GEOM[log_n]
+    assert rel_l2(model(x, log_n, log_e), oracle.fft_1d(x, log_n)) < 1e-5
+
+
+@pytest.mark.parametrize("log_n,log_e", [(10, 3), (12, 3), (11, 2), (9, 5), (12, 6)])
+def test_model_other_radices(log_n, log_e):
+    rng = np.random.default_rng(log_n * 7 + log_e)
+    x = uniform_c64(rng, 2 << log_n)
+    assert rel_l2(model(x, log_n, log_e), oracle.fft_1d(x, log_n)) < 1e-5
+
+
+def test_twiddle_rows_are_16_byte_aligned():
+    # The kernel loads table rows as float4 pairs: every row start k*R + offset
+    # must be even (8-byte entries -> 16-byte aligned).
+    for log_n, (log_e, _) in GEOM.items():
+        _, offs = stockham_table(log_n, log_e)
+        assert all(o % 2 == 0 for o in offs), log_n
+
+
+def test_geometry_fits_hardware():
+    for log_n, (log_e, fpb) in GEOM.items():
+        threads = ((1 << log_n) >> log_e) * fpb
+        assert 1 <= threads <= 1024
+        lds = fpb * ((1 << log_n) + (1 << log_n) // 16) * 8
+        assert lds <= 64 * 1024, (log_n, lds)
