@@ -129,8 +129,10 @@ def cpu_baseline(np, x, log_n, gpu_out, budget_s: float):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    # The GPU reaches steady clocks after ~100 back-to-back launches of this
+    # kernel (~20 ms); fewer warmup steps time the ramp, not the kernel.
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of single-thread CPU timing")

@@ -496,10 +496,9 @@ int fg_stream_copy(fg_device_t dev, const void* d_in, void* d_out, size_t bytes,
             k_mod = dev->fft_module.get();
         }
         uint64_t n4 = bytes / 16;
-        const uint32_t block = 256;
+        const uint32_t block = 64;
         uint64_t blocks = (n4 + block - 1) / block;
-        const uint64_t cap = (uint64_t)dev->dev->handle()->cu_count * 64;  // grid-stride beyond this
-        if (blocks > cap) blocks = cap;
+        if (blocks > 0x7fffffffull) blocks = 0x7fffffffull;  // the kernel strides beyond this
         if (blocks == 0) return;
         const void* src = d_in;
         void* dst = d_out;

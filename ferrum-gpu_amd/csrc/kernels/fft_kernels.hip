@@ -39,15 +39,19 @@ FG_STOCKHAM(12, 4, 1)    // N=4096: 256 threads
 
 // ---------------------------------------------------------------- utilities
 
-// Streaming copy, 16 bytes per lane: the bandwidth yardstick the bench
-// reports beside the FFT, and the known-size kernel used to scale rocprof's
-// FETCH_SIZE / WRITE_SIZE counters.
-extern "C" __global__ __launch_bounds__(256) void fg_copy_f4(const float4* __restrict__ in,
-                                                             float4* __restrict__ out,
-                                                             uint64_t n4) {
-    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (; i < n4; i += stride) out[i] = in[i];
+// Streaming copy, 16 bytes per lane with nontemporal hints, one element per
+// thread in 64-thread workgroups (the fastest plain-copy shape measured on
+// gfx950): the HBM yardstick the bench reports beside the FFT, and the
+// known-size kernel used to scale rocprof's FETCH_SIZE / WRITE_SIZE counters.
+extern "C" __global__ __launch_bounds__(64) void fg_copy_f4(const float4* __restrict__ in,
+                                                            float4* __restrict__ out,
+                                                            uint64_t n4) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    const v4f* src = reinterpret_cast<const v4f*>(in);
+    v4f* dst = reinterpret_cast<v4f*>(out);
+    uint64_t i = (uint64_t)blockIdx.x * 64 + threadIdx.x;
+    const uint64_t stride = (uint64_t)gridDim.x * 64;
+    for (; i < n4; i += stride) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
 // c = a + b over n floats: the substrate smoke kernel (the reference's

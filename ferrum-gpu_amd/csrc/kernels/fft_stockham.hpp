@@ -149,7 +149,7 @@ __device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
     float2 x[Sh::E];
     if (valid) {
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = src[t + Sh::T * m];
+        for (int m = 0; m < Sh::E; ++m) x[m] = load_stream(src + t + Sh::T * m);
     } else {
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) x[m] = make_float2(0.f, 0.f);
@@ -164,7 +164,7 @@ __device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
         for (int m = 0; m < Sh::E; ++m) {
             float2 v = x[m];
             if constexpr (INV) v = cscale(cconj(v), scale);
-            dst[t + Sh::T * m] = v;
+            store_stream(dst + t + Sh::T * m, v);
         }
     }
 }
