@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <fstream>
 #include <iterator>
 
@@ -72,53 +73,253 @@ std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e) {
     return t;
 }
 
+std::vector<Cf32> big_twiddles() {
+    std::vector<Cf32> t(8192);
+    for (int j = 0; j < 4096; ++j) {
+        const double a = 2.0 * M_PI * (double)j / 4096.0;
+        const double b = 2.0 * M_PI * (double)j / 16777216.0;
+        t[j] = Cf32{(float)cos(a), (float)-sin(a)};
+        t[4096 + j] = Cf32{(float)cos(b), (float)-sin(b)};
+    }
+    return t;
+}
+
+std::vector<uint32_t> split_1d(uint32_t log_n) {
+    // Two passes while each digit's tile still spans >= 16 columns
+    // (L * G <= 16384 complex of LDS), three passes beyond 2^20.
+    if (log_n <= 20) {
+        const uint32_t a = log_n / 2;
+        return {log_n - a, a};
+    }
+    const uint32_t base = log_n / 3, rest = log_n - 3 * base;
+    return {base + (rest > 0 ? 1u : 0u), base + (rest > 1 ? 1u : 0u), base};
+}
+
+uint32_t tile_columns(uint32_t log_l) {
+    const uint32_t g = 16384u >> log_l;
+    return g > 64 ? 64 : g;
+}
+
+namespace {
+
+uint32_t elems_per_thread_log(uint32_t log_l) { return log_l < 4 ? log_l : 4; }
+
+std::string tile_name(uint32_t log_l, uint32_t g, bool rowwise) {
+    return "fg_tile_l" + std::to_string(log_l) + "_g" + std::to_string(g) + (rowwise ? "_r" : "_c");
+}
+
+}  // namespace
+
+const void* FftPlan::stage_table(uint32_t log_l) {
+    for (auto& e : stage_tables_)
+        if (e.first == log_l) return e.second.data();
+    auto tw = stockham_twiddles(log_l, elems_per_thread_log(log_l));
+    Buffer<Cf32, HipBackend> b = dev_->alloc<Cf32>(tw.size());
+    b.copy_from_host(tw.data(), tw.size());
+    stage_tables_.emplace_back(log_l, std::move(b));
+    return stage_tables_.back().second.data();
+}
+
+const void* FftPlan::big_table() {
+    if (!big_.data()) {
+        auto t = big_twiddles();
+        big_ = dev_->alloc<Cf32>(t.size());
+        big_.copy_from_host(t.data(), t.size());
+    }
+    return big_.data();
+}
+
+void FftPlan::add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t count, Buf src, Buf dst) {
+    const StockhamGeom g = kStockham[log_l];
+    Step s;
+    s.name = "fg_fft_n" + std::to_string(log_l);
+    s.fn = HipBackend::get_kernel(mod, s.name.c_str());
+    const uint64_t blocks = (count + g.fpb - 1) / g.fpb;
+    if (blocks > 0x7fffffffull) invalid("batch too large for one launch");
+    s.grid = Dim3((uint32_t)blocks);
+    s.block = Dim3(((1u << log_l) >> g.log_e) * g.fpb);
+    s.src = src;
+    s.dst = dst;
+    s.tw = stage_table(log_l);
+    s.count = count;
+    steps_.push_back(s);
+}
+
+void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g, bool rowwise,
+                       const TileGeom& geom, uint64_t tiles, Buf src, Buf dst) {
+    // The kernel reads columns at stride 1 (column-wise) or elements at stride
+    // 1 (row-wise) and always writes columns at stride 1.
+    if ((rowwise ? geom.ies : geom.ics) != 1 || geom.ocs != 1) fail(FG_ERR_INTERNAL, "tile geometry not unit-stride");
+    if (tiles == 0 || tiles > 0x7fffffffull) invalid("too many tiles for one launch");
+    Step s;
+    s.tile = true;
+    s.name = tile_name(log_l, g, rowwise);
+    s.fn = HipBackend::get_kernel(mod, s.name.c_str());
+    s.grid = Dim3((uint32_t)tiles);
+    s.block = Dim3(g * ((1u << log_l) >> elems_per_thread_log(log_l)));
+    s.src = src;
+    s.dst = dst;
+    s.tw = stage_table(log_l);
+    s.geom = geom;
+    steps_.push_back(s);
+}
+
 std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_n,
                                           size_t batch) {
     if (log_n < kMinLogN1D || log_n > kMaxLogN1D)
         invalid("log_n must be in [" + std::to_string(kMinLogN1D) + ", " + std::to_string(kMaxLogN1D) +
                 "], got " + std::to_string(log_n));
     if (batch == 0) invalid("batch must be positive");
-    if (log_n > kMaxLogNSingle)
-        fail(FG_ERR_INVALID_ARGUMENT, "log_n " + std::to_string(log_n) + " needs the two-pass path, not built");
-    std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::Stockham1D, log_n, batch));
-    const StockhamGeom g = kStockham[log_n];
-    const uint32_t threads = (1u << log_n) >> g.log_e;
-    auto tw = stockham_twiddles(log_n, g.log_e);
-    p->tables_.push_back(dev.alloc<Cf32>(tw.size()));
-    p->tables_.back().copy_from_host(tw.data(), tw.size());
+    if (log_n <= kMaxLogNSingle) {
+        std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::Stockham1D, log_n, batch));
+        p->add_stockham(mod, log_n, batch, Buf::In, Buf::Out);
+        p->main_kernel_ = p->steps_[0].name;
+        return p;
+    }
 
-    Step s;
-    const std::string base = "fg_fft_n" + std::to_string(log_n);
-    s.fwd = HipBackend::get_kernel(mod, (base + "_fwd").c_str());
-    s.inv = HipBackend::get_kernel(mod, (base + "_inv").c_str());
-    const uint64_t blocks = (batch + g.fpb - 1) / g.fpb;
-    if (blocks > 0x7fffffffull) invalid("batch too large for one launch");
-    s.grid = Dim3((uint32_t)blocks);
-    s.block = Dim3(threads * g.fpb);
-    s.src = Buf::In;
-    s.dst = Buf::Out;
-    s.tw = p->tables_.back().data();
-    s.count = batch;
-    s.scales = true;
-    s.conj_in = true;
-    p->steps_.push_back(s);
-    p->main_kernel_ = base + "_fwd";
+    // N = N_1 * ... * N_P, digit 1 slowest; S_i = stride of digit i.
+    std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::MultiPass1D, log_n, batch));
+    const std::vector<uint32_t> logs = split_1d(log_n);
+    const size_t P = logs.size();
+    const uint64_t N = 1ull << log_n;
+    std::vector<uint64_t> S(P + 1);
+    S[0] = N;
+    for (size_t i = 1; i <= P; ++i) S[i] = S[i - 1] >> logs[i - 1];
+    if (N * batch > (1ull << 40)) invalid("transform too large");
+    p->work_ = dev.alloc<Cf32>(N * batch);
+    const void* big = p->big_table();
+    (void)big;
+    // Passes 1..P-1: DFT over digit i for every value of the faster digits
+    // (columns, contiguous) and of the slower, already transformed digits;
+    // four-step twiddle W_{S_{i-1}}^{r_i k_i}; in place in the workspace.
+    for (size_t i = 1; i < P; ++i) {
+        const uint32_t log_l = logs[i - 1];
+        const uint32_t g = tile_columns(log_l);
+        if (S[i] < g) fail(FG_ERR_INTERNAL, "digit split leaves fewer columns than a tile");
+        TileGeom t{};
+        t.t0n = (uint32_t)(S[i] / g);
+        t.t1n = (uint32_t)(N / S[i - 1]);
+        t.is0 = t.os0 = g;
+        t.is1 = t.os1 = S[i - 1];
+        t.is2 = t.os2 = N;
+        t.ics = t.ocs = 1;
+        t.ies = t.oes = S[i];
+        t.twc = 1;
+        t.tw0 = g;
+        t.tw1 = 0;
+        t.log_m = (uint32_t)__builtin_ctzll(S[i - 1]);
+        p->add_tile(mod, log_l, g, false, t, (uint64_t)t.t0n * t.t1n * batch, i == 1 ? Buf::In : Buf::Work,
+                    Buf::Work);
+    }
+    // Pass P: contiguous rows of N_P for each (k_1, k_2..k_{P-1}); G' rows of
+    // consecutive k_1 per tile, stored to the digit-reversed output position
+    // k_1 + N_1 k_2 + N_1 N_2 k_P (P <= 3).
+    {
+        const uint32_t log_l = logs[P - 1];
+        const uint64_t L = 1ull << log_l, n1 = 1ull << logs[0];
+        const uint32_t g = tile_columns(log_l);
+        if (n1 < g) fail(FG_ERR_INTERNAL, "digit split leaves fewer rows than a tile");
+        TileGeom t{};
+        t.t0n = (uint32_t)(n1 / g);
+        t.t1n = (uint32_t)(N / (n1 * L));
+        t.is0 = g * S[1];
+        t.is1 = L;
+        t.is2 = N;
+        t.ics = S[1];
+        t.ies = 1;
+        t.os0 = g;
+        t.os1 = n1;
+        t.os2 = N;
+        t.ocs = 1;
+        t.oes = N / L;
+        p->add_tile(mod, log_l, g, true, t, (uint64_t)t.t0n * t.t1n * batch, Buf::Work, Buf::Out);
+    }
+    p->main_kernel_ = p->steps_[0].name;
     return p;
 }
 
-std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice&, const HipBackend::Module&, uint32_t log_n, size_t batch) {
+std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_n,
+                                          size_t batch) {
     if (log_n < kMinLogN2D || log_n > kMaxLogN2D)
         invalid("2D requires log_n in [" + std::to_string(kMinLogN2D) + ", " + std::to_string(kMaxLogN2D) +
                 "]; got " + std::to_string(log_n));
     if (batch == 0) invalid("batch must be positive");
-    fail(FG_ERR_INVALID_ARGUMENT, "2D path not built");
+    std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::TwoD, log_n, batch));
+    const uint64_t N = 1ull << log_n, NN = N * N;
+    const bool split = tile_columns(log_n) < 16;  // 4096-point columns would leave < 16 per tile
+    if (split) p->work_ = dev.alloc<Cf32>(NN * batch);
+    // Row pass (the reference's K1 row FFT, py lib.rs:325-336): N*batch rows.
+    p->add_stockham(mod, log_n, N * batch, Buf::In, split ? Buf::Work : Buf::Out);
+    if (!split) {
+        // Column pass, in place: G adjacent columns of length N per tile.
+        const uint32_t g = (uint32_t)std::min<uint64_t>(tile_columns(log_n), N);
+        TileGeom t{};
+        t.t0n = (uint32_t)(N / g);
+        t.t1n = 1;
+        t.is0 = t.os0 = g;
+        t.is1 = t.os1 = 0;
+        t.is2 = t.os2 = NN;
+        t.ics = t.ocs = 1;
+        t.ies = t.oes = N;
+        p->add_tile(mod, log_n, g, false, t, (uint64_t)t.t0n * batch, Buf::Out, Buf::Out);
+    } else {
+        // Column FFT of length N = C_1 * C_2 over the slow axis, as two
+        // column passes with 64 adjacent columns per tile.
+        const uint32_t l1 = log_n - log_n / 2, l2 = log_n / 2;
+        const uint64_t C1 = 1ull << l1, C2 = 1ull << l2;
+        const uint32_t g = 64;
+        TileGeom a{};
+        a.t0n = (uint32_t)(N / g);
+        a.t1n = (uint32_t)C2;
+        a.is0 = a.os0 = g;
+        a.is1 = a.os1 = N;
+        a.is2 = a.os2 = NN;
+        a.ics = a.ocs = 1;
+        a.ies = a.oes = C2 * N;
+        a.twc = 0;
+        a.tw0 = 0;
+        a.tw1 = 1;
+        a.log_m = log_n;
+        p->big_table();
+        p->add_tile(mod, l1, g, false, a, (uint64_t)a.t0n * a.t1n * batch, Buf::Work, Buf::Work);
+        TileGeom b{};
+        b.t0n = (uint32_t)(N / g);
+        b.t1n = (uint32_t)C1;
+        b.is0 = g;
+        b.is1 = C2 * N;
+        b.is2 = NN;
+        b.ics = 1;
+        b.ies = N;
+        b.os0 = g;
+        b.os1 = N;
+        b.os2 = NN;
+        b.ocs = 1;
+        b.oes = C1 * N;
+        p->add_tile(mod, l2, g, false, b, (uint64_t)b.t0n * b.t1n * batch, Buf::Work, Buf::Out);
+    }
+    p->main_kernel_ = p->steps_.back().name;
+    return p;
+}
+
+std::vector<std::string> FftPlan::kernel_names() const {
+    std::vector<std::string> v;
+    for (const Step& s : steps_) v.push_back(s.name);
+    return v;
 }
 
 void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream) const {
     if (!in || !out) invalid("fft exec: null buffer");
     const bool inverse = dir == Direction::Inverse;
-    const float scale = (inverse && normalize) ? 1.0f / (float)elems() : 1.0f;
-    for (const Step& s : steps_) {
+    const float scale = (inverse && normalize)
+                            ? (kind_ == Kind::TwoD ? 1.0f / ((float)(1u << log_n_) * (float)(1u << log_n_))
+                                                   : 1.0f / (float)(1ull << log_n_))
+                            : 1.0f;
+    const void* big = big_.data();
+    for (size_t i = 0; i < steps_.size(); ++i) {
+        const Step& s = steps_[i];
+        uint32_t flags = 0;
+        if (inverse && i == 0) flags |= FG_PASS_CONJ_IN;
+        if (inverse && i + 1 == steps_.size()) flags |= FG_PASS_CONJ_SCALE_OUT;
         auto bind = [&](Buf b) -> void* {
             switch (b) {
                 case Buf::In: return const_cast<void*>(in);
@@ -129,11 +330,18 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
         void* src = bind(s.src);
         void* dst = bind(s.dst);
         const void* tw = s.tw;
-        uint64_t count = s.count;
-        float sc = s.scales ? scale : 1.0f;
-        HipBackend::KernelHandle k = inverse ? s.inv : s.fwd;
-        void* args[] = {&src, &dst, (void*)&tw, &count, &sc};
-        HipBackend::launch(dev_->handle(), stream, k, s.grid, s.block, 0, args);
+        if (!s.tile) {
+            uint64_t count = s.count;
+            float sc = scale;
+            void* args[] = {&src, &dst, (void*)&tw, &count, &sc, &flags};
+            HipBackend::launch(dev_->handle(), stream, s.fn, s.grid, s.block, 0, args);
+        } else {
+            TileGeom g = s.geom;
+            g.flags = flags;
+            g.scale = scale;
+            void* args[] = {&src, &dst, (void*)&tw, (void*)&big, &g};
+            HipBackend::launch(dev_->handle(), stream, s.fn, s.grid, s.block, 0, args);
+        }
     }
 }
 

@@ -14,6 +14,7 @@
 
 #include "device.hpp"
 #include "hip_backend.hpp"
+#include "kernels/tile_geom.h"
 
 namespace fg {
 
@@ -32,13 +33,13 @@ KernelArtifact fft_code_object();
 
 // Supported shapes (the reference: 1D [2, 12], plan.rs:58; 2D [4, 12],
 // crates/ferrum-gpu-py/src/lib.rs:537).  1D is widened to 2^24 by the
-// two-pass decomposition.
+// multi-pass decomposition.
 constexpr uint32_t kMinLogN1D = 2, kMaxLogN1D = 24, kMaxLogNSingle = 12;
 constexpr uint32_t kMinLogN2D = 4, kMaxLogN2D = 12;
 
 class FftPlan {
 public:
-    enum class Kind { Stockham1D, FourStep1D, TwoD };
+    enum class Kind { Stockham1D, MultiPass1D, TwoD };
 
     static std::unique_ptr<FftPlan> make_1d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_n,
                                             size_t batch);
@@ -56,40 +57,56 @@ public:
     int launches() const { return (int)steps_.size(); }
     const std::string& main_kernel() const { return main_kernel_; }
     size_t workspace_bytes() const { return work_.bytes(); }
+    // Kernel names in launch order.
+    std::vector<std::string> kernel_names() const;
 
 private:
-    // One kernel launch.  Buffers are named symbolically and bound at exec:
-    // the caller's input, the caller's output, or the plan's workspace.
+    // Buffers are named symbolically and bound at exec: the caller's input,
+    // the caller's output, or the plan's workspace.
     enum class Buf { In, Out, Work };
     struct Step {
-        HipBackend::KernelHandle fwd = nullptr;  // kernel used for the forward direction
-        HipBackend::KernelHandle inv = nullptr;  // kernel used for the inverse direction
+        bool tile = false;                      // tile pass (else single-pass Stockham)
+        std::string name;
+        HipBackend::KernelHandle fn = nullptr;
         Dim3 grid, block;
         Buf src = Buf::In, dst = Buf::Out;
-        const void* tw = nullptr;  // twiddle table in HBM
-        uint64_t count = 0;        // transforms (or tiles) the launch covers
-        uint64_t p0 = 0, p1 = 0;   // kernel-specific scalars
-        bool scales = false;       // applies the inverse's conjugate+scale on store
-        bool conj_in = false;      // applies the inverse's input conjugation on load
+        const void* tw = nullptr;               // Stockham stage table
+        uint64_t count = 0;                     // Stockham: transforms in the launch
+        TileGeom geom{};                        // tile: addressing (flags/scale set at exec)
     };
 
     FftPlan(HipDevice& dev, Kind kind, uint32_t log_n, size_t batch)
         : dev_(&dev), kind_(kind), log_n_(log_n), batch_(batch) {}
+
+    // Stage table for a length-2^log_l Stockham transform (uploaded once per plan).
+    const void* stage_table(uint32_t log_l);
+    const void* big_table();
+    void add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t count, Buf src, Buf dst);
+    void add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g, bool rowwise, const TileGeom& geom,
+                  uint64_t tiles, Buf src, Buf dst);
 
     HipDevice* dev_;
     Kind kind_;
     uint32_t log_n_;
     size_t batch_;
     std::vector<Step> steps_;
-    std::vector<Buffer<Cf32, HipBackend>> tables_;
+    std::vector<std::pair<uint32_t, Buffer<Cf32, HipBackend>>> stage_tables_;
+    Buffer<Cf32, HipBackend> big_;
     Buffer<Cf32, HipBackend> work_;
     std::string main_kernel_;
 };
 
-// Host twiddle tables (exposed for the CPU-side tests of the plan logic).
+// ---- host-side pieces exposed for the CPU tests of the plan logic ----------
+
 // Mixed-radix Stockham table for N = 2^log_n with 2^log_e elements per thread:
 // per stage s >= 1 (L = 2^(s*log_e), R = that stage's radix) the block
 // [k][p] = W_{L*R}^{p*k}, k < L, p < R, computed in fp64 and rounded to f32.
 std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e);
+// Two-level root table: [j] = W_4096^j, [4096 + j] = W_{2^24}^j, j < 4096.
+std::vector<Cf32> big_twiddles();
+// Digit split (log2 sizes, slowest digit first) of a 1D length 2^log_n > 4096.
+std::vector<uint32_t> split_1d(uint32_t log_n);
+// Columns per tile for a column-wise pass of length 2^log_l.
+uint32_t tile_columns(uint32_t log_l);
 
 }  // namespace fg

@@ -15,14 +15,10 @@ using namespace fg;
 // workgroup of FPB * (N / E) threads.
 #define FG_STOCKHAM(LOGN, LOGE, FPB)                                                        \
     extern "C" __global__ __launch_bounds__(FPB * ((1 << LOGN) >> LOGE)) void                \
-        fg_fft_n##LOGN##_fwd(const float2* __restrict__ in, float2* __restrict__ out,        \
-                             const float2* __restrict__ tw, uint64_t batch, float scale) {  \
-        fft_stockham_body<LOGN, LOGE, FPB, false>(in, out, tw, batch, scale);               \
-    }                                                                                        \
-    extern "C" __global__ __launch_bounds__(FPB * ((1 << LOGN) >> LOGE)) void                \
-        fg_fft_n##LOGN##_inv(const float2* __restrict__ in, float2* __restrict__ out,        \
-                             const float2* __restrict__ tw, uint64_t batch, float scale) {  \
-        fft_stockham_body<LOGN, LOGE, FPB, true>(in, out, tw, batch, scale);                \
+        fg_fft_n##LOGN(const float2* __restrict__ in, float2* __restrict__ out,              \
+                       const float2* __restrict__ tw, uint64_t batch, float scale,          \
+                       uint32_t flags) {                                                    \
+        fft_stockham_body<LOGN, LOGE, FPB>(in, out, tw, batch, scale, flags);               \
     }
 
 FG_STOCKHAM(2, 2, 64)    // N=4:    1 thread  / transform, 64 per wave
@@ -63,3 +59,33 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) c[i] = a[i] + b[i];
 }
+
+// ------------------------------------------------------- multi-pass tiles
+//
+// fg_tile_l<LOGL>_g<G>_<c|r>: one pass over G columns of length 2^LOGL per
+// workgroup (G * 2^LOGL / 16 threads).  'c': columns contiguous in memory
+// (column passes); 'r': rows contiguous (the last 1D pass, which transposes
+// through LDS).  Mirrored on the host by kTileTable in fft_plan.cpp.
+#include "fft_tile.hpp"
+
+#define FG_TILE(LOGL, G, RW, TAG)                                                                    \
+    extern "C" __global__ __launch_bounds__(G * ((1 << LOGL) >> (LOGL < 4 ? LOGL : 4))) void        \
+        fg_tile_l##LOGL##_g##G##_##TAG(const float2* __restrict__ in, float2* __restrict__ out,     \
+                                       const float2* __restrict__ tw, const float2* __restrict__ big, \
+                                       TileGeom g) {                                                  \
+        fft_tile_body<LOGL, (LOGL < 4 ? LOGL : 4), G, RW>(in, out, tw, big, g);                      \
+    }
+
+FG_TILE(4, 16, false, c)
+FG_TILE(5, 32, false, c)
+FG_TILE(5, 64, false, c)
+FG_TILE(6, 64, false, c)
+FG_TILE(7, 64, false, c)
+FG_TILE(8, 64, false, c)
+FG_TILE(9, 32, false, c)
+FG_TILE(10, 16, false, c)
+FG_TILE(6, 64, true, r)
+FG_TILE(7, 64, true, r)
+FG_TILE(8, 64, true, r)
+FG_TILE(9, 32, true, r)
+FG_TILE(10, 16, true, r)

@@ -16,9 +16,11 @@
 // Intermediate stages exchange through LDS with one pad slot per 16 entries,
 // which breaks the stride-E pattern of the first scatter across LDS banks.
 //
-// Inverse: conjugate on load, conjugate (and scale) on store.
+// Inverse: conjugate on load, conjugate (and scale) on store (runtime flags,
+// so a multi-pass plan can apply each half in a different pass).
 #pragma once
 #include "fft_common.hpp"
+#include "tile_geom.h"
 
 namespace fg {
 
@@ -129,12 +131,13 @@ struct StockhamStages {
     }
 };
 
-// Kernel body: FPB transforms per workgroup of FPB*T threads.
-template <int LOGN, int LOGE, int FPB, bool INV>
+// Kernel body: FPB transforms per workgroup of FPB*T threads.  flags take
+// FG_PASS_CONJ_IN / FG_PASS_CONJ_SCALE_OUT (tile_geom.h): the inverse is both.
+template <int LOGN, int LOGE, int FPB>
 __device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
                                                   float2* __restrict__ out,
                                                   const float2* __restrict__ tw,
-                                                  uint64_t batch, float scale) {
+                                                  uint64_t batch, float scale, uint32_t flags) {
     using Sh = StockhamShape<LOGN, LOGE>;
     constexpr bool ONE_WAVE = (Sh::T * FPB) <= 64;
     __shared__ float2 lds_all[FPB][Sh::LDS_ELEMS];
@@ -154,16 +157,17 @@ __device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) x[m] = make_float2(0.f, 0.f);
     }
-    if constexpr (INV) {
+    if (flags & FG_PASS_CONJ_IN) {
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) x[m] = cconj(x[m]);
     }
     StockhamStages<LOGN, LOGE, 0>::template run<ONE_WAVE>(x, t, tw, lds_all[slot]);
     if (valid) {
+        const bool cs = (flags & FG_PASS_CONJ_SCALE_OUT) != 0;
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) {
             float2 v = x[m];
-            if constexpr (INV) v = cscale(cconj(v), scale);
+            if (cs) v = cscale(cconj(v), scale);
             store_stream(dst + t + Sh::T * m, v);
         }
     }

@@ -1,0 +1,126 @@
+// fft_tile.hpp -- one pass of a multi-pass FFT: G independent transforms of
+// length L = 2^LOGL ("columns") per workgroup, read and written through
+// arbitrary (column, element) strides, with the four-step twiddle fused into
+// the store.
+//
+// Used for 1D lengths above 4096 (N = N_1 * N_2 [* N_3], every pass moves the
+// whole array once) and for the column FFT of 2D images.  The column index is
+// the lane index within a wave, so every global access of a wave covers G
+// adjacent columns -- G*8 contiguous bytes per element row -- and every LDS
+// access of a wave touches one element position of G columns (contiguous in
+// the [position][column] LDS layout, so no bank conflicts).
+//
+// Tile addressing (TileGeom): tile b = t0 + t0n*(t1 + t1n*t2) has input base
+// t0*is0 + t1*is1 + t2*is2 and output base t0*os0 + t1*os1 + t2*os2; element n of
+// column c is at in_base + c*ics + n*ies, output k of column c at
+// out_base + c*ocs + k*oes.  If log_m != 0 the output is multiplied by
+// W_M^(r*k), M = 2^log_m, r = twc*c + tw0*t0 + tw1*t1 (the four-step twiddle of
+// crates/ferrum-gpu-fft/src/warp_fft.rs:138-143, generalised to any pass).
+#pragma once
+#include "fft_stockham.hpp"
+#include "tile_geom.h"
+
+namespace fg {
+
+// W_M^e for M = 2^log_m <= 2^24 from two 4096-entry tables:
+// big[j] = W_4096^j and big[4096 + j] = W_{2^24}^j, so
+// W_{2^24}^e' = big[e' >> 12] * big[4096 + (e' & 4095)] with e' = e * 2^(24 - log_m).
+__device__ __forceinline__ float2 big_twiddle(const float2* __restrict__ big, uint64_t e, uint32_t log_m) {
+    const uint32_t ep = (uint32_t)((e << (24 - log_m)) & 0xFFFFFFull);
+    return cmul(big[ep >> 12], big[4096 + (ep & 4095)]);
+}
+
+// LDS row pitch of the [position][column] layout: one pad column keeps the
+// row-wise staging writes (lanes along positions) off a single bank.
+template <int G>
+struct TilePitch {
+    static constexpr int value = G + 1;
+};
+
+// Stockham stages on a [position][column] LDS tile: thread (c, q) holds
+// positions q + T*m of column c.
+template <int LOGL, int LOGE, int G, int S>
+struct TileStages {
+    using Sh = StockhamShape<LOGL, LOGE>;
+    static constexpr int P = TilePitch<G>::value;
+    __device__ __forceinline__ static void run(float2* x, int q, int c, const float2* __restrict__ tw,
+                                               float2* __restrict__ lds) {
+        stockham_stage_regs<LOGL, LOGE, S>(x, q, tw);
+        if constexpr (S + 1 < Sh::NSTAGES) {
+            constexpr int LOGR = (S < Sh::NFULL) ? LOGE : Sh::REM;
+            constexpr int NB = Sh::E >> LOGR;
+            constexpr int R = 1 << LOGR;
+            __syncthreads();  // previous readers of the tile are done
+#pragma unroll
+            for (int i = 0; i < NB; ++i)
+#pragma unroll
+                for (int r = 0; r < R; ++r) lds[stockham_dst<LOGL, LOGE, S>(q, i, r) * P + c] = x[i + NB * r];
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < Sh::E; ++m) x[m] = lds[(q + Sh::T * m) * P + c];
+            TileStages<LOGL, LOGE, G, S + 1>::run(x, q, c, tw, lds);
+        }
+    }
+};
+
+// ROWWISE: input elements of a column are contiguous (ies == 1, rows of a
+// matrix), so loads run along elements and the tile is transposed into LDS
+// first; otherwise columns are contiguous (ics == 1) and each thread loads its
+// own Stockham positions straight into VGPRs.  Output always has ocs == 1.
+template <int LOGL, int LOGE, int G, bool ROWWISE>
+__device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, float2* __restrict__ out,
+                                              const float2* __restrict__ tw, const float2* __restrict__ big,
+                                              const TileGeom& g) {
+    using Sh = StockhamShape<LOGL, LOGE>;
+    constexpr int P = TilePitch<G>::value;
+    constexpr int THREADS = G * Sh::T;
+    __shared__ float2 lds[Sh::N * P];
+
+    const int tid = threadIdx.x;
+    const int c = tid % G;
+    const int q = tid / G;
+    uint32_t b = blockIdx.x;
+    const uint32_t t0 = b % g.t0n;
+    b /= g.t0n;
+    const uint32_t t1 = b % g.t1n;
+    const uint32_t t2 = b / g.t1n;
+    const uint64_t ib = t0 * g.is0 + t1 * g.is1 + (uint64_t)t2 * g.is2;
+    const uint64_t ob = t0 * g.os0 + t1 * g.os1 + (uint64_t)t2 * g.os2;
+
+    float2 x[Sh::E];
+    if constexpr (ROWWISE) {
+        // Coalesced along each row: linear element li -> (column li / L, position li % L).
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) {
+            const int li = tid + THREADS * m;
+            const int cc = li >> LOGL;
+            const int n = li & (Sh::N - 1);
+            lds[n * P + cc] = load_stream(in + ib + (uint64_t)cc * g.ics + n);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = lds[(q + Sh::T * m) * P + c];
+    } else {
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = load_stream(in + ib + c + (uint64_t)(q + Sh::T * m) * g.ies);
+    }
+    if (g.flags & FG_PASS_CONJ_IN) {
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = cconj(x[m]);
+    }
+    TileStages<LOGL, LOGE, G, 0>::run(x, q, c, tw, lds);
+
+    const bool twid = g.log_m != 0;
+    const uint64_t r = (uint64_t)g.twc * c + (uint64_t)g.tw0 * t0 + (uint64_t)g.tw1 * t1;
+    const bool cs = (g.flags & FG_PASS_CONJ_SCALE_OUT) != 0;
+#pragma unroll
+    for (int m = 0; m < Sh::E; ++m) {
+        const int k = q + Sh::T * m;
+        float2 v = x[m];
+        if (twid) v = cmul(v, big_twiddle(big, r * (uint64_t)k, g.log_m));
+        if (cs) v = cscale(cconj(v), g.scale);
+        store_stream(out + ob + c + (uint64_t)k * g.oes, v);
+    }
+}
+
+}  // namespace fg

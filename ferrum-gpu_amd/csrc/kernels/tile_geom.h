@@ -1,0 +1,34 @@
+/* tile_geom.h -- kernel-argument structs shared by the host runtime (g++) and
+ * the gfx950 kernels (hipcc).  Plain C types only, so both compilers lay them
+ * out identically. */
+#ifndef FG_TILE_GEOM_H
+#define FG_TILE_GEOM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+namespace fg {
+#endif
+
+/* Per-pass flags (Stockham and tile kernels alike). */
+#define FG_PASS_CONJ_IN 1u        /* conjugate every element on load */
+#define FG_PASS_CONJ_SCALE_OUT 2u /* conjugate, then multiply by `scale`, on store */
+
+/* Addressing of one multi-pass tile pass (see fft_tile.hpp). */
+typedef struct TileGeom {
+    uint64_t is0, is1, is2; /* input base = t0*is0 + t1*is1 + t2*is2 */
+    uint64_t os0, os1, os2; /* output base = t0*os0 + t1*os1 + t2*os2 */
+    uint64_t ics, ies;      /* input column / element stride (complex elements) */
+    uint64_t ocs, oes;      /* output column / element stride */
+    uint32_t t0n, t1n;      /* tile counts along t0 and t1 (t2 takes the rest) */
+    uint32_t twc, tw0, tw1; /* four-step twiddle digit r = twc*c + tw0*t0 + tw1*t1 */
+    uint32_t log_m;         /* twiddle W_M^(r*k), M = 2^log_m; 0 = none */
+    uint32_t flags;         /* FG_PASS_* */
+    float scale;
+    uint32_t pad_;
+} TileGeom;
+
+#ifdef __cplusplus
+}  // namespace fg
+#endif
+#endif

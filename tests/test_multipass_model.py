@@ -1,0 +1,173 @@
+"""CPU model of the multi-pass decompositions used for N > 4096 (1D) and 2D,
+checked against the oracle before any kernel exists for them.
+
+1D, N = N_1 * ... * N_P (digit 1 slowest, S_i = N_{i+1} * ... * N_P):
+  pass i < P: for every value of the faster digits r_i and the already
+      transformed slower digits k_1..k_{i-1}: DFT over n_i (stride S_i),
+      multiply by W_{S_{i-1}}^{r_i * k_i} (S_0 = N), store in place;
+  pass P:  DFT over n_P (contiguous rows), store to the digit-reversed output
+      position k_1 + N_1 k_2 + N_1 N_2 k_3 + ...
+2D, N x N image: row FFTs, then the column FFT of length N split the same
+  way (N = C_1 * C_2 with both passes over the slow axis).
+
+`tile_geometry` builds the per-pass geometry (strides, tile counts, twiddle
+coefficients) exactly as FftPlan does on the host; `run_geometry` executes it
+with numpy so the index arithmetic is proven here.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_l2, uniform_c64
+
+
+def tile_columns(log_l):
+    """Columns per tile (tile_columns in fft_plan.cpp)."""
+    return min(64, 16384 >> log_l)
+
+
+def split_1d(log_n):
+    """Digit sizes (log2) for N = 2^log_n, slowest first (split_1d in fft_plan.cpp)."""
+    if log_n <= 20:
+        a = log_n // 2
+        return [log_n - a, a]
+    base = log_n // 3
+    rest = log_n - 3 * base
+    return [base + (1 if rest > 0 else 0), base + (1 if rest > 1 else 0), base]
+
+
+def tile_geometry_1d(log_n, batch):
+    """Per-pass geometry dicts (TileGeom), built as FftPlan::make_1d builds them."""
+    logs = split_1d(log_n)
+    P = len(logs)
+    N = 1 << log_n
+    sizes = [1 << l for l in logs]
+    S = [N]
+    for s in sizes:
+        S.append(S[-1] // s)          # S[i] = stride of digit i (1-based), S[P] = 1
+    passes = []
+    for i in range(1, P):
+        L = sizes[i - 1]
+        cols = S[i]                   # r_i ranges over [0, S_i): the faster digits
+        g = tile_columns(logs[i - 1])
+        assert cols >= g
+        t0n = cols // g               # column groups
+        t1n = N // (S[i - 1])         # values of the slower transformed digits k_1..k_{i-1}
+        passes.append(dict(log_l=logs[i - 1], g=g, rowwise=False,
+                           t0n=t0n, t1n=t1n,
+                           is0=g, is1=S[i - 1], is2=N, ics=1, ies=S[i],
+                           os0=g, os1=S[i - 1], os2=N, ocs=1, oes=S[i],
+                           twc=1, tw0=g, tw1=0, log_m=int(np.log2(S[i - 1]))))
+    # last pass: rows of length N_P, grouped by G' consecutive values of k_1
+    L = sizes[-1]
+    n1 = sizes[0]
+    gp = tile_columns(logs[-1])
+    assert n1 >= gp
+    inner = N // (n1 * L)             # values of k_2..k_{P-1}
+    # the row for (k_1, kmid) starts at k_1*S_1 + sum k_j S_j = k_1*S_1 + kmid*L
+    passes.append(dict(log_l=logs[-1], g=gp, rowwise=True,
+                       t0n=n1 // gp, t1n=inner,
+                       is0=gp * S[1], is1=L, is2=N, ics=S[1], ies=1,
+                       os0=gp, os1=n1, os2=N, ocs=1, oes=N // L,
+                       twc=0, tw0=0, tw1=0, log_m=0))
+    return passes
+
+
+def tile_geometry_2d(log_n, batch):
+    """Column FFT of each N x N image after the row pass, as FftPlan::make_2d builds it:
+    one pass while a tile still spans >= 16 columns, else N = C_1 * C_2 in two."""
+    N = 1 << log_n
+    if tile_columns(log_n) >= 16:
+        g = min(tile_columns(log_n), N)
+        return [dict(log_l=log_n, g=g, rowwise=False, t0n=N // g, t1n=1,
+                     is0=g, is1=0, is2=N * N, ics=1, ies=N,
+                     os0=g, os1=0, os2=N * N, ocs=1, oes=N,
+                     twc=0, tw0=0, tw1=0, log_m=0)]
+    l1 = log_n - log_n // 2
+    l2 = log_n // 2
+    C1, C2 = 1 << l1, 1 << l2
+    g = 64
+    # pass 1: DFT over the slow row digit n_hi (rows n_lo + C2*n_hi) for each (n_lo, column)
+    p1 = dict(log_l=l1, g=g, rowwise=False, t0n=N // g, t1n=C2,
+              is0=g, is1=N, is2=N * N, ics=1, ies=C2 * N,
+              os0=g, os1=N, os2=N * N, ocs=1, oes=C2 * N,
+              twc=0, tw0=0, tw1=1, log_m=log_n)
+    # pass 2: DFT over n_lo (rows C2*k_hi + n_lo) for each (k_hi, column); output row k_hi + C1*k_lo
+    p2 = dict(log_l=l2, g=g, rowwise=False, t0n=N // g, t1n=C1,
+              is0=g, is1=C2 * N, is2=N * N, ics=1, ies=N,
+              os0=g, os1=N, os2=N * N, ocs=1, oes=C1 * N,
+              twc=0, tw0=0, tw1=0, log_m=0)
+    return [p1, p2]
+
+
+def run_geometry(buf_in, passes, batch, elems):
+    """numpy execution of tile passes: out(c, k) = DFT_L over n of in(c, n), times the
+    four-step twiddle, with the affine tile addressing of the kernel."""
+    src = buf_in.astype(np.complex128).copy()
+    for p in passes:
+        L = 1 << p["log_l"]
+        dst = np.zeros_like(src)
+        n = np.arange(L)
+        touched = np.zeros(src.size, dtype=np.int64)
+        for t2 in range(batch):
+            for t1 in range(p["t1n"]):
+                for t0 in range(p["t0n"]):
+                    ib = t0 * p["is0"] + t1 * p["is1"] + t2 * p["is2"]
+                    ob = t0 * p["os0"] + t1 * p["os1"] + t2 * p["os2"]
+                    c = np.arange(p["g"])
+                    iaddr = ib + c[:, None] * p["ics"] + n[None, :] * p["ies"]
+                    oaddr = ob + c[:, None] * p["ocs"] + n[None, :] * p["oes"]
+                    assert iaddr.max() < src.size and oaddr.max() < src.size
+                    y = np.fft.fft(src[iaddr], axis=1)
+                    if p["log_m"]:
+                        M = 1 << p["log_m"]
+                        r = (p["twc"] * c + p["tw0"] * t0 + p["tw1"] * t1) % M
+                        e = (r[:, None] * n[None, :]) % M
+                        y = y * np.exp(-2j * np.pi * e / M)
+                    dst[oaddr] = y
+                    touched[oaddr] += 1
+        # every output position is written exactly once
+        assert np.all(touched == 1)
+        src = dst
+    return src
+
+
+@pytest.mark.parametrize("log_n", [13, 14, 15, 16, 17, 18, 20])
+def test_1d_multipass_matches_oracle(log_n):
+    rng = np.random.default_rng(log_n)
+    batch = 2
+    x = uniform_c64(rng, batch << log_n)
+    got = run_geometry(x, tile_geometry_1d(log_n, batch), batch, 1 << log_n)
+    assert rel_l2(got, oracle.fft_1d(x, log_n)) < 1e-5
+
+
+def test_1d_three_pass_small():
+    # exercise the 3-pass geometry at a size numpy loops finish quickly
+    log_n = 21
+    passes = tile_geometry_1d(log_n, 1)
+    assert len(passes) == 3
+    rng = np.random.default_rng(0)
+    x = uniform_c64(rng, 1 << log_n)
+    got = run_geometry(x, passes, 1, 1 << log_n)
+    assert rel_l2(got, np.fft.fft(x.astype(np.complex128))) < 1e-5
+
+
+@pytest.mark.parametrize("log_n", [4, 5, 6, 8, 10, 11])
+def test_2d_column_passes_match_oracle(log_n):
+    rng = np.random.default_rng(log_n + 100)
+    n = 1 << log_n
+    batch = 2 if log_n <= 10 else 1
+    x = uniform_c64(rng, batch * n * n).reshape(batch, n, n)
+    rows = np.fft.fft(x.astype(np.complex128), axis=2).reshape(-1)
+    got = run_geometry(rows, tile_geometry_2d(log_n, batch), batch, n * n).reshape(batch, n, n)
+    assert rel_l2(got, oracle.fft_2d(x, log_n)) < 1e-5
+
+
+def test_split_sizes_fit_the_tile_kernel():
+    for log_n in range(13, 25):
+        logs = split_1d(log_n)
+        assert sum(logs) == log_n
+        assert all(4 <= l <= 11 for l in logs), (log_n, logs)
