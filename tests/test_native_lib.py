@@ -57,7 +57,7 @@ def test_code_object_is_embedded_for_gfx950():
     data = open(N.LIB_PATH, "rb").read()
     assert data.count(b"\x7fELF") >= 2
     assert b"gfx950" in data
-    for k in ("fg_fft_n10_fwd", "fg_fft_n12_inv", "fg_copy_f4", "fg_vector_add"):
+    for k in ("fg_fft_n10", "fg_fft_n12", "fg_tile_l8_g64_c", "fg_tile_l8_g64_r", "fg_copy_f4", "fg_vector_add"):
         assert k.encode() in data
 
 
