@@ -11,6 +11,7 @@
 #include <mutex>
 #include <string>
 #include <tuple>
+#include <vector>
 
 #include "device.hpp"
 #include "fft_plan.hpp"
@@ -430,6 +431,39 @@ int fg_fft_exec(fg_fft_plan_t plan, const void* d_in, void* d_out, int direction
         need(d_in, "d_in");
         need(d_out, "d_out");
         plan->plan->exec(d_in, d_out, parse_dir(direction), normalize != 0, (hipStream_t)stream);
+    });
+}
+
+int fg_fft_exec_events(fg_fft_plan_t plan, const void* d_in, void* d_out, int direction, int normalize,
+                       fg_stream_t stream, fg_event_t* events, int nevents) {
+    return guarded([&] {
+        need(plan, "plan");
+        need(d_in, "d_in");
+        need(d_out, "d_out");
+        need(events, "events");
+        const FftPlan& p = *plan->plan;
+        if (nevents != p.launches() + 1)
+            fg::invalid("fg_fft_exec_events: need " + std::to_string(p.launches() + 1) + " events, got " +
+                        std::to_string(nevents));
+        std::vector<hipEvent_t> evs((size_t)nevents);
+        for (int i = 0; i < nevents; ++i) {
+            need(events[i], "event");
+            evs[i] = events[i]->ev;
+        }
+        p.exec(d_in, d_out, parse_dir(direction), normalize != 0, (hipStream_t)stream, evs.data());
+    });
+}
+
+int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char* name, size_t cap) {
+    return guarded([&] {
+        need(plan, "plan");
+        need(name, "name");
+        auto names = plan->plan->kernel_names();
+        if (index < 0 || (size_t)index >= names.size()) fg::invalid("launch index out of range");
+        if (cap) {
+            strncpy(name, names[index].c_str(), cap - 1);
+            name[cap - 1] = 0;
+        }
     });
 }
 

@@ -96,9 +96,16 @@ std::vector<uint32_t> split_1d(uint32_t log_n) {
 }
 
 uint32_t tile_columns(uint32_t log_l) {
-    const uint32_t g = 16384u >> log_l;
-    return g > 64 ? 64 : g;
+    // Measured on gfx950 at 2^24 = 256^3: 32 columns of 256 points (two
+    // 66 KB workgroups per CU) beat 64 (one 133 KB workgroup); fewer than 16
+    // columns (128-byte segments) loses HBM efficiency, so the floor is 16.
+    uint32_t g = 8192u >> log_l;
+    if (g > 64) g = 64;
+    if (g < 16) g = 16;
+    return g;
 }
+
+bool split_2d_columns(uint32_t log_n) { return log_n > 10; }
 
 namespace {
 
@@ -246,7 +253,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     if (batch == 0) invalid("batch must be positive");
     std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::TwoD, log_n, batch));
     const uint64_t N = 1ull << log_n, NN = N * N;
-    const bool split = tile_columns(log_n) < 16;  // 4096-point columns would leave < 16 per tile
+    const bool split = split_2d_columns(log_n);  // a 2048/4096-point column tile would leave < 16 columns
     if (split) p->work_ = dev.alloc<Cf32>(NN * batch);
     // Row pass (the reference's K1 row FFT, py lib.rs:325-336): N*batch rows.
     p->add_stockham(mod, log_n, N * batch, Buf::In, split ? Buf::Work : Buf::Out);
@@ -307,7 +314,8 @@ std::vector<std::string> FftPlan::kernel_names() const {
     return v;
 }
 
-void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream) const {
+void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
+                   hipEvent_t* events) const {
     if (!in || !out) invalid("fft exec: null buffer");
     const bool inverse = dir == Direction::Inverse;
     const float scale = (inverse && normalize)
@@ -315,7 +323,9 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
                                                    : 1.0f / (float)(1ull << log_n_))
                             : 1.0f;
     const void* big = big_.data();
+    hipStream_t st = stream ? stream : dev_->default_stream();
     for (size_t i = 0; i < steps_.size(); ++i) {
+        if (events) hip_check(hipEventRecord(events[i], st), "hipEventRecord");
         const Step& s = steps_[i];
         uint32_t flags = 0;
         if (inverse && i == 0) flags |= FG_PASS_CONJ_IN;
@@ -343,6 +353,7 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
             HipBackend::launch(dev_->handle(), stream, s.fn, s.grid, s.block, 0, args);
         }
     }
+    if (events) hip_check(hipEventRecord(events[steps_.size()], st), "hipEventRecord");
 }
 
 }  // namespace fg

@@ -47,7 +47,10 @@ public:
                                             size_t batch);
 
     // Forward or inverse transform of batch transforms from in to out (may alias).
-    void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream) const;
+    // With `events` (launches() + 1 of them), events[i] is recorded on the
+    // stream before launch i and events[launches()] after the last one.
+    void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
+              hipEvent_t* events = nullptr) const;
 
     Kind kind() const { return kind_; }
     uint32_t log_n() const { return log_n_; }
@@ -106,7 +109,9 @@ std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e);
 std::vector<Cf32> big_twiddles();
 // Digit split (log2 sizes, slowest digit first) of a 1D length 2^log_n > 4096.
 std::vector<uint32_t> split_1d(uint32_t log_n);
-// Columns per tile for a column-wise pass of length 2^log_l.
+// Columns per tile for a pass of length 2^log_l.
 uint32_t tile_columns(uint32_t log_l);
+// Whether the column FFT of an N x N image (N = 2^log_n) runs as two passes.
+bool split_2d_columns(uint32_t log_n);
 
 }  // namespace fg

@@ -73,19 +73,21 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
         fg_tile_l##LOGL##_g##G##_##TAG(const float2* __restrict__ in, float2* __restrict__ out,     \
                                        const float2* __restrict__ tw, const float2* __restrict__ big, \
                                        TileGeom g) {                                                  \
-        fft_tile_body<LOGL, (LOGL < 4 ? LOGL : 4), G, RW>(in, out, tw, big, g);                      \
+        fft_tile_body<LOGL, (LOGL < 4 ? LOGL : 4), G, RW, true>(in, out, tw, big, g);                \
     }
 
+// Column passes (1D digits of 128..1024 points, 2D columns of 16..1024 and
+// the 2048/4096 column splits) and row passes (last 1D digit).
 FG_TILE(4, 16, false, c)
 FG_TILE(5, 32, false, c)
 FG_TILE(5, 64, false, c)
 FG_TILE(6, 64, false, c)
 FG_TILE(7, 64, false, c)
-FG_TILE(8, 64, false, c)
-FG_TILE(9, 32, false, c)
+FG_TILE(8, 32, false, c)
+FG_TILE(9, 16, false, c)
 FG_TILE(10, 16, false, c)
 FG_TILE(6, 64, true, r)
 FG_TILE(7, 64, true, r)
-FG_TILE(8, 64, true, r)
-FG_TILE(9, 32, true, r)
+FG_TILE(8, 32, true, r)
+FG_TILE(9, 16, true, r)
 FG_TILE(10, 16, true, r)

@@ -30,6 +30,28 @@ __device__ __forceinline__ float2 big_twiddle(const float2* __restrict__ big, ui
     return cmul(big[ep >> 12], big[4096 + (ep & 4095)]);
 }
 
+// Multiplies x[m] (output position k = q + T*m) by W_M^(r*k).  TWREC = false
+// looks every factor up (2 table reads + 1 multiply each); TWREC = true looks
+// up W^(r*q) and W^(r*T) once and forms the rest as W^(r*q) * (W^(r*T))^m by
+// repeated multiplication (error grows by about one rounding per step, ~1e-6
+// relative after 16 steps).
+template <int E, int T, bool TWREC>
+__device__ __forceinline__ void apply_pass_twiddle(float2* x, const float2* __restrict__ big, uint64_t r, int q,
+                                                   uint32_t log_m) {
+    if constexpr (TWREC) {
+        float2 w = big_twiddle(big, r * (uint64_t)q, log_m);
+        const float2 step = big_twiddle(big, r * (uint64_t)T, log_m);
+#pragma unroll
+        for (int m = 0; m < E; ++m) {
+            x[m] = cmul(x[m], w);
+            if (m + 1 < E) w = cmul(w, step);
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < E; ++m) x[m] = cmul(x[m], big_twiddle(big, r * (uint64_t)(q + T * m), log_m));
+    }
+}
+
 // LDS row pitch of the [position][column] layout: one pad column keeps the
 // row-wise staging writes (lanes along positions) off a single bank.
 template <int G>
@@ -67,7 +89,7 @@ struct TileStages {
 // matrix), so loads run along elements and the tile is transposed into LDS
 // first; otherwise columns are contiguous (ics == 1) and each thread loads its
 // own Stockham positions straight into VGPRs.  Output always has ocs == 1.
-template <int LOGL, int LOGE, int G, bool ROWWISE>
+template <int LOGL, int LOGE, int G, bool ROWWISE, bool TWREC = false>
 __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, float2* __restrict__ out,
                                               const float2* __restrict__ tw, const float2* __restrict__ big,
                                               const TileGeom& g) {
@@ -110,14 +132,15 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
     }
     TileStages<LOGL, LOGE, G, 0>::run(x, q, c, tw, lds);
 
-    const bool twid = g.log_m != 0;
-    const uint64_t r = (uint64_t)g.twc * c + (uint64_t)g.tw0 * t0 + (uint64_t)g.tw1 * t1;
+    if (g.log_m != 0) {
+        const uint64_t r = (uint64_t)g.twc * c + (uint64_t)g.tw0 * t0 + (uint64_t)g.tw1 * t1;
+        apply_pass_twiddle<Sh::E, Sh::T, TWREC>(x, big, r, q, g.log_m);
+    }
     const bool cs = (g.flags & FG_PASS_CONJ_SCALE_OUT) != 0;
 #pragma unroll
     for (int m = 0; m < Sh::E; ++m) {
         const int k = q + Sh::T * m;
         float2 v = x[m];
-        if (twid) v = cmul(v, big_twiddle(big, r * (uint64_t)k, g.log_m));
         if (cs) v = cscale(cconj(v), g.scale);
         store_stream(out + ob + c + (uint64_t)k * g.oes, v);
     }

@@ -104,6 +104,8 @@ _sig("fg_fft_plan_2d", _vp, _u32, _sz, _P(_vp))
 _sig("fg_fft_plan_destroy", _vp)
 _sig("fg_fft_exec", _vp, _vp, _vp, _i, _i, _vp)
 _sig("fg_fft_plan_describe", _vp, _P(_i), ctypes.c_char_p, _sz, _P(_sz))
+_sig("fg_fft_exec_events", _vp, _vp, _vp, _i, _i, _vp, _P(_vp), _i)
+_sig("fg_fft_plan_kernel", _vp, _i, ctypes.c_char_p, _sz)
 _sig("fg_fft_1d_c2c_pow2_host", _vp, _vp, _vp, _sz, _u32, _i, _i)
 _sig("fg_fft_2d_c2c_pow2_host", _vp, _vp, _vp, _u32, _sz, _i, _i)
 _sig("fg_stream_copy", _vp, _vp, _vp, _sz, _vp)

@@ -143,6 +143,23 @@ class _Plan:
         _n.check(_n.lib.fg_fft_exec(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),
                                     ctypes.c_void_p(stream or None)))
 
+    def execute_recording(self, d_in, d_out, events, direction="forward", normalize=False,
+                          stream: int = 0) -> None:
+        """execute() that records events[i] before launch i and events[-1] after the
+        last launch (len(events) == launches + 1), without synchronising."""
+        d = _direction(direction)
+        arr = (ctypes.c_void_p * len(events))(*[e._e.value for e in events])
+        _n.check(_n.lib.fg_fft_exec_events(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),
+                                           ctypes.c_void_p(stream or None), arr, len(events)))
+
+    def kernel_names(self) -> list[str]:
+        names = []
+        for i in range(self.describe()["launches"]):
+            buf = ctypes.create_string_buffer(128)
+            _n.check(_n.lib.fg_fft_plan_kernel(self._p, i, buf, 128))
+            names.append(buf.value.decode())
+        return names
+
     def describe(self) -> dict:
         launches = ctypes.c_int()
         name = ctypes.create_string_buffer(128)

@@ -147,6 +147,16 @@ FG_API int fg_fft_plan_destroy(fg_fft_plan_t plan);
  * direction: FG_FORWARD or FG_INVERSE.  stream NULL = device default stream. */
 FG_API int fg_fft_exec(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction, int normalize,
                 fg_stream_t stream);
+/* fg_fft_exec that also records events[i] on the stream before launch i and
+ * events[launches] after the last launch (nevents must be launches + 1); no
+ * synchronisation.  For per-kernel timing in benchmarks: the reference's
+ * bench brackets its single launch with an event pair
+ * (crates/ferrum-gpu-bench/src/lib.rs:163-198); multi-pass plans need one
+ * pair per launch. */
+FG_API int fg_fft_exec_events(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction,
+                              int normalize, fg_stream_t stream, fg_event_t *events, int nevents);
+/* Kernel name of launch `index` of an execution. */
+FG_API int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char *name, size_t cap);
 /* Number of kernel launches per execution and the name of the kernel that
  * moves the most bytes (what the bench times and profiles). */
 FG_API int fg_fft_plan_describe(fg_fft_plan_t plan, int *launches, char *main_kernel, size_t cap,

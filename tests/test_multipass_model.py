@@ -26,7 +26,7 @@ from conftest import rel_l2, uniform_c64
 
 def tile_columns(log_l):
     """Columns per tile (tile_columns in fft_plan.cpp)."""
-    return min(64, 16384 >> log_l)
+    return max(16, min(64, 8192 >> log_l))
 
 
 def split_1d(log_n):
@@ -80,7 +80,7 @@ def tile_geometry_2d(log_n, batch):
     """Column FFT of each N x N image after the row pass, as FftPlan::make_2d builds it:
     one pass while a tile still spans >= 16 columns, else N = C_1 * C_2 in two."""
     N = 1 << log_n
-    if tile_columns(log_n) >= 16:
+    if log_n <= 10:                   # split_2d_columns in fft_plan.cpp
         g = min(tile_columns(log_n), N)
         return [dict(log_l=log_n, g=g, rowwise=False, t0n=N // g, t1n=1,
                      is0=g, is1=0, is2=N * N, ics=1, ies=N,

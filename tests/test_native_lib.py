@@ -52,13 +52,41 @@ def test_version_and_backend():
     assert N.backend_id() == N.FG_BACKEND_HIP == 3  # BackendId with Hip added
 
 
+def instantiated_kernels():
+    src = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
+    names = {f"fg_fft_n{m.group(1)}" for m in re.finditer(r"^FG_STOCKHAM\((\d+),", src, flags=re.M)}
+    for m in re.finditer(r"^FG_TILE\((\d+), (\d+), (true|false), ([cr])\)", src, flags=re.M):
+        names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_{m.group(4)}")
+    return names
+
+
+def planned_kernels():
+    """Every kernel name FftPlan can request (mirrors fft_plan.cpp via the CPU models)."""
+    from test_multipass_model import tile_geometry_1d, tile_geometry_2d
+
+    names = {f"fg_fft_n{l}" for l in range(2, 13)}
+    for log_n in range(13, 25):
+        for p in tile_geometry_1d(log_n, 1):
+            names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}")
+    for log_n in range(4, 13):
+        for p in tile_geometry_2d(log_n, 1):
+            names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}")
+    return names
+
+
+def test_every_planned_kernel_is_instantiated():
+    missing = planned_kernels() - instantiated_kernels()
+    assert not missing, sorted(missing)
+
+
 def test_code_object_is_embedded_for_gfx950():
-    # The .so carries the gfx950 code object (an ELF for amdgcn) in .rodata.
+    # The .so carries the gfx950 code object (an ELF for amdgcn) in .rodata,
+    # with every instantiated kernel.
     data = open(N.LIB_PATH, "rb").read()
     assert data.count(b"\x7fELF") >= 2
     assert b"gfx950" in data
-    for k in ("fg_fft_n10", "fg_fft_n12", "fg_tile_l8_g64_c", "fg_tile_l8_g64_r", "fg_copy_f4", "fg_vector_add"):
-        assert k.encode() in data
+    for k in sorted(instantiated_kernels()) + ["fg_copy_f4", "fg_vector_add"]:
+        assert k.encode() in data, k
 
 
 # --------------------------------------------------- argument validation
