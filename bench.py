@@ -224,9 +224,14 @@ def main() -> int:
     dev.sync()
     log(f"warmup {args.warmup} done")
 
-    evs = [[[Event(dev) for _ in range(launches + 1)] for _ in steps] for _ in range(args.steps)]
+    # One event after every launch (plus one before the first): launch i ran
+    # between consecutive events.  One marker per launch costs ~2 us of gap per
+    # launch; a pair per launch measured ~6 us.
+    start = Event(dev)
+    evs = [[[Event(dev) for _ in range(launches)] for _ in steps] for _ in range(args.steps)]
     dev.sync()
     t0 = time.perf_counter()
+    start.record(stream)
     for k in range(args.steps):
         step(evs[k])
     dev.sync()
@@ -234,10 +239,12 @@ def main() -> int:
     log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms")
 
     per_kernel: dict[str, list[float]] = {}
+    prev = start
     for k in range(args.steps):
         for j in range(len(steps)):
             for i, name in enumerate(kernels):
-                per_kernel.setdefault(f"{i}:{name}", []).append(evs[k][j][i].elapsed_ms(evs[k][j][i + 1]))
+                per_kernel.setdefault(f"{i}:{name}", []).append(prev.elapsed_ms(evs[k][j][i]))
+                prev = evs[k][j][i]
     kernel_ms = {key: float(np.mean(v)) for key, v in per_kernel.items()}
     dominant = max(kernel_ms, key=lambda key: kernel_ms[key] * len(per_kernel[key]))
     dom_name = dominant.split(":", 1)[1]

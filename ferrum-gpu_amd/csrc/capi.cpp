@@ -442,8 +442,8 @@ int fg_fft_exec_events(fg_fft_plan_t plan, const void* d_in, void* d_out, int di
         need(d_out, "d_out");
         need(events, "events");
         const FftPlan& p = *plan->plan;
-        if (nevents != p.launches() + 1)
-            fg::invalid("fg_fft_exec_events: need " + std::to_string(p.launches() + 1) + " events, got " +
+        if (nevents != p.launches())
+            fg::invalid("fg_fft_exec_events: need " + std::to_string(p.launches()) + " events, got " +
                         std::to_string(nevents));
         std::vector<hipEvent_t> evs((size_t)nevents);
         for (int i = 0; i < nevents; ++i) {

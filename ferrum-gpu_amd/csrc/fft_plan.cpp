@@ -325,7 +325,6 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
     const void* big = big_.data();
     hipStream_t st = stream ? stream : dev_->default_stream();
     for (size_t i = 0; i < steps_.size(); ++i) {
-        if (events) hip_check(hipEventRecord(events[i], st), "hipEventRecord");
         const Step& s = steps_[i];
         uint32_t flags = 0;
         if (inverse && i == 0) flags |= FG_PASS_CONJ_IN;
@@ -352,8 +351,8 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
             void* args[] = {&src, &dst, (void*)&tw, (void*)&big, &g};
             HipBackend::launch(dev_->handle(), stream, s.fn, s.grid, s.block, 0, args);
         }
+        if (events) hip_check(hipEventRecord(events[i], st), "hipEventRecord");
     }
-    if (events) hip_check(hipEventRecord(events[steps_.size()], st), "hipEventRecord");
 }
 
 }  // namespace fg

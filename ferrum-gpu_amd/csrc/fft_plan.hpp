@@ -47,8 +47,8 @@ public:
                                             size_t batch);
 
     // Forward or inverse transform of batch transforms from in to out (may alias).
-    // With `events` (launches() + 1 of them), events[i] is recorded on the
-    // stream before launch i and events[launches()] after the last one.
+    // With `events` (launches() of them), events[i] is recorded on the stream
+    // right after launch i.
     void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
               hipEvent_t* events = nullptr) const;
 

@@ -140,19 +140,38 @@ __device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
                                                   uint64_t batch, float scale, uint32_t flags) {
     using Sh = StockhamShape<LOGN, LOGE>;
     constexpr bool ONE_WAVE = (Sh::T * FPB) <= 64;
+    // With fewer than 8 threads per transform a thread's positions t + T*m
+    // give each wave only T*8-byte pieces per load; such sizes move the
+    // workgroup's FPB contiguous transforms through LDS instead, 64 lanes x 8
+    // contiguous bytes per instruction.
+    constexpr bool STAGED = Sh::T < 8 && FPB > 1;  // measured: N = 128 (T = 8) is faster direct
+    constexpr int BLOCK = FPB * Sh::T;
     __shared__ float2 lds_all[FPB][Sh::LDS_ELEMS];
     const int tid = threadIdx.x;
     const int slot = tid / Sh::T;
     const int t = tid - slot * Sh::T;
-    const uint64_t f = (uint64_t)blockIdx.x * FPB + slot;
+    const uint64_t f0 = (uint64_t)blockIdx.x * FPB;
+    const uint64_t f = f0 + slot;
     const bool valid = f < batch;
-    const float2* src = in + f * Sh::N;
-    float2* dst = out + f * Sh::N;
+    const bool cs = (flags & FG_PASS_CONJ_SCALE_OUT) != 0;
 
     float2 x[Sh::E];
-    if (valid) {
+    if constexpr (STAGED) {
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = load_stream(src + t + Sh::T * m);
+        for (int j = 0; j < Sh::E; ++j) {
+            const int e = tid + BLOCK * j;  // element of the block's FPB*N
+            const int fs = e >> LOGN;
+            float2 v = make_float2(0.f, 0.f);
+            if (f0 + fs < batch) v = load_stream(in + f0 * Sh::N + e);
+            lds_all[fs][lds_pos(e & (Sh::N - 1))] = v;
+        }
+        if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = lds_all[slot][lds_pos(t + Sh::T * m)];
+        if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
+    } else if (valid) {
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = load_stream(in + f * Sh::N + t + Sh::T * m);
     } else {
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) x[m] = make_float2(0.f, 0.f);
@@ -162,13 +181,27 @@ __device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
         for (int m = 0; m < Sh::E; ++m) x[m] = cconj(x[m]);
     }
     StockhamStages<LOGN, LOGE, 0>::template run<ONE_WAVE>(x, t, tw, lds_all[slot]);
-    if (valid) {
-        const bool cs = (flags & FG_PASS_CONJ_SCALE_OUT) != 0;
+    if constexpr (STAGED) {
+        if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) {
             float2 v = x[m];
             if (cs) v = cscale(cconj(v), scale);
-            store_stream(dst + t + Sh::T * m, v);
+            lds_all[slot][lds_pos(t + Sh::T * m)] = v;
+        }
+        if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
+#pragma unroll
+        for (int j = 0; j < Sh::E; ++j) {
+            const int e = tid + BLOCK * j;
+            const int fs = e >> LOGN;
+            if (f0 + fs < batch) store_stream(out + f0 * Sh::N + e, lds_all[fs][lds_pos(e & (Sh::N - 1))]);
+        }
+    } else if (valid) {
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) {
+            float2 v = x[m];
+            if (cs) v = cscale(cconj(v), scale);
+            store_stream(out + f * Sh::N + t + Sh::T * m, v);
         }
     }
 }

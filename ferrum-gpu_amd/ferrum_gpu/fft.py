@@ -145,8 +145,9 @@ class _Plan:
 
     def execute_recording(self, d_in, d_out, events, direction="forward", normalize=False,
                           stream: int = 0) -> None:
-        """execute() that records events[i] before launch i and events[-1] after the
-        last launch (len(events) == launches + 1), without synchronising."""
+        """execute() that records events[i] right after launch i (len(events) ==
+        launches), without synchronising; launch i ran between the previous event
+        recorded on the stream and events[i]."""
         d = _direction(direction)
         arr = (ctypes.c_void_p * len(events))(*[e._e.value for e in events])
         _n.check(_n.lib.fg_fft_exec_events(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),

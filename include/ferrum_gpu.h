@@ -147,12 +147,13 @@ FG_API int fg_fft_plan_destroy(fg_fft_plan_t plan);
  * direction: FG_FORWARD or FG_INVERSE.  stream NULL = device default stream. */
 FG_API int fg_fft_exec(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction, int normalize,
                 fg_stream_t stream);
-/* fg_fft_exec that also records events[i] on the stream before launch i and
- * events[launches] after the last launch (nevents must be launches + 1); no
- * synchronisation.  For per-kernel timing in benchmarks: the reference's
- * bench brackets its single launch with an event pair
- * (crates/ferrum-gpu-bench/src/lib.rs:163-198); multi-pass plans need one
- * pair per launch. */
+/* fg_fft_exec that also records events[i] on the stream right after launch i
+ * (nevents must equal the plan's launch count); no synchronisation.  Launch
+ * i's duration is the time from the previous event on the stream (the
+ * caller's start event, or events[i-1]) to events[i].  For per-kernel timing
+ * in benchmarks: the reference's bench brackets its single launch with an
+ * event pair (crates/ferrum-gpu-bench/src/lib.rs:163-198); recording one event
+ * per launch keeps the marker overhead between back-to-back launches to one. */
 FG_API int fg_fft_exec_events(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction,
                               int normalize, fg_stream_t stream, fg_event_t *events, int nevents);
 /* Kernel name of launch `index` of an execution. */

@@ -110,6 +110,21 @@ def test_twiddle_rows_are_16_byte_aligned():
         assert all(o % 2 == 0 for o in offs), log_n
 
 
+def test_staged_block_mapping_covers_each_element_once():
+    # Sizes with T < 8 threads per transform stage their FPB transforms
+    # through LDS: element e = tid + BLOCK*j of the block -> transform e >> log_n,
+    # position e & (N-1).  Every element once, every LDS index in its slot.
+    for log_n, (log_e, fpb) in GEOM.items():
+        n, t_per = 1 << log_n, (1 << log_n) >> log_e
+        if not (t_per < 8 and fpb > 1):
+            continue
+        block, e_per = fpb * t_per, 1 << log_e
+        e = (np.arange(block)[:, None] + block * np.arange(e_per)[None, :]).reshape(-1)
+        assert np.array_equal(np.sort(e), np.arange(fpb * n))
+        assert (e >> log_n).max() < fpb
+        assert lds_pos(e & (n - 1)).max() < n + n // 16
+
+
 def test_geometry_fits_hardware():
     for log_n, (log_e, fpb) in GEOM.items():
         threads = ((1 << log_n) >> log_e) * fpb
