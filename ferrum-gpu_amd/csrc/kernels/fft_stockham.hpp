@@ -103,6 +103,49 @@ __device__ __forceinline__ int stockham_dst(int t, int i, int q) {
     return j * L * R + k + q * L;
 }
 
+// LDS addresses as a per-thread base plus compile-time offsets, using
+// lds_pos(a + 16c) = lds_pos(a) + 17c: the gather of position t + T*m and the
+// scatter of output q of butterfly i then need no per-element index
+// arithmetic (ds_read/ds_write take the offset as an immediate).
+template <int LOGN, int LOGE>
+__device__ __forceinline__ void lds_gather(float2* x, const float2* __restrict__ lds, int t) {
+    using Sh = StockhamShape<LOGN, LOGE>;
+    if constexpr (Sh::T % 16 == 0) {
+        const float2* base = lds + lds_pos(t);
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = base[m * (Sh::T + Sh::T / 16)];
+    } else {
+#pragma unroll
+        for (int m = 0; m < Sh::E; ++m) x[m] = lds[lds_pos(t + Sh::T * m)];
+    }
+}
+
+template <int LOGN, int LOGE, int S>
+__device__ __forceinline__ void lds_scatter(const float2* x, float2* __restrict__ lds, int t) {
+    using Sh = StockhamShape<LOGN, LOGE>;
+    constexpr int LOGR = (S < Sh::NFULL) ? LOGE : Sh::REM;
+    constexpr int NB = Sh::E >> LOGR;
+    constexpr int R = 1 << LOGR;
+    constexpr int L = 1 << (S * LOGE);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if constexpr (L == 1 && R == 16) {
+            // dst = 16*b + q, q < 16  ->  lds_pos = 17*b + q
+            float2* base = lds + 17 * (t + Sh::T * i);
+#pragma unroll
+            for (int q = 0; q < R; ++q) base[q] = x[i + NB * q];
+        } else if constexpr (L % 16 == 0) {
+            // dst = (j*L*R + k) + q*L with L a multiple of 16
+            float2* base = lds + lds_pos(stockham_dst<LOGN, LOGE, S>(t, i, 0));
+#pragma unroll
+            for (int q = 0; q < R; ++q) base[q * (L + L / 16)] = x[i + NB * q];
+        } else {
+#pragma unroll
+            for (int q = 0; q < R; ++q) lds[lds_pos(stockham_dst<LOGN, LOGE, S>(t, i, q))] = x[i + NB * q];
+        }
+    }
+}
+
 template <int LOGN, int LOGE, int S>
 struct StockhamStages {
     using Sh = StockhamShape<LOGN, LOGE>;
@@ -112,17 +155,9 @@ struct StockhamStages {
                                                float2* __restrict__ lds) {
         stockham_stage_regs<LOGN, LOGE, S>(x, t, tw);
         if constexpr (S + 1 < Sh::NSTAGES) {
-            constexpr int LOGR = (S < Sh::NFULL) ? LOGE : Sh::REM;
-            constexpr int NB = Sh::E >> LOGR;
-            constexpr int R = 1 << LOGR;
-#pragma unroll
-            for (int i = 0; i < NB; ++i)
-#pragma unroll
-                for (int q = 0; q < R; ++q)
-                    lds[lds_pos(stockham_dst<LOGN, LOGE, S>(t, i, q))] = x[i + NB * q];
+            lds_scatter<LOGN, LOGE, S>(x, lds, t);
             if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
-#pragma unroll
-            for (int m = 0; m < Sh::E; ++m) x[m] = lds[lds_pos(t + Sh::T * m)];
+            lds_gather<LOGN, LOGE>(x, lds, t);
             if constexpr (S + 2 < Sh::NSTAGES) {
                 if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
             }
