@@ -30,7 +30,8 @@ struct fg_device {
     std::unique_ptr<HipDevice> dev;
     HipBackend::Module fft_module;
     std::mutex mu;  // guards the plan cache and the staging buffer of the host path
-    std::map<std::tuple<int, uint32_t, size_t>, std::unique_ptr<FftPlan>> plans;
+    // key: (dims, log_n or log_cols, log_rows (0 for 1D), batch)
+    std::map<std::tuple<int, uint32_t, uint32_t, size_t>, std::unique_ptr<FftPlan>> plans;
     Buffer<Cf32, HipBackend> staging;
 };
 
@@ -111,12 +112,12 @@ fg_device* default_device() {
     return dev;
 }
 
-FftPlan& cached_plan(fg_device* d, int dims, uint32_t log_n, size_t batch) {
-    auto key = std::make_tuple(dims, log_n, batch);
+FftPlan& cached_plan(fg_device* d, int dims, uint32_t log_n, uint32_t log_rows, size_t batch) {
+    auto key = std::make_tuple(dims, log_n, log_rows, batch);
     auto it = d->plans.find(key);
     if (it != d->plans.end()) return *it->second;
     auto p = dims == 1 ? FftPlan::make_1d(*d->dev, d->fft_module, log_n, batch)
-                       : FftPlan::make_2d(*d->dev, d->fft_module, log_n, batch);
+                       : FftPlan::make_2d(*d->dev, d->fft_module, log_rows, log_n, batch);
     FftPlan& ref = *p;
     d->plans.emplace(key, std::move(p));
     return ref;
@@ -130,10 +131,10 @@ Direction parse_dir(int direction) {
 
 // Host path shared by the 1D and 2D entry points: stage through one device
 // buffer (grown on demand, kept per device), run in place, copy back.
-void run_host(fg_device* d, int dims, uint32_t log_n, size_t batch, size_t total, const float* in, float* out,
-              Direction dir, bool normalize) {
+void run_host(fg_device* d, int dims, uint32_t log_n, uint32_t log_rows, size_t batch, size_t total,
+              const float* in, float* out, Direction dir, bool normalize) {
     std::lock_guard<std::mutex> g(d->mu);
-    FftPlan& plan = cached_plan(d, dims, log_n, batch);
+    FftPlan& plan = cached_plan(d, dims, log_n, log_rows, batch);
     if (d->staging.len() < total) {
         d->staging.reset();
         d->staging = d->dev->alloc<Cf32>(total);
@@ -415,7 +416,7 @@ int fg_fft_plan_2d(fg_device_t dev, uint32_t log_n, size_t batch, fg_fft_plan_t*
         *out = nullptr;
         std::unique_ptr<fg_fft_plan> p(new fg_fft_plan);
         p->dev = dev;
-        p->plan = FftPlan::make_2d(*dev->dev, dev->fft_module, log_n, batch);
+        p->plan = FftPlan::make_2d(*dev->dev, dev->fft_module, log_n, log_n, batch);
         *out = p.release();
     });
 }
@@ -496,7 +497,7 @@ int fg_fft_1d_c2c_pow2_host(fg_device_t dev, const float* in, float* out, size_t
         need(in, "in");
         need(out, "out");
         fg_device* d = dev ? dev : default_device();
-        run_host(d, 1, log_n, total_complex / n, total_complex, in, out, dir, normalize != 0);
+        run_host(d, 1, log_n, 0, total_complex / n, total_complex, in, out, dir, normalize != 0);
     });
 }
 
@@ -513,7 +514,44 @@ int fg_fft_2d_c2c_pow2_host(fg_device_t dev, const float* in, float* out, uint32
         need(out, "out");
         fg_device* d = dev ? dev : default_device();
         const size_t total = (size_t(1) << (2 * log_n)) * batch;
-        run_host(d, 2, log_n, batch, total, in, out, dir, normalize != 0);
+        run_host(d, 2, log_n, log_n, batch, total, in, out, dir, normalize != 0);
+    });
+}
+
+int fg_fft_2d_rect_host(fg_device_t dev, const float* in, float* out, uint32_t log_rows, uint32_t log_cols,
+                        size_t batch, int direction, int normalize) {
+    return guarded([&] {
+        for (uint32_t l : {log_rows, log_cols})
+            if (l < fg::kMinLogN2D || l > fg::kMaxLogN2D)
+                fg::invalid("2D requires log_n in [" + std::to_string(fg::kMinLogN2D) + ", " +
+                            std::to_string(fg::kMaxLogN2D) + "]; got " + std::to_string(l));
+        if (batch == 0) fg::invalid("batch must be positive");
+        Direction dir = parse_dir(direction);
+        need(in, "in");
+        need(out, "out");
+        fg_device* d = dev ? dev : default_device();
+        const size_t total = (size_t(1) << (log_rows + log_cols)) * batch;
+        run_host(d, 2, log_cols, log_rows, batch, total, in, out, dir, normalize != 0);
+    });
+}
+
+int fg_fft_plan_2d_rect(fg_device_t dev, uint32_t log_rows, uint32_t log_cols, size_t batch, fg_fft_plan_t* out) {
+    return guarded([&] {
+        need(dev, "device");
+        need(out, "out");
+        *out = nullptr;
+        std::unique_ptr<fg_fft_plan> p(new fg_fft_plan);
+        p->dev = dev;
+        p->plan = FftPlan::make_2d(*dev->dev, dev->fft_module, log_rows, log_cols, batch);
+        *out = p.release();
+    });
+}
+
+int fg_transpose_c64(fg_device_t dev, const void* d_in, void* d_out, uint32_t rows, uint32_t cols, size_t batch,
+                     fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        fg::transpose_c64(*dev->dev, dev->fft_module, d_in, d_out, rows, cols, batch, (hipStream_t)stream);
     });
 }
 

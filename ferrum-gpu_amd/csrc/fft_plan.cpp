@@ -105,7 +105,7 @@ uint32_t tile_columns(uint32_t log_l) {
     return g;
 }
 
-bool split_2d_columns(uint32_t log_n) { return log_n > 10; }
+bool split_2d_columns(uint32_t log_rows) { return log_rows > 10; }
 
 namespace {
 
@@ -178,14 +178,14 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
                 "], got " + std::to_string(log_n));
     if (batch == 0) invalid("batch must be positive");
     if (log_n <= kMaxLogNSingle) {
-        std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::Stockham1D, log_n, batch));
+        std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::Stockham1D, log_n, 0, batch));
         p->add_stockham(mod, log_n, batch, Buf::In, Buf::Out);
         p->main_kernel_ = p->steps_[0].name;
         return p;
     }
 
     // N = N_1 * ... * N_P, digit 1 slowest; S_i = stride of digit i.
-    std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::MultiPass1D, log_n, batch));
+    std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::MultiPass1D, log_n, 0, batch));
     const std::vector<uint32_t> logs = split_1d(log_n);
     const size_t P = logs.size();
     const uint64_t N = 1ull << log_n;
@@ -245,67 +245,89 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
     return p;
 }
 
-std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_n,
-                                          size_t batch) {
-    if (log_n < kMinLogN2D || log_n > kMaxLogN2D)
-        invalid("2D requires log_n in [" + std::to_string(kMinLogN2D) + ", " + std::to_string(kMaxLogN2D) +
-                "]; got " + std::to_string(log_n));
+std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_rows,
+                                          uint32_t log_cols, size_t batch) {
+    for (uint32_t l : {log_rows, log_cols})
+        if (l < kMinLogN2D || l > kMaxLogN2D)
+            invalid("2D requires log_n in [" + std::to_string(kMinLogN2D) + ", " + std::to_string(kMaxLogN2D) +
+                    "]; got " + std::to_string(l));
     if (batch == 0) invalid("batch must be positive");
-    std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::TwoD, log_n, batch));
-    const uint64_t N = 1ull << log_n, NN = N * N;
-    const bool split = split_2d_columns(log_n);  // a 2048/4096-point column tile would leave < 16 columns
-    if (split) p->work_ = dev.alloc<Cf32>(NN * batch);
-    // Row pass (the reference's K1 row FFT, py lib.rs:325-336): N*batch rows.
-    p->add_stockham(mod, log_n, N * batch, Buf::In, split ? Buf::Work : Buf::Out);
+    std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::TwoD, log_cols, log_rows, batch));
+    const uint64_t R = 1ull << log_rows, C = 1ull << log_cols, RC = R * C;
+    const bool split = split_2d_columns(log_rows);
+    if (split) p->work_ = dev.alloc<Cf32>(RC * batch);
+    // Row pass (the reference's K1 row FFT, py lib.rs:325-336): R*batch rows of C.
+    p->add_stockham(mod, log_cols, R * batch, Buf::In, split ? Buf::Work : Buf::Out);
     if (!split) {
-        // Column pass, in place: G adjacent columns of length N per tile.
-        const uint32_t g = (uint32_t)std::min<uint64_t>(tile_columns(log_n), N);
+        // Column pass, in place: G adjacent columns of length R per tile.
+        const uint32_t g = (uint32_t)std::min<uint64_t>(tile_columns(log_rows), C);
         TileGeom t{};
-        t.t0n = (uint32_t)(N / g);
+        t.t0n = (uint32_t)(C / g);
         t.t1n = 1;
         t.is0 = t.os0 = g;
         t.is1 = t.os1 = 0;
-        t.is2 = t.os2 = NN;
+        t.is2 = t.os2 = RC;
         t.ics = t.ocs = 1;
-        t.ies = t.oes = N;
-        p->add_tile(mod, log_n, g, false, t, (uint64_t)t.t0n * batch, Buf::Out, Buf::Out);
+        t.ies = t.oes = C;
+        p->add_tile(mod, log_rows, g, false, t, (uint64_t)t.t0n * batch, Buf::Out, Buf::Out);
     } else {
-        // Column FFT of length N = C_1 * C_2 over the slow axis, as two
-        // column passes with 64 adjacent columns per tile.
-        const uint32_t l1 = log_n - log_n / 2, l2 = log_n / 2;
-        const uint64_t C1 = 1ull << l1, C2 = 1ull << l2;
-        const uint32_t g = 64;
+        // Column FFT of length R = R_1 * R_2 over the slow axis, as two column
+        // passes over G = min(64, C) adjacent columns.
+        const uint32_t l1 = log_rows - log_rows / 2, l2 = log_rows / 2;
+        const uint64_t R1 = 1ull << l1, R2 = 1ull << l2;
+        const uint32_t g = (uint32_t)std::min<uint64_t>(64, C);
         TileGeom a{};
-        a.t0n = (uint32_t)(N / g);
-        a.t1n = (uint32_t)C2;
+        a.t0n = (uint32_t)(C / g);
+        a.t1n = (uint32_t)R2;
         a.is0 = a.os0 = g;
-        a.is1 = a.os1 = N;
-        a.is2 = a.os2 = NN;
+        a.is1 = a.os1 = C;
+        a.is2 = a.os2 = RC;
         a.ics = a.ocs = 1;
-        a.ies = a.oes = C2 * N;
+        a.ies = a.oes = R2 * C;
         a.twc = 0;
         a.tw0 = 0;
         a.tw1 = 1;
-        a.log_m = log_n;
+        a.log_m = log_rows;
         p->big_table();
         p->add_tile(mod, l1, g, false, a, (uint64_t)a.t0n * a.t1n * batch, Buf::Work, Buf::Work);
         TileGeom b{};
-        b.t0n = (uint32_t)(N / g);
-        b.t1n = (uint32_t)C1;
+        b.t0n = (uint32_t)(C / g);
+        b.t1n = (uint32_t)R1;
         b.is0 = g;
-        b.is1 = C2 * N;
-        b.is2 = NN;
+        b.is1 = R2 * C;
+        b.is2 = RC;
         b.ics = 1;
-        b.ies = N;
+        b.ies = C;
         b.os0 = g;
-        b.os1 = N;
-        b.os2 = NN;
+        b.os1 = C;
+        b.os2 = RC;
         b.ocs = 1;
-        b.oes = C1 * N;
+        b.oes = R1 * C;
         p->add_tile(mod, l2, g, false, b, (uint64_t)b.t0n * b.t1n * batch, Buf::Work, Buf::Out);
     }
     p->main_kernel_ = p->steps_.back().name;
     return p;
+}
+
+void transpose_c64(HipDevice& dev, const HipBackend::Module& mod, const void* in, void* out, uint32_t rows,
+                   uint32_t cols, size_t batch, hipStream_t stream) {
+    if (!in || !out) invalid("transpose: null buffer");
+    if (in == out) invalid("transpose: in and out must not alias");
+    if (rows == 0 || cols == 0 || batch == 0) invalid("transpose: rows, cols and batch must be positive");
+    const uint32_t tc = (cols + 63) / 64, tr = (rows + 63) / 64;
+    const uint64_t tiles = (uint64_t)tc * tr * batch;
+    if (tiles > 0x7fffffffull) invalid("transpose: too many tiles for one launch");
+    static thread_local const void* cached_mod = nullptr;
+    static thread_local HipBackend::KernelHandle k = nullptr;
+    if (!k || cached_mod != mod.get()) {
+        k = HipBackend::get_kernel(mod, "fg_transpose_c64");
+        cached_mod = mod.get();
+    }
+    const void* src = in;
+    void* dst = out;
+    uint32_t r = rows, c = cols, a = tc, b = tr;
+    void* args[] = {(void*)&src, &dst, &r, &c, &a, &b};
+    HipBackend::launch(dev.handle(), stream, k, Dim3((uint32_t)tiles), Dim3(256), 0, args);
 }
 
 std::vector<std::string> FftPlan::kernel_names() const {
@@ -318,8 +340,9 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
                    hipEvent_t* events) const {
     if (!in || !out) invalid("fft exec: null buffer");
     const bool inverse = dir == Direction::Inverse;
+    // 1/N (1D, plan.rs semantics) or 1/(rows*cols) (2D, cpu_2d.rs:55-61): powers of two, exact.
     const float scale = (inverse && normalize)
-                            ? (kind_ == Kind::TwoD ? 1.0f / ((float)(1u << log_n_) * (float)(1u << log_n_))
+                            ? (kind_ == Kind::TwoD ? 1.0f / ((float)(1u << log_rows_) * (float)(1u << log_n_))
                                                    : 1.0f / (float)(1ull << log_n_))
                             : 1.0f;
     const void* big = big_.data();

@@ -43,8 +43,10 @@ public:
 
     static std::unique_ptr<FftPlan> make_1d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_n,
                                             size_t batch);
-    static std::unique_ptr<FftPlan> make_2d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_n,
-                                            size_t batch);
+    // 2D plan for `batch` row-major images of 2^log_rows x 2^log_cols (the
+    // reference's Plan2D is the square case, log_rows == log_cols).
+    static std::unique_ptr<FftPlan> make_2d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_rows,
+                                            uint32_t log_cols, size_t batch);
 
     // Forward or inverse transform of batch transforms from in to out (may alias).
     // With `events` (launches() of them), events[i] is recorded on the stream
@@ -53,10 +55,12 @@ public:
               hipEvent_t* events = nullptr) const;
 
     Kind kind() const { return kind_; }
+    // 1D: log2 of the length; 2D: log2 of the row length (columns).
     uint32_t log_n() const { return log_n_; }
+    uint32_t log_rows() const { return log_rows_; }
     size_t batch() const { return batch_; }
     // Complex elements per transform (N, or N*N for 2D).
-    size_t elems() const { return kind_ == Kind::TwoD ? (size_t(1) << (2 * log_n_)) : (size_t(1) << log_n_); }
+    size_t elems() const { return size_t(1) << (log_n_ + log_rows_); }
     int launches() const { return (int)steps_.size(); }
     const std::string& main_kernel() const { return main_kernel_; }
     size_t workspace_bytes() const { return work_.bytes(); }
@@ -78,8 +82,8 @@ private:
         TileGeom geom{};                        // tile: addressing (flags/scale set at exec)
     };
 
-    FftPlan(HipDevice& dev, Kind kind, uint32_t log_n, size_t batch)
-        : dev_(&dev), kind_(kind), log_n_(log_n), batch_(batch) {}
+    FftPlan(HipDevice& dev, Kind kind, uint32_t log_n, uint32_t log_rows, size_t batch)
+        : dev_(&dev), kind_(kind), log_n_(log_n), log_rows_(log_rows), batch_(batch) {}
 
     // Stage table for a length-2^log_l Stockham transform (uploaded once per plan).
     const void* stage_table(uint32_t log_l);
@@ -91,6 +95,7 @@ private:
     HipDevice* dev_;
     Kind kind_;
     uint32_t log_n_;
+    uint32_t log_rows_;  // 0 for 1D
     size_t batch_;
     std::vector<Step> steps_;
     std::vector<std::pair<uint32_t, Buffer<Cf32, HipBackend>>> stage_tables_;
@@ -111,7 +116,10 @@ std::vector<Cf32> big_twiddles();
 std::vector<uint32_t> split_1d(uint32_t log_n);
 // Columns per tile for a pass of length 2^log_l.
 uint32_t tile_columns(uint32_t log_l);
-// Whether the column FFT of an N x N image (N = 2^log_n) runs as two passes.
-bool split_2d_columns(uint32_t log_n);
+// Whether the column FFT of an image with 2^log_rows rows runs as two passes.
+bool split_2d_columns(uint32_t log_rows);
+// Launch the tiled transpose out[b][c][r] = in[b][r][c] on `stream`.
+void transpose_c64(HipDevice& dev, const HipBackend::Module& mod, const void* in, void* out, uint32_t rows,
+                   uint32_t cols, size_t batch, hipStream_t stream);
 
 }  // namespace fg

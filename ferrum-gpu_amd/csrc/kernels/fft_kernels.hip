@@ -50,6 +50,39 @@ extern "C" __global__ __launch_bounds__(64) void fg_copy_f4(const float4* __rest
     for (; i < n4; i += stride) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
+// out[b][c][r] = in[b][r][c] for `batch` rows x cols complex64 matrices: the
+// tiled transpose of the reference's 2D path (transpose_complex_pow2,
+// crates/ferrum-gpu-fft-kernels/src/kernels_body.rs:763-805), here as a
+// standalone operation on any shape.  64 x 64 tiles through LDS (pitch 65:
+// the transposed reads of a wave hit distinct banks); both the global reads
+// and writes are 64 lanes x 8 contiguous bytes.  tiles_c = ceil(cols / 64),
+// tiles_r = ceil(rows / 64); grid = tiles_c * tiles_r * batch.
+extern "C" __global__ __launch_bounds__(256) void fg_transpose_c64(const float2* __restrict__ in,
+                                                                   float2* __restrict__ out, uint32_t rows,
+                                                                   uint32_t cols, uint32_t tiles_c,
+                                                                   uint32_t tiles_r) {
+    __shared__ float2 tile[64][65];
+    uint32_t bx = blockIdx.x;
+    const uint32_t tc = bx % tiles_c;
+    bx /= tiles_c;
+    const uint32_t tr = bx % tiles_r;
+    const uint64_t img = (uint64_t)(bx / tiles_r) * rows * cols;
+    const uint32_t tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const uint32_t c = tc * 64 + tx;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t r = tr * 64 + ty + 4 * i;
+        if (r < rows && c < cols) tile[ty + 4 * i][tx] = load_stream(in + img + (uint64_t)r * cols + c);
+    }
+    __syncthreads();
+    const uint32_t orow_col = tr * 64 + tx;  // output column = input row
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t orow = tc * 64 + ty + 4 * i;  // output row = input column
+        if (orow < cols && orow_col < rows) store_stream(out + img + (uint64_t)orow * rows + orow_col, tile[tx][ty + 4 * i]);
+    }
+}
+
 // c = a + b over n floats: the substrate smoke kernel (the reference's
 // hand-written vector_add, examples/vector-add/src/main.rs:17-60).
 extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __restrict__ a,
@@ -76,16 +109,26 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
         fft_tile_body<LOGL, (LOGL < 4 ? LOGL : 4), G, RW, true>(in, out, tw, big, g);                \
     }
 
-// Column passes (1D digits of 128..1024 points, 2D columns of 16..1024 and
-// the 2048/4096 column splits) and row passes (last 1D digit).
+// Column passes: 1D digits of 128..1024 points (G = 64/32/16 by length), and
+// 2D column FFTs of 16..1024 points (or the 2048/4096 splits into 64 x 32 and
+// 64 x 64) over G = min(that width, image columns) adjacent columns.
 FG_TILE(4, 16, false, c)
+FG_TILE(4, 32, false, c)
+FG_TILE(4, 64, false, c)
+FG_TILE(5, 16, false, c)
 FG_TILE(5, 32, false, c)
 FG_TILE(5, 64, false, c)
+FG_TILE(6, 16, false, c)
+FG_TILE(6, 32, false, c)
 FG_TILE(6, 64, false, c)
+FG_TILE(7, 16, false, c)
+FG_TILE(7, 32, false, c)
 FG_TILE(7, 64, false, c)
+FG_TILE(8, 16, false, c)
 FG_TILE(8, 32, false, c)
 FG_TILE(9, 16, false, c)
 FG_TILE(10, 16, false, c)
+// Row passes (last 1D digit: rows contiguous, transposed store).
 FG_TILE(6, 64, true, r)
 FG_TILE(7, 64, true, r)
 FG_TILE(8, 32, true, r)

@@ -109,6 +109,9 @@ _sig("fg_fft_plan_kernel", _vp, _i, ctypes.c_char_p, _sz)
 _sig("fg_fft_1d_c2c_pow2_host", _vp, _vp, _vp, _sz, _u32, _i, _i)
 _sig("fg_fft_2d_c2c_pow2_host", _vp, _vp, _vp, _u32, _sz, _i, _i)
 _sig("fg_stream_copy", _vp, _vp, _vp, _sz, _vp)
+_sig("fg_fft_plan_2d_rect", _vp, _u32, _u32, _sz, _P(_vp))
+_sig("fg_fft_2d_rect_host", _vp, _vp, _vp, _u32, _u32, _sz, _i, _i)
+_sig("fg_transpose_c64", _vp, _vp, _vp, _u32, _u32, _sz, _vp)
 
 
 def last_error() -> str:

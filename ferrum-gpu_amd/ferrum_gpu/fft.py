@@ -19,8 +19,8 @@ import numpy as np
 from ferrum_gpu import _native as _n
 from ferrum_gpu.hip import Device, DeviceBuffer
 
-__all__ = ["fft_1d_c2c_pow2", "fft_2d_c2c_pow2", "Plan1D", "Plan2D", "MIN_LOG_N", "MAX_LOG_N",
-           "MIN_LOG_N_2D", "MAX_LOG_N_2D"]
+__all__ = ["fft_1d_c2c_pow2", "fft_2d_c2c_pow2", "fft2_c2c_pow2", "Plan1D", "Plan2D", "transpose",
+           "MIN_LOG_N", "MAX_LOG_N", "MIN_LOG_N_2D", "MAX_LOG_N_2D"]
 
 MIN_LOG_N, MAX_LOG_N = 2, 24
 MIN_LOG_N_2D, MAX_LOG_N_2D = 4, 12
@@ -191,10 +191,49 @@ class Plan1D(_Plan):
 
 
 class Plan2D(_Plan):
-    """Plan for ``batch`` N x N images, N = ``2**log_n`` (Plan2D::new, plan.rs:111-119)."""
+    """Plan for ``batch`` N x N images, N = ``2**log_n`` (Plan2D::new, plan.rs:111-119).
 
-    def __init__(self, log_n: int, batch: int, device: Device):
+    With ``log_cols`` the images are ``2**log_n`` rows x ``2**log_cols`` columns.
+    """
+
+    def __init__(self, log_n: int, batch: int, device: Device, log_cols: int | None = None):
         p = ctypes.c_void_p()
-        _n.check(_n.lib.fg_fft_plan_2d(device.handle, int(log_n), int(batch), ctypes.byref(p)))
-        super().__init__(device, p, 1 << (2 * int(log_n)), int(batch))
-        self.log_n = int(log_n)
+        log_rows = int(log_n)
+        log_c = log_rows if log_cols is None else int(log_cols)
+        if log_cols is None:
+            _n.check(_n.lib.fg_fft_plan_2d(device.handle, log_rows, int(batch), ctypes.byref(p)))
+        else:
+            _n.check(_n.lib.fg_fft_plan_2d_rect(device.handle, log_rows, log_c, int(batch), ctypes.byref(p)))
+        super().__init__(device, p, 1 << (log_rows + log_c), int(batch))
+        self.log_n = log_rows
+        self.log_cols = log_c
+
+
+def fft2_c2c_pow2(arr, direction="forward", normalize=False, device=None):
+    """2D FFT over the last two axes of a ``complex64`` array of shape
+    ``(..., 2**a, 2**b)`` (4 <= a, b <= 12), rows and columns of any
+    power-of-two lengths; ``normalize`` scales the inverse by 1/(rows*cols)."""
+    a = _complex64_array(arr, (2, 3, 4))
+    rows, cols = a.shape[-2], a.shape[-1]
+    lr, lc = rows.bit_length() - 1, cols.bit_length() - 1
+    if rows != 1 << lr or cols != 1 << lc or not (MIN_LOG_N_2D <= lr <= MAX_LOG_N_2D) \
+            or not (MIN_LOG_N_2D <= lc <= MAX_LOG_N_2D):
+        raise ValueError(f"arr shape {list(a.shape)}: the last two axes must be powers of two in "
+                         f"[2^{MIN_LOG_N_2D}, 2^{MAX_LOG_N_2D}]")
+    batch = a.size // (rows * cols)
+    if batch == 0:
+        raise ValueError(f"arr shape {list(a.shape)} holds no image")
+    d = _direction(direction)
+    out = np.empty_like(a)
+    rc = _n.lib.fg_fft_2d_rect_host(_device_handle(device), a.ctypes.data, out.ctypes.data, lr, lc, batch, d,
+                                    int(bool(normalize)))
+    if rc != _n.FG_OK:
+        raise ValueError(f"ferrum-gpu fft 2d error: {_n.last_error()}")
+    return out
+
+
+def transpose(device: Device, d_in, d_out, rows: int, cols: int, batch: int = 1, stream: int = 0) -> None:
+    """out[b][c][r] = in[b][r][c] for ``batch`` rows x cols complex64 matrices on
+    the device (stream-ordered; in and out must not alias)."""
+    _n.check(_n.lib.fg_transpose_c64(device.handle, _ptr(d_in), _ptr(d_out), int(rows), int(cols), int(batch),
+                                     ctypes.c_void_p(stream or None)))

@@ -175,6 +175,21 @@ FG_API int fg_fft_1d_c2c_pow2_host(fg_device_t dev, const float *in, float *out,
 FG_API int fg_fft_2d_c2c_pow2_host(fg_device_t dev, const float *in, float *out, uint32_t log_n,
                             size_t batch, int direction, int normalize);
 
+/* Non-square 2D (SURVEY's "general 2D", beyond Plan2D's square images,
+ * crates/ferrum-gpu-fft/src/plan.rs:98-135): `batch` row-major images of
+ * 2^log_rows x 2^log_cols, each log in [4, 12]; normalize scales the inverse
+ * by 1/(rows*cols). */
+FG_API int fg_fft_plan_2d_rect(fg_device_t dev, uint32_t log_rows, uint32_t log_cols, size_t batch,
+                               fg_fft_plan_t *out);
+FG_API int fg_fft_2d_rect_host(fg_device_t dev, const float *in, float *out, uint32_t log_rows,
+                               uint32_t log_cols, size_t batch, int direction, int normalize);
+/* Tiled transpose out[b][c][r] = in[b][r][c] of `batch` rows x cols complex64
+ * matrices on the device (the reference's transpose_complex_pow2 kernel,
+ * crates/ferrum-gpu-fft-kernels/src/kernels_body.rs:763-805, for any shape);
+ * in and out must not alias.  Stream-ordered, asynchronous. */
+FG_API int fg_transpose_c64(fg_device_t dev, const void *d_in, void *d_out, uint32_t rows, uint32_t cols,
+                            size_t batch, fg_stream_t stream);
+
 /* Streaming device copy of `bytes` (a multiple of 16) with the code object's
  * copy kernel: the HBM yardstick reported beside the FFT. */
 FG_API int fg_stream_copy(fg_device_t dev, const void *d_in, void *d_out, size_t bytes,

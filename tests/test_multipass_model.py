@@ -76,29 +76,31 @@ def tile_geometry_1d(log_n, batch):
     return passes
 
 
-def tile_geometry_2d(log_n, batch):
-    """Column FFT of each N x N image after the row pass, as FftPlan::make_2d builds it:
-    one pass while a tile still spans >= 16 columns, else N = C_1 * C_2 in two."""
-    N = 1 << log_n
+def tile_geometry_2d(log_n, batch, log_cols=None):
+    """Column FFT of each R x C image after the row pass, as FftPlan::make_2d builds it
+    (R = 2^log_n rows, C = 2^log_cols columns, square by default): one pass up to
+    1024 rows, else R = R_1 * R_2 in two passes over min(64, C) columns."""
+    R = 1 << log_n
+    C = R if log_cols is None else 1 << log_cols
     if log_n <= 10:                   # split_2d_columns in fft_plan.cpp
-        g = min(tile_columns(log_n), N)
-        return [dict(log_l=log_n, g=g, rowwise=False, t0n=N // g, t1n=1,
-                     is0=g, is1=0, is2=N * N, ics=1, ies=N,
-                     os0=g, os1=0, os2=N * N, ocs=1, oes=N,
+        g = min(tile_columns(log_n), C)
+        return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
+                     is0=g, is1=0, is2=R * C, ics=1, ies=C,
+                     os0=g, os1=0, os2=R * C, ocs=1, oes=C,
                      twc=0, tw0=0, tw1=0, log_m=0)]
     l1 = log_n - log_n // 2
     l2 = log_n // 2
-    C1, C2 = 1 << l1, 1 << l2
-    g = 64
-    # pass 1: DFT over the slow row digit n_hi (rows n_lo + C2*n_hi) for each (n_lo, column)
-    p1 = dict(log_l=l1, g=g, rowwise=False, t0n=N // g, t1n=C2,
-              is0=g, is1=N, is2=N * N, ics=1, ies=C2 * N,
-              os0=g, os1=N, os2=N * N, ocs=1, oes=C2 * N,
+    R1, R2 = 1 << l1, 1 << l2
+    g = min(64, C)
+    # pass 1: DFT over the slow row digit n_hi (rows n_lo + R2*n_hi) for each (n_lo, column)
+    p1 = dict(log_l=l1, g=g, rowwise=False, t0n=C // g, t1n=R2,
+              is0=g, is1=C, is2=R * C, ics=1, ies=R2 * C,
+              os0=g, os1=C, os2=R * C, ocs=1, oes=R2 * C,
               twc=0, tw0=0, tw1=1, log_m=log_n)
-    # pass 2: DFT over n_lo (rows C2*k_hi + n_lo) for each (k_hi, column); output row k_hi + C1*k_lo
-    p2 = dict(log_l=l2, g=g, rowwise=False, t0n=N // g, t1n=C1,
-              is0=g, is1=C2 * N, is2=N * N, ics=1, ies=N,
-              os0=g, os1=N, os2=N * N, ocs=1, oes=C1 * N,
+    # pass 2: DFT over n_lo (rows R2*k_hi + n_lo) for each (k_hi, column); output row k_hi + R1*k_lo
+    p2 = dict(log_l=l2, g=g, rowwise=False, t0n=C // g, t1n=R1,
+              is0=g, is1=R2 * C, is2=R * C, ics=1, ies=C,
+              os0=g, os1=C, os2=R * C, ocs=1, oes=R1 * C,
               twc=0, tw0=0, tw1=0, log_m=0)
     return [p1, p2]
 
@@ -164,6 +166,16 @@ def test_2d_column_passes_match_oracle(log_n):
     rows = np.fft.fft(x.astype(np.complex128), axis=2).reshape(-1)
     got = run_geometry(rows, tile_geometry_2d(log_n, batch), batch, n * n).reshape(batch, n, n)
     assert rel_l2(got, oracle.fft_2d(x, log_n)) < 1e-5
+
+
+@pytest.mark.parametrize("lr,lc", [(4, 9), (9, 4), (6, 12), (11, 4), (11, 6), (5, 7)])
+def test_2d_rectangular_column_passes(lr, lc):
+    rng = np.random.default_rng(lr * 13 + lc)
+    R, C = 1 << lr, 1 << lc
+    x = uniform_c64(rng, R * C).reshape(1, R, C)
+    rows = np.fft.fft(x.astype(np.complex128), axis=2).reshape(-1)
+    got = run_geometry(rows, tile_geometry_2d(lr, 1, lc), 1, R * C).reshape(1, R, C)
+    assert rel_l2(got, np.fft.fft2(x.astype(np.complex128))) < 1e-5
 
 
 def test_split_sizes_fit_the_tile_kernel():

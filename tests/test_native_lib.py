@@ -68,9 +68,10 @@ def planned_kernels():
     for log_n in range(13, 25):
         for p in tile_geometry_1d(log_n, 1):
             names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}")
-    for log_n in range(4, 13):
-        for p in tile_geometry_2d(log_n, 1):
-            names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}")
+    for lr in range(4, 13):
+        for lc in range(4, 13):
+            for p in tile_geometry_2d(lr, 1, lc):
+                names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}")
     return names
 
 
