@@ -33,6 +33,7 @@ struct fg_device {
     // key: (dims, log_n or log_cols, log_rows (0 for 1D), batch)
     std::map<std::tuple<int, uint32_t, uint32_t, size_t>, std::unique_ptr<FftPlan>> plans;
     Buffer<Cf32, HipBackend> staging;
+    fg::Pointwise pointwise;  // elementwise kernels of fft_module
 };
 
 struct fg_module {
@@ -90,6 +91,7 @@ fg_device* open_device(int ordinal) {
     std::unique_ptr<fg_device> d(new fg_device);
     d->dev.reset(new HipDevice(h));
     d->fft_module = d->dev->load_or_cache(fg::fft_code_object());
+    d->pointwise = fg::Pointwise(d->fft_module);
     return d.release();
 }
 
@@ -435,6 +437,15 @@ int fg_fft_exec(fg_fft_plan_t plan, const void* d_in, void* d_out, int direction
     });
 }
 
+int fg_fft_exec_split(fg_fft_plan_t plan, const void* d_in_re, const void* d_in_im, void* d_out_re,
+                      void* d_out_im, int direction, int normalize, fg_stream_t stream) {
+    return guarded([&] {
+        need(plan, "plan");
+        plan->plan->exec_split(d_in_re, d_in_im, d_out_re, d_out_im, parse_dir(direction), normalize != 0,
+                               (hipStream_t)stream);
+    });
+}
+
 int fg_fft_exec_events(fg_fft_plan_t plan, const void* d_in, void* d_out, int direction, int normalize,
                        fg_stream_t stream, fg_event_t* events, int nevents) {
     return guarded([&] {
@@ -552,6 +563,35 @@ int fg_transpose_c64(fg_device_t dev, const void* d_in, void* d_out, uint32_t ro
     return guarded([&] {
         need(dev, "device");
         fg::transpose_c64(*dev->dev, dev->fft_module, d_in, d_out, rows, cols, batch, (hipStream_t)stream);
+    });
+}
+
+int fg_cmul_c64(fg_device_t dev, const void* a, const void* b, void* out, size_t n, fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        dev->pointwise.cmul_c64(dev->dev->handle(), a, b, out, n, (hipStream_t)stream);
+    });
+}
+
+int fg_cmul_split(fg_device_t dev, const void* a_re, const void* a_im, const void* b_re, const void* b_im,
+                  void* o_re, void* o_im, size_t n, fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        dev->pointwise.cmul_split(dev->dev->handle(), a_re, a_im, b_re, b_im, o_re, o_im, n, (hipStream_t)stream);
+    });
+}
+
+int fg_deinterleave_c64(fg_device_t dev, const void* in, void* re, void* im, size_t n, fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        dev->pointwise.deinterleave(dev->dev->handle(), in, re, im, n, (hipStream_t)stream);
+    });
+}
+
+int fg_interleave_c64(fg_device_t dev, const void* re, const void* im, void* out, size_t n, fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        dev->pointwise.interleave(dev->dev->handle(), re, im, out, n, (hipStream_t)stream);
     });
 }
 

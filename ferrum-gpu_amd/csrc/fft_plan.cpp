@@ -181,6 +181,8 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::Stockham1D, log_n, 0, batch));
         p->add_stockham(mod, log_n, batch, Buf::In, Buf::Out);
         p->main_kernel_ = p->steps_[0].name;
+        p->split_fn_ = HipBackend::get_kernel(mod, (p->main_kernel_ + "_split").c_str());
+        p->pw_ = Pointwise(mod);
         return p;
     }
 
@@ -242,6 +244,7 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         p->add_tile(mod, log_l, g, true, t, (uint64_t)t.t0n * t.t1n * batch, Buf::Work, Buf::Out);
     }
     p->main_kernel_ = p->steps_[0].name;
+    p->pw_ = Pointwise(mod);
     return p;
 }
 
@@ -306,6 +309,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         p->add_tile(mod, l2, g, false, b, (uint64_t)b.t0n * b.t1n * batch, Buf::Work, Buf::Out);
     }
     p->main_kernel_ = p->steps_.back().name;
+    p->pw_ = Pointwise(mod);
     return p;
 }
 
@@ -336,15 +340,18 @@ std::vector<std::string> FftPlan::kernel_names() const {
     return v;
 }
 
+float FftPlan::scale_for(Direction dir, bool normalize) const {
+    // 1/N (1D, plan.rs semantics) or 1/(rows*cols) (2D, cpu_2d.rs:55-61): powers of two, exact.
+    if (dir != Direction::Inverse || !normalize) return 1.0f;
+    return kind_ == Kind::TwoD ? 1.0f / ((float)(1u << log_rows_) * (float)(1u << log_n_))
+                               : 1.0f / (float)(1ull << log_n_);
+}
+
 void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
                    hipEvent_t* events) const {
     if (!in || !out) invalid("fft exec: null buffer");
     const bool inverse = dir == Direction::Inverse;
-    // 1/N (1D, plan.rs semantics) or 1/(rows*cols) (2D, cpu_2d.rs:55-61): powers of two, exact.
-    const float scale = (inverse && normalize)
-                            ? (kind_ == Kind::TwoD ? 1.0f / ((float)(1u << log_rows_) * (float)(1u << log_n_))
-                                                   : 1.0f / (float)(1ull << log_n_))
-                            : 1.0f;
+    const float scale = scale_for(dir, normalize);
     const void* big = big_.data();
     hipStream_t st = stream ? stream : dev_->default_stream();
     for (size_t i = 0; i < steps_.size(); ++i) {
@@ -376,6 +383,38 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
         }
         if (events) hip_check(hipEventRecord(events[i], st), "hipEventRecord");
     }
+}
+
+void FftPlan::exec_split(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
+                         bool normalize, hipStream_t stream) const {
+    if (!in_re || !in_im || !out_re || !out_im) invalid("fft exec_split: null buffer");
+    const uint64_t n = (uint64_t)elems() * batch_, nb = 4 * n;
+    auto overlap = [nb](const void* a, const void* b) {
+        const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+        return x < y + nb && y < x + nb;
+    };
+    // Each part is either the same array as its input counterpart or disjoint
+    // from every other array.
+    if (overlap(out_re, out_im) || overlap(out_re, in_im) || overlap(out_im, in_re) ||
+        (out_re != in_re && overlap(out_re, in_re)) || (out_im != in_im && overlap(out_im, in_im)))
+        invalid("fft exec_split: overlapping buffers (only out_re == in_re and out_im == in_im may alias)");
+    if (split_fn_) {
+        const Step& s = steps_[0];
+        uint32_t flags = dir == Direction::Inverse ? (FG_PASS_CONJ_IN | FG_PASS_CONJ_SCALE_OUT) : 0u;
+        float sc = scale_for(dir, normalize);
+        const void* tw = s.tw;
+        uint64_t count = s.count;
+        void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, &count, &sc, &flags};
+        HipBackend::launch(dev_->handle(), stream, split_fn_, s.grid, s.block, 0, args);
+        return;
+    }
+    {
+        std::lock_guard<std::mutex> lock(stage_mu_);
+        if (!stage_.data()) stage_ = dev_->alloc<Cf32>(n);
+    }
+    pw_.interleave(dev_->handle(), in_re, in_im, stage_.data(), n, stream);
+    exec(stage_.data(), stage_.data(), dir, normalize, stream);
+    pw_.deinterleave(dev_->handle(), stage_.data(), out_re, out_im, n, stream);
 }
 
 }  // namespace fg

@@ -9,12 +9,14 @@
 #pragma once
 
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "device.hpp"
 #include "hip_backend.hpp"
 #include "kernels/tile_geom.h"
+#include "pointwise_ops.hpp"
 
 namespace fg {
 
@@ -53,6 +55,16 @@ public:
     // right after launch i.
     void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
               hipEvent_t* events = nullptr) const;
+    // exec() on the split layout: real and imaginary parts in separate f32
+    // arrays of batch * elems() each (the reference's *_split kernels,
+    // kernels_body.rs:509-626).  Single-pass plans read and write the split
+    // arrays in their one launch; other plans interleave into a staging buffer
+    // (allocated at their first split call), run in place there and
+    // deinterleave.  out_re/out_im may be in_re/in_im (in place).
+    void exec_split(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
+                    bool normalize, hipStream_t stream) const;
+    // Launches exec_split makes: 1 for single-pass plans, launches() + 2 otherwise.
+    int split_launches() const { return split_fn_ ? 1 : launches() + 2; }
 
     Kind kind() const { return kind_; }
     // 1D: log2 of the length; 2D: log2 of the row length (columns).
@@ -86,6 +98,7 @@ private:
         : dev_(&dev), kind_(kind), log_n_(log_n), log_rows_(log_rows), batch_(batch) {}
 
     // Stage table for a length-2^log_l Stockham transform (uploaded once per plan).
+    float scale_for(Direction dir, bool normalize) const;
     const void* stage_table(uint32_t log_l);
     const void* big_table();
     void add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t count, Buf src, Buf dst);
@@ -102,6 +115,10 @@ private:
     Buffer<Cf32, HipBackend> big_;
     Buffer<Cf32, HipBackend> work_;
     std::string main_kernel_;
+    HipBackend::KernelHandle split_fn_ = nullptr;  // single-pass plans: the split-layout kernel
+    Pointwise pw_;
+    mutable std::mutex stage_mu_;                   // guards the lazy allocation of stage_
+    mutable Buffer<Cf32, HipBackend> stage_;        // split layout staging of multi-launch plans
 };
 
 // ---- host-side pieces exposed for the CPU tests of the plan logic ----------

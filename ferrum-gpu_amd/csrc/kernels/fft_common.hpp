@@ -134,6 +134,32 @@ __device__ __forceinline__ void store_stream(float2* p, float2 a) {
     fg_v2f v = {a.x, a.y};
     __builtin_nontemporal_store(v, reinterpret_cast<fg_v2f*>(p));
 }
+__device__ __forceinline__ float load_stream(const float* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void store_stream(float* p, float a) { __builtin_nontemporal_store(a, p); }
+
+// Global layouts of transform data.  Element i of the flat batch (transform f,
+// position p: i = f * N + p) is in[i] in the interleaved complex64 layout (the
+// reference's Complex32 arrays), or (re[i], im[i]) in the split layout: two f32
+// arrays, the reference's SoA kernels (kernels_body.rs:509-626).
+struct InterleavedIO {
+    const float2* in;
+    float2* out;
+    __device__ __forceinline__ float2 load(uint64_t i) const { return load_stream(in + i); }
+    __device__ __forceinline__ void store(uint64_t i, float2 v) const { store_stream(out + i, v); }
+};
+struct SplitIO {
+    const float* in_re;
+    const float* in_im;
+    float* out_re;
+    float* out_im;
+    __device__ __forceinline__ float2 load(uint64_t i) const {
+        return make_float2(load_stream(in_re + i), load_stream(in_im + i));
+    }
+    __device__ __forceinline__ void store(uint64_t i, float2 v) const {
+        store_stream(out_re + i, v.x);
+        store_stream(out_im + i, v.y);
+    }
+};
 
 // Wave-scope ordering of LDS traffic: a wave's LDS operations execute in
 // program order, so a compiler-level barrier plus wavefront-scope fences is

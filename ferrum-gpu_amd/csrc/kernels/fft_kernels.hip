@@ -12,13 +12,23 @@ using namespace fg;
 
 // Launch geometry is fixed per kernel and mirrored on the host in
 // fft_plan.cpp (kStockhamTable): LOGE = min(4, LOGN); FPB transforms per
-// workgroup of FPB * (N / E) threads.
-#define FG_STOCKHAM(LOGN, LOGE, FPB)                                                        \
-    extern "C" __global__ __launch_bounds__(FPB * ((1 << LOGN) >> LOGE)) void                \
-        fg_fft_n##LOGN(const float2* __restrict__ in, float2* __restrict__ out,              \
-                       const float2* __restrict__ tw, uint64_t batch, float scale,          \
-                       uint32_t flags) {                                                    \
-        fft_stockham_body<LOGN, LOGE, FPB>(in, out, tw, batch, scale, flags);               \
+// workgroup of FPB * (N / E) threads.  fg_fft_n<L> reads and writes
+// interleaved complex64; fg_fft_n<L>_split the split layout (re and im arrays,
+// the reference's *_split kernels K4/K8/K11), with the same arithmetic.
+#define FG_STOCKHAM(LOGN, LOGE, FPB)                                                          \
+    extern "C" __global__ __launch_bounds__(FPB * ((1 << LOGN) >> LOGE)) void                  \
+        fg_fft_n##LOGN(const float2* __restrict__ in, float2* __restrict__ out,                \
+                       const float2* __restrict__ tw, uint64_t batch, float scale,            \
+                       uint32_t flags) {                                                      \
+        fft_stockham_body<LOGN, LOGE, FPB>(InterleavedIO{in, out}, tw, batch, scale, flags);  \
+    }                                                                                         \
+    extern "C" __global__ __launch_bounds__(FPB * ((1 << LOGN) >> LOGE)) void                  \
+        fg_fft_n##LOGN##_split(const float* __restrict__ in_re, const float* __restrict__ in_im, \
+                               float* __restrict__ out_re, float* __restrict__ out_im,          \
+                               const float2* __restrict__ tw, uint64_t batch, float scale,    \
+                               uint32_t flags) {                                              \
+        fft_stockham_body<LOGN, LOGE, FPB>(SplitIO{in_re, in_im, out_re, out_im}, tw, batch,  \
+                                           scale, flags);                                     \
     }
 
 FG_STOCKHAM(2, 2, 64)    // N=4:    1 thread  / transform, 64 per wave
@@ -134,3 +144,32 @@ FG_TILE(7, 64, true, r)
 FG_TILE(8, 32, true, r)
 FG_TILE(9, 16, true, r)
 FG_TILE(10, 16, true, r)
+
+// ------------------------------------------------------------- pointwise
+//
+// fg_<op>_v4: four elements per thread step with 16-byte accesses (every
+// pointer 16-byte aligned); fg_<op>_v1: one element, any alignment.  n is the
+// number of complex elements.  256-thread workgroups, grid-stride.
+#include "pointwise.hpp"
+
+#define FG_POINTWISE(W)                                                                               \
+    extern "C" __global__ __launch_bounds__(256) void fg_cmul_c64_v##W(                              \
+        const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out, uint64_t n) { \
+        cmul_c64_body<W>(a, b, out, n);                                                               \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(256) void fg_cmul_split_v##W(                            \
+        const float* __restrict__ a_re, const float* __restrict__ a_im, const float* __restrict__ b_re, \
+        const float* __restrict__ b_im, float* __restrict__ o_re, float* __restrict__ o_im, uint64_t n) { \
+        cmul_split_body<W>(a_re, a_im, b_re, b_im, o_re, o_im, n);                                    \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(256) void fg_deinterleave_c64_v##W(                      \
+        const float* __restrict__ in, float* __restrict__ re, float* __restrict__ im, uint64_t n) {   \
+        deinterleave_body<W>(in, re, im, n);                                                          \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(256) void fg_interleave_c64_v##W(                        \
+        const float* __restrict__ re, const float* __restrict__ im, float* __restrict__ out, uint64_t n) { \
+        interleave_body<W>(re, im, out, n);                                                           \
+    }
+
+FG_POINTWISE(4)
+FG_POINTWISE(1)

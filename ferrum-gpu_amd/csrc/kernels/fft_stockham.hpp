@@ -166,12 +166,11 @@ struct StockhamStages {
     }
 };
 
-// Kernel body: FPB transforms per workgroup of FPB*T threads.  flags take
-// FG_PASS_CONJ_IN / FG_PASS_CONJ_SCALE_OUT (tile_geom.h): the inverse is both.
-template <int LOGN, int LOGE, int FPB>
-__device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
-                                                  float2* __restrict__ out,
-                                                  const float2* __restrict__ tw,
+// Kernel body: FPB transforms per workgroup of FPB*T threads; IO is the global
+// layout (InterleavedIO or SplitIO).  flags take FG_PASS_CONJ_IN /
+// FG_PASS_CONJ_SCALE_OUT (tile_geom.h): the inverse is both.
+template <int LOGN, int LOGE, int FPB, class IO>
+__device__ __forceinline__ void fft_stockham_body(const IO io, const float2* __restrict__ tw,
                                                   uint64_t batch, float scale, uint32_t flags) {
     using Sh = StockhamShape<LOGN, LOGE>;
     constexpr bool ONE_WAVE = (Sh::T * FPB) <= 64;
@@ -197,7 +196,7 @@ __device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
             const int e = tid + BLOCK * j;  // element of the block's FPB*N
             const int fs = e >> LOGN;
             float2 v = make_float2(0.f, 0.f);
-            if (f0 + fs < batch) v = load_stream(in + f0 * Sh::N + e);
+            if (f0 + fs < batch) v = io.load(f0 * Sh::N + e);
             lds_all[fs][lds_pos(e & (Sh::N - 1))] = v;
         }
         if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
@@ -206,7 +205,7 @@ __device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
         if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
     } else if (valid) {
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = load_stream(in + f * Sh::N + t + Sh::T * m);
+        for (int m = 0; m < Sh::E; ++m) x[m] = io.load(f * Sh::N + t + Sh::T * m);
     } else {
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) x[m] = make_float2(0.f, 0.f);
@@ -229,14 +228,14 @@ __device__ __forceinline__ void fft_stockham_body(const float2* __restrict__ in,
         for (int j = 0; j < Sh::E; ++j) {
             const int e = tid + BLOCK * j;
             const int fs = e >> LOGN;
-            if (f0 + fs < batch) store_stream(out + f0 * Sh::N + e, lds_all[fs][lds_pos(e & (Sh::N - 1))]);
+            if (f0 + fs < batch) io.store(f0 * Sh::N + e, lds_all[fs][lds_pos(e & (Sh::N - 1))]);
         }
     } else if (valid) {
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) {
             float2 v = x[m];
             if (cs) v = cscale(cconj(v), scale);
-            store_stream(out + f * Sh::N + t + Sh::T * m, v);
+            io.store(f * Sh::N + t + Sh::T * m, v);
         }
     }
 }

@@ -1,0 +1,109 @@
+// pointwise_ops.cpp -- see pointwise_ops.hpp.
+#include "pointwise_ops.hpp"
+
+#include <initializer_list>
+#include <string>
+
+namespace fg {
+
+namespace {
+
+constexpr uint32_t kThreads = 256;
+constexpr uint64_t kMaxBlocks = 1u << 16;  // 16.8 M threads; the kernels stride over the rest
+
+bool aligned16(std::initializer_list<const void*> ps) {
+    for (const void* p : ps)
+        if (reinterpret_cast<uintptr_t>(p) & 15u) return false;
+    return true;
+}
+
+void need_ptrs(const char* op, std::initializer_list<const void*> ps) {
+    for (const void* p : ps)
+        if (!p) invalid(std::string(op) + ": null buffer");
+}
+
+// Input and output ranges of n complex (8n bytes) or n floats (4n bytes) must
+// be identical or disjoint where the kernel reads one array and writes another
+// with a different stride.
+bool overlap(const void* a, uint64_t abytes, const void* b, uint64_t bbytes) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + bbytes && y < x + abytes;
+}
+
+void launch(const HipBackend::DeviceHandle& dev, hipStream_t stream, HipBackend::KernelHandle k, uint64_t n,
+            int width, void** args) {
+    const uint64_t chunks = (n + width - 1) / width;
+    uint64_t blocks = (chunks + kThreads - 1) / kThreads;
+    if (blocks > kMaxBlocks) blocks = kMaxBlocks;
+    HipBackend::launch(dev, stream, k, Dim3((uint32_t)blocks), Dim3(kThreads), 0, args);
+}
+
+}  // namespace
+
+Pointwise::Pointwise(const HipBackend::Module& mod) {
+    for (int v = 0; v < 2; ++v) {
+        const std::string w = v ? "_v4" : "_v1";
+        cmul_c64_[v] = HipBackend::get_kernel(mod, ("fg_cmul_c64" + w).c_str());
+        cmul_split_[v] = HipBackend::get_kernel(mod, ("fg_cmul_split" + w).c_str());
+        deinterleave_[v] = HipBackend::get_kernel(mod, ("fg_deinterleave_c64" + w).c_str());
+        interleave_[v] = HipBackend::get_kernel(mod, ("fg_interleave_c64" + w).c_str());
+    }
+}
+
+void Pointwise::cmul_c64(const HipBackend::DeviceHandle& dev, const void* a, const void* b, void* out, uint64_t n,
+                         hipStream_t stream) const {
+    if (n == 0) return;
+    need_ptrs("cmul_c64", {a, b, out});
+    // Element i of out depends only on element i of a and b: out may be a or b,
+    // but must not overlap either at another offset.
+    for (const void* x : {a, b})
+        if (x != out && overlap(out, 8 * n, x, 8 * n)) invalid("cmul_c64: out partially overlaps an input");
+    const int v = aligned16({a, b, out}) ? 1 : 0;
+    void* args[] = {(void*)&a, (void*)&b, &out, &n};
+    launch(dev, stream, cmul_c64_[v], n, v ? 4 : 1, args);
+}
+
+void Pointwise::cmul_split(const HipBackend::DeviceHandle& dev, const void* a_re, const void* a_im,
+                           const void* b_re, const void* b_im, void* o_re, void* o_im, uint64_t n,
+                           hipStream_t stream) const {
+    if (n == 0) return;
+    need_ptrs("cmul_split", {a_re, a_im, b_re, b_im, o_re, o_im});
+    const uint64_t nb = 4 * n;
+    // Element i of the outputs depends only on element i of the inputs, so
+    // o_re may be a_re or b_re and o_im may be a_im or b_im; any other overlap
+    // of an output with an input or with the other output is rejected.
+    for (const void* x : {a_re, b_re, a_im, b_im}) {
+        const bool same_part_re = x == a_re || x == b_re;
+        if (!(same_part_re && x == o_re) && overlap(o_re, nb, x, nb))
+            invalid("cmul_split: o_re overlaps an input other than a_re / b_re");
+        if (!(!same_part_re && x == o_im) && overlap(o_im, nb, x, nb))
+            invalid("cmul_split: o_im overlaps an input other than a_im / b_im");
+    }
+    if (overlap(o_re, nb, o_im, nb)) invalid("cmul_split: o_re and o_im overlap");
+    const int v = aligned16({a_re, a_im, b_re, b_im, o_re, o_im}) ? 1 : 0;
+    void* args[] = {(void*)&a_re, (void*)&a_im, (void*)&b_re, (void*)&b_im, &o_re, &o_im, &n};
+    launch(dev, stream, cmul_split_[v], n, v ? 4 : 1, args);
+}
+
+void Pointwise::deinterleave(const HipBackend::DeviceHandle& dev, const void* in, void* re, void* im, uint64_t n,
+                             hipStream_t stream) const {
+    if (n == 0) return;
+    need_ptrs("deinterleave", {in, re, im});
+    if (overlap(in, 8 * n, re, 4 * n) || overlap(in, 8 * n, im, 4 * n) || overlap(re, 4 * n, im, 4 * n))
+        invalid("deinterleave: buffers overlap");
+    const int v = aligned16({in, re, im}) ? 1 : 0;
+    void* args[] = {(void*)&in, &re, &im, &n};
+    launch(dev, stream, deinterleave_[v], n, v ? 4 : 1, args);
+}
+
+void Pointwise::interleave(const HipBackend::DeviceHandle& dev, const void* re, const void* im, void* out,
+                           uint64_t n, hipStream_t stream) const {
+    if (n == 0) return;
+    need_ptrs("interleave", {re, im, out});
+    if (overlap(out, 8 * n, re, 4 * n) || overlap(out, 8 * n, im, 4 * n)) invalid("interleave: buffers overlap");
+    const int v = aligned16({re, im, out}) ? 1 : 0;
+    void* args[] = {(void*)&re, (void*)&im, &out, &n};
+    launch(dev, stream, interleave_[v], n, v ? 4 : 1, args);
+}
+
+}  // namespace fg

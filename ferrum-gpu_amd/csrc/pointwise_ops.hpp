@@ -1,0 +1,44 @@
+// pointwise_ops.hpp -- host launchers of the elementwise complex kernels
+// (kernels/pointwise.hpp): the reference's cmul_interleaved, cmul_split,
+// deinterleave and interleave (kernels_body.rs:1612-1672), which it defines
+// for its split-layout study and never launches from the FFT path.
+//
+// n counts complex elements.  Each launcher picks the 16-byte-access kernel
+// when every pointer is 16-byte aligned and the element-wise one otherwise;
+// both give identical results.  All are stream-ordered and asynchronous.
+#pragma once
+
+#include <cstdint>
+
+#include "device.hpp"
+#include "hip_backend.hpp"
+
+namespace fg {
+
+class Pointwise {
+public:
+    explicit Pointwise(const HipBackend::Module& mod);
+    Pointwise() = default;
+
+    // out[i] = a[i] * b[i]; complex64 interleaved.  out may alias a or b.
+    void cmul_c64(const HipBackend::DeviceHandle& dev, const void* a, const void* b, void* out, uint64_t n,
+                  hipStream_t stream) const;
+    // (o_re, o_im)[i] = (a_re, a_im)[i] * (b_re, b_im)[i]; split layout.
+    void cmul_split(const HipBackend::DeviceHandle& dev, const void* a_re, const void* a_im, const void* b_re,
+                    const void* b_im, void* o_re, void* o_im, uint64_t n, hipStream_t stream) const;
+    // re[i] = in[i].re, im[i] = in[i].im.  Outputs must not alias the input.
+    void deinterleave(const HipBackend::DeviceHandle& dev, const void* in, void* re, void* im, uint64_t n,
+                      hipStream_t stream) const;
+    // out[i] = (re[i], im[i]).  The output must not alias the inputs.
+    void interleave(const HipBackend::DeviceHandle& dev, const void* re, const void* im, void* out, uint64_t n,
+                    hipStream_t stream) const;
+
+private:
+    // [0]: one element per thread step, any alignment; [1]: four, 16-byte accesses.
+    HipBackend::KernelHandle cmul_c64_[2] = {nullptr, nullptr};
+    HipBackend::KernelHandle cmul_split_[2] = {nullptr, nullptr};
+    HipBackend::KernelHandle deinterleave_[2] = {nullptr, nullptr};
+    HipBackend::KernelHandle interleave_[2] = {nullptr, nullptr};
+};
+
+}  // namespace fg

@@ -118,6 +118,7 @@ def fft_2d_c2c_pow2(arr, log_n, direction="forward", normalize=False, device=Non
 
 
 def _ptr(x) -> ctypes.c_void_p:
+    """A device address from a DeviceBuffer, a GPU torch tensor or an int."""
     if isinstance(x, DeviceBuffer):
         return ctypes.c_void_p(x.ptr)
     if hasattr(x, "data_ptr"):  # a torch tensor on the GPU
@@ -152,6 +153,15 @@ class _Plan:
         arr = (ctypes.c_void_p * len(events))(*[e._e.value for e in events])
         _n.check(_n.lib.fg_fft_exec_events(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),
                                            ctypes.c_void_p(stream or None), arr, len(events)))
+
+    def execute_split(self, in_re, in_im, out_re, out_im, direction="forward", normalize=False,
+                      stream: int = 0) -> None:
+        """execute() on the split layout: real and imaginary parts in separate
+        float32 device arrays of ``batch * elems`` each (the reference's *_split
+        kernels).  out_re/out_im may be in_re/in_im; stream-ordered."""
+        d = _direction(direction)
+        _n.check(_n.lib.fg_fft_exec_split(self._p, _ptr(in_re), _ptr(in_im), _ptr(out_re), _ptr(out_im), d,
+                                          int(bool(normalize)), ctypes.c_void_p(stream or None)))
 
     def kernel_names(self) -> list[str]:
         names = []

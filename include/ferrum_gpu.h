@@ -190,6 +190,38 @@ FG_API int fg_fft_2d_rect_host(fg_device_t dev, const float *in, float *out, uin
 FG_API int fg_transpose_c64(fg_device_t dev, const void *d_in, void *d_out, uint32_t rows, uint32_t cols,
                             size_t batch, fg_stream_t stream);
 
+/* Split layout (structure of arrays): real and imaginary parts in two f32
+ * arrays of batch * elements each, transform f at element offset f * elements
+ * (the reference's fft_c2c_{256_r16s,1024,4096_4step_reg}_split kernels,
+ * crates/ferrum-gpu-fft-kernels/src/kernels_body.rs:509-626, 986-1130,
+ * 1463-1610, for every plan).  Same results as fg_fft_exec on the interleaved
+ * data.  d_out_re / d_out_im may equal d_in_re / d_in_im; no other overlap.
+ * Single-pass plans (1D, N <= 4096) run one launch; other plans stage through
+ * an interleaved buffer the plan allocates at its first split call.
+ * Stream-ordered, asynchronous. */
+FG_API int fg_fft_exec_split(fg_fft_plan_t plan, const void *d_in_re, const void *d_in_im,
+                             void *d_out_re, void *d_out_im, int direction, int normalize,
+                             fg_stream_t stream);
+
+/* Elementwise kernels over n complex elements (kernels_body.rs:1612-1672).
+ * Products are evaluated as re = ar*br - ai*bi, im = ar*bi + ai*br in f32
+ * without fused multiply-add, like the reference.  Any alignment of complex64
+ * / f32 data; 16-byte-aligned pointers take 16-byte accesses.  An output may
+ * be the same array as an input of the same part; other overlaps are
+ * rejected.  Stream-ordered, asynchronous. */
+/* out = a * b, interleaved complex64 (cmul_interleaved, :1612-1627). */
+FG_API int fg_cmul_c64(fg_device_t dev, const void *d_a, const void *d_b, void *d_out, size_t n,
+                       fg_stream_t stream);
+/* (o_re, o_im) = (a_re, a_im) * (b_re, b_im), split layout (cmul_split, :1629-1645). */
+FG_API int fg_cmul_split(fg_device_t dev, const void *d_a_re, const void *d_a_im, const void *d_b_re,
+                         const void *d_b_im, void *d_o_re, void *d_o_im, size_t n, fg_stream_t stream);
+/* re[i], im[i] = in[i] (deinterleave, :1647-1659). */
+FG_API int fg_deinterleave_c64(fg_device_t dev, const void *d_in, void *d_re, void *d_im, size_t n,
+                               fg_stream_t stream);
+/* out[i] = (re[i], im[i]) (interleave, :1661-1671). */
+FG_API int fg_interleave_c64(fg_device_t dev, const void *d_re, const void *d_im, void *d_out, size_t n,
+                             fg_stream_t stream);
+
 /* Streaming device copy of `bytes` (a multiple of 16) with the code object's
  * copy kernel: the HBM yardstick reported beside the FFT. */
 FG_API int fg_stream_copy(fg_device_t dev, const void *d_in, void *d_out, size_t bytes,

@@ -18,6 +18,9 @@ Parity pins (what checks each function against something it did not produce):
       radix-2 path (cpu_radix4.rs:105-159, cpu_radix8.rs:153-216,
       warp_fft.rs:211-311).
   or_dft_naive / or_dft_bins_f64 -- DFT([1,2,3,4]) and numpy complex128.
+  or_cmul_interleaved / or_cmul_split -- numpy float32 elementwise products
+      (each product and the sum rounded to f32), i*i = -1, z*conj(z) = |z|^2.
+  or_deinterleave / or_interleave -- numpy .real/.imag views, and each other's inverse.
 """
 
 from __future__ import annotations
@@ -75,6 +78,10 @@ def lib() -> ctypes.CDLL:
             L.or_dft_naive.argtypes = [fp, fp, sz]
             L.or_dft_bins_f64.argtypes = [fp, sz, ctypes.POINTER(ctypes.c_int64), sz,
                                           ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+            L.or_cmul_interleaved.argtypes = [fp, fp, fp, sz]
+            L.or_cmul_split.argtypes = [fp, fp, fp, fp, fp, fp, sz]
+            L.or_deinterleave.argtypes = [fp, fp, fp, sz]
+            L.or_interleave.argtypes = [fp, fp, fp, sz]
             _lib = L
     return _lib
 
@@ -219,4 +226,38 @@ def dft_bins_f64(x, bins, sign: int = -1) -> np.ndarray:
     out = np.empty(b.size, dtype=np.complex128)
     lib().or_dft_bins_f64(_fptr(a), a.size, b.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
                           b.size, sign, out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    return out
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def cmul_interleaved(a, b) -> np.ndarray:
+    """a * b elementwise over complex64 arrays (f32, no fused multiply-add)."""
+    x, y = _as_c64(a), _as_c64(b)
+    assert x.shape == y.shape
+    out = np.empty_like(x)
+    lib().or_cmul_interleaved(_fptr(x), _fptr(y), _fptr(out), x.size)
+    return out
+
+
+def cmul_split(a_re, a_im, b_re, b_im) -> tuple[np.ndarray, np.ndarray]:
+    ar, ai, br, bi = _f32(a_re), _f32(a_im), _f32(b_re), _f32(b_im)
+    o_re, o_im = np.empty_like(ar), np.empty_like(ar)
+    lib().or_cmul_split(_fptr(ar), _fptr(ai), _fptr(br), _fptr(bi), _fptr(o_re), _fptr(o_im), ar.size)
+    return o_re, o_im
+
+
+def deinterleave(x) -> tuple[np.ndarray, np.ndarray]:
+    a = _as_c64(x)
+    re, im = np.empty(a.size, np.float32), np.empty(a.size, np.float32)
+    lib().or_deinterleave(_fptr(a), _fptr(re), _fptr(im), a.size)
+    return re, im
+
+
+def interleave(re, im) -> np.ndarray:
+    r, m = _f32(re), _f32(im)
+    out = np.empty(r.size, np.complex64)
+    lib().or_interleave(_fptr(r), _fptr(m), _fptr(out), r.size)
     return out

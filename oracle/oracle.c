@@ -405,3 +405,40 @@ void or_dft_bins_f64(const float *in, size_t n, const int64_t *bins, size_t nbin
         out[2 * bi + 1] = si;
     }
 }
+
+/* ---- pointwise kernels ----------------------------------------------------
+ * One element per kernel thread in the reference; the products are written
+ * ar*br - ai*bi and ar*bi + ai*br, two f32 roundings and a rounded sum (the
+ * file is built with -ffp-contract=off, as Rust does not contract). */
+
+void or_cmul_interleaved(const float *a, const float *b, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const float ar = a[2 * i], ai = a[2 * i + 1];
+        const float br = b[2 * i], bi = b[2 * i + 1];
+        out[2 * i] = ar * br - ai * bi;
+        out[2 * i + 1] = ar * bi + ai * br;
+    }
+}
+
+void or_cmul_split(const float *a_re, const float *a_im, const float *b_re, const float *b_im,
+                   float *o_re, float *o_im, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const float ar = a_re[i], ai = a_im[i], br = b_re[i], bi = b_im[i];
+        o_re[i] = ar * br - ai * bi;
+        o_im[i] = ar * bi + ai * br;
+    }
+}
+
+void or_deinterleave(const float *in, float *re, float *im, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        re[i] = in[2 * i];
+        im[i] = in[2 * i + 1];
+    }
+}
+
+void or_interleave(const float *re, const float *im, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        out[2 * i] = re[i];
+        out[2 * i + 1] = im[i];
+    }
+}

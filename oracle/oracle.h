@@ -80,6 +80,18 @@ void or_dft_naive(const float *in, float *out, size_t n);
 void or_dft_bins_f64(const float *in, size_t n, const int64_t *bins, size_t nbins,
                      int sign, double *out);
 
+/* ---- pointwise kernels (crates/ferrum-gpu-fft-kernels/src/kernels_body.rs) -- */
+
+/* out = a * b over n interleaved complex (cmul_interleaved, :1612-1627). */
+void or_cmul_interleaved(const float *a, const float *b, float *out, size_t n);
+/* (o_re, o_im) = (a_re, a_im) * (b_re, b_im) over n elements (cmul_split, :1629-1645). */
+void or_cmul_split(const float *a_re, const float *a_im, const float *b_re, const float *b_im,
+                   float *o_re, float *o_im, size_t n);
+/* re[i], im[i] = in[2i], in[2i+1] (deinterleave, :1647-1659). */
+void or_deinterleave(const float *in, float *re, float *im, size_t n);
+/* out[2i], out[2i+1] = re[i], im[i] (interleave, :1661-1671). */
+void or_interleave(const float *re, const float *im, float *out, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

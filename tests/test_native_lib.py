@@ -55,6 +55,7 @@ def test_version_and_backend():
 def instantiated_kernels():
     src = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
     names = {f"fg_fft_n{m.group(1)}" for m in re.finditer(r"^FG_STOCKHAM\((\d+),", src, flags=re.M)}
+    names |= {f"{n}_split" for n in names}
     for m in re.finditer(r"^FG_TILE\((\d+), (\d+), (true|false), ([cr])\)", src, flags=re.M):
         names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_{m.group(4)}")
     return names
@@ -64,7 +65,7 @@ def planned_kernels():
     """Every kernel name FftPlan can request (mirrors fft_plan.cpp via the CPU models)."""
     from test_multipass_model import tile_geometry_1d, tile_geometry_2d
 
-    names = {f"fg_fft_n{l}" for l in range(2, 13)}
+    names = {f"fg_fft_n{l}" for l in range(2, 13)} | {f"fg_fft_n{l}_split" for l in range(2, 13)}
     for log_n in range(13, 25):
         for p in tile_geometry_1d(log_n, 1):
             names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}")
@@ -86,8 +87,21 @@ def test_code_object_is_embedded_for_gfx950():
     data = open(N.LIB_PATH, "rb").read()
     assert data.count(b"\x7fELF") >= 2
     assert b"gfx950" in data
-    for k in sorted(instantiated_kernels()) + ["fg_copy_f4", "fg_vector_add"]:
+    for k in sorted(instantiated_kernels()) + ["fg_copy_f4", "fg_vector_add", "fg_transpose_c64"] + POINTWISE:
         assert k.encode() in data, k
+
+
+POINTWISE = [f"fg_{op}_v{w}" for op in ("cmul_c64", "cmul_split", "deinterleave_c64", "interleave_c64")
+             for w in (1, 4)]
+
+
+def test_pointwise_kernels_are_instantiated():
+    src = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
+    widths = re.findall(r"^FG_POINTWISE\((\d+)\)", src, flags=re.M)
+    assert sorted(widths) == ["1", "4"]
+    host = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "pointwise_ops.cpp")).read()
+    for op in ("cmul_c64", "cmul_split", "deinterleave_c64", "interleave_c64"):
+        assert f'"fg_{op}"' in host
 
 
 # --------------------------------------------------- argument validation
@@ -146,6 +160,16 @@ def test_c_abi_validation_without_device():
     assert rc == N.FG_ERR_INVALID_ARGUMENT and "plan is null" in N.last_error()
     rc = N.lib.fg_fft_plan_1d(None, 10, 1, ctypes.byref(ctypes.c_void_p()))
     assert rc == N.FG_ERR_INVALID_ARGUMENT
+
+
+def test_split_and_pointwise_validation_without_device():
+    rc = N.lib.fg_fft_exec_split(None, None, None, None, None, 1, 0, None)
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "plan is null" in N.last_error()
+    # (entry point, number of device-pointer arguments between dev and n)
+    for fn, nptrs in (("fg_cmul_c64", 3), ("fg_cmul_split", 6), ("fg_deinterleave_c64", 3),
+                      ("fg_interleave_c64", 3)):
+        rc = getattr(N.lib, fn)(None, *([None] * nptrs), 16, None)
+        assert rc == N.FG_ERR_INVALID_ARGUMENT and "device is null" in N.last_error(), fn
 
 
 def test_last_error_is_thread_local():

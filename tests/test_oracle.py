@@ -325,3 +325,60 @@ def test_checks_reject_planted_mistakes():
     lane = _slow_input(16, 1)
     no_tw = oracle.radix4_forward_lane(lane, 4, np.ones_like(oracle.twiddles_radix4(4)))
     assert _per_bin_rel(no_tw, np.fft.fft(lane.astype(np.complex128))) > 1e-2
+
+
+# ------------------------------------------------------- pointwise kernels
+
+
+def _numpy_cmul_f32(ar, ai, br, bi):
+    # float32 numpy arithmetic rounds each product and the sum to f32: the
+    # reference's unfused `ar * br - ai * bi`, `ar * bi + ai * br`.
+    return ar * br - ai * bi, ar * bi + ai * br
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 100003])
+def test_cmul_matches_numpy_f32_exactly(n):
+    rng = np.random.default_rng(n)
+    a, b = uniform_c64(rng, n), uniform_c64(rng, n)
+    re, im = _numpy_cmul_f32(a.real.copy(), a.imag.copy(), b.real.copy(), b.imag.copy())
+    got = oracle.cmul_interleaved(a, b)
+    assert np.array_equal(got.real, re) and np.array_equal(got.imag, im)
+    s_re, s_im = oracle.cmul_split(a.real, a.imag, b.real, b.imag)
+    assert np.array_equal(s_re, re) and np.array_equal(s_im, im)
+    # complex128 product rounded once differs from the f32 formula by at most
+    # a few ulps of the operands' magnitude (sanity of the operand roles)
+    ref = (a.astype(np.complex128) * b.astype(np.complex128))
+    assert np.max(np.abs(got - ref)) < 1e-6
+
+
+def test_cmul_closed_forms():
+    z = np.array([0.5 - 1.25j, 3 + 4j, -2.5 + 0.125j], np.complex64)
+    i = np.full(3, 1j, np.complex64)
+    assert np.array_equal(oracle.cmul_interleaved(i, i), np.full(3, -1, np.complex64))
+    zz = oracle.cmul_interleaved(z, np.conj(z))
+    assert np.array_equal(zz.imag, np.zeros(3, np.float32))      # ar*(-ai) + ai*ar = 0 exactly
+    assert np.array_equal(zz.real, np.array([1.8125, 25, 6.265625], np.float32))
+    one = np.ones(3, np.complex64)
+    assert np.array_equal(oracle.cmul_interleaved(z, one), z)
+
+
+def test_deinterleave_interleave_are_views_and_inverses():
+    x = uniform_c64(np.random.default_rng(5), 1001)
+    re, im = oracle.deinterleave(x)
+    assert np.array_equal(re, x.real) and np.array_equal(im, x.imag)
+    assert np.array_equal(oracle.interleave(re, im), x)
+    assert np.array_equal(oracle.interleave(x.real, x.imag), x)
+
+
+def test_pointwise_checks_reject_planted_mistakes():
+    rng = np.random.default_rng(9)
+    a, b = uniform_c64(rng, 64), uniform_c64(rng, 64)
+    re, im = _numpy_cmul_f32(a.real.copy(), a.imag.copy(), b.real.copy(), b.imag.copy())
+    wrong = [oracle.cmul_interleaved(a, np.conj(b)),                 # conjugated operand
+             oracle.cmul_interleaved(a, b[::-1].copy()),              # wrong index
+             oracle.cmul_interleaved(np.conj(a), np.conj(b)),         # sign of the imaginary part
+             oracle.interleave(*oracle.deinterleave(a * 1j)) * b]     # swapped parts
+    for w in wrong:
+        assert not (np.array_equal(w.real, re) and np.array_equal(w.imag, im))
+    sw_re, sw_im = oracle.deinterleave(a)
+    assert not np.array_equal(oracle.interleave(sw_im, sw_re), a)   # re/im swapped
