@@ -5,22 +5,24 @@ Default workload (the one the north-star target is quoted
 on): batched 1D forward C2C complex64 FFT, N = 1024, batch = 65536 (512 MiB in,
 512 MiB out), re/im iid N(0,1) from seed 3, device-resident buffers.
 `--workload` selects the other BASELINE configurations (cfg1, cfg2_256,
-cfg2_4096, cfg4, cfg5) for the numbers quoted in DESIGN.md.
+cfg2_4096, cfg4, cfg5) and the operations beside the path (cfg3_split: config 3
+in the split layout; cmul, cmul_split, deinterleave, interleave: the pointwise
+kernels over config 3's 2^26 elements; transpose: an 8192 x 8192 complex64
+matrix) for the numbers quoted in DESIGN.md.
 
-A "step" is one pass of the hot path over the workload's batch (for cfg2: the
-forward and the normalised inverse transform).  W untimed warmup steps, then
-K timed steps between two device synchronisations.  Every kernel launch of the
-timed steps is bracketed by HIP events recorded on the stream it runs on,
-which gives each kernel's average duration for the roofline.
+A "step" is one pass of the workload over its batch (for cfg2: the forward and
+the normalised inverse transform).  W untimed warmup steps, then K timed steps
+between two device synchronisations.  Every kernel launch of the timed steps
+is followed by a HIP event recorded on the stream it runs on (plus one event
+before the first), which gives each kernel's duration for the roofline.
 
 Prints ONE JSON line on stdout (progress goes to stderr):
-  value        = algorithmic bytes per step (16 * elems * batch per transform
-                 executed) / wall time per step, GB/s
-  roofline     = the dominant kernel: bytes it moves per launch (it reads and
-                 writes the whole array once) / its average launch duration,
-                 against the 8 TB/s HBM peak
-  cpu_baseline = the CPU Stockham oracle (C restatement of the reference's
-                 crates/ferrum-gpu-fft/src/cpu.rs / cpu_2d.rs) timed on this host
+  value        = algorithmic bytes per step / wall time per step, GB/s (FFT:
+                 16 * elems * batch per transform executed)
+  roofline     = the dominant kernel: algorithmic bytes it moves per launch /
+                 its average launch duration, against the 8 TB/s HBM peak
+  cpu_baseline = the CPU oracle (C restatement of the reference's CPU path)
+                 timed on this host, also the checker of the GPU output
 """
 
 from __future__ import annotations
@@ -39,21 +41,34 @@ for p in (ROOT, os.path.join(ROOT, "ferrum-gpu_amd")):
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E peak, 8 TB/s
 
-# name: dims, log_n, batch, seed, distribution, [(direction, normalize) per step], description
-WORKLOADS = {
-    "cfg3": (1, 10, 65536, 3, "normal", [("forward", False)],
+# FFT workloads: name -> (dims, log_n, batch, seed, distribution,
+# [(direction, normalize) per step], layout, description)
+FFT_WORKLOADS = {
+    "cfg3": (1, 10, 65536, 3, "normal", [("forward", False)], "interleaved",
              "1D forward C2C FFT N=1024 batch=65536 complex64, re/im iid N(0,1) seed 3"),
-    "cfg1": (1, 10, 256, 1, "uniform", [("forward", False)],
+    "cfg1": (1, 10, 256, 1, "uniform", [("forward", False)], "interleaved",
              "1D forward C2C FFT N=1024 batch=256 complex64, re/im iid U[-1,1) seed 1"),
-    "cfg2_256": (1, 8, 256, 2, "uniform", [("forward", False), ("inverse", True)],
+    "cfg2_256": (1, 8, 256, 2, "uniform", [("forward", False), ("inverse", True)], "interleaved",
                  "1D forward+inverse C2C FFT N=256 batch=256 complex64, re/im iid U[-1,1) seed 2"),
-    "cfg2_4096": (1, 12, 256, 2, "uniform", [("forward", False), ("inverse", True)],
+    "cfg2_4096": (1, 12, 256, 2, "uniform", [("forward", False), ("inverse", True)], "interleaved",
                   "1D forward+inverse C2C FFT N=4096 batch=256 complex64, re/im iid U[-1,1) seed 2"),
-    "cfg4": (1, 24, 4, 4, "normal", [("forward", False)],
+    "cfg4": (1, 24, 4, 4, "normal", [("forward", False)], "interleaved",
              "1D forward C2C FFT N=2^24 batch=4 complex64, re/im iid N(0,1) seed 4"),
-    "cfg5": (2, 12, 2, 5, "uniform", [("forward", False)],
+    "cfg5": (2, 12, 2, 5, "uniform", [("forward", False)], "interleaved",
              "2D forward C2C FFT 4096x4096 batch=2 complex64, re/im iid U[-1,1) seed 5"),
+    "cfg3_split": (1, 10, 65536, 3, "normal", [("forward", False)], "split",
+                   "1D forward C2C FFT N=1024 batch=65536, split layout (re, im f32 arrays), "
+                   "re/im iid N(0,1) seed 3"),
 }
+# Elementwise / data-movement workloads: name -> (elements, description)
+OP_WORKLOADS = {
+    "cmul": (1 << 26, "pointwise complex multiply out=a*b, 2^26 interleaved complex64, N(0,1) seeds 3/13"),
+    "cmul_split": (1 << 26, "pointwise complex multiply, split layout, 2^26 elements, N(0,1) seeds 3/13"),
+    "deinterleave": (1 << 26, "interleaved complex64 -> (re, im) f32 arrays, 2^26 elements, N(0,1) seed 3"),
+    "interleave": (1 << 26, "(re, im) f32 arrays -> interleaved complex64, 2^26 elements, N(0,1) seed 3"),
+    "transpose": (1 << 26, "out-of-place transpose of an 8192x8192 complex64 matrix, N(0,1) seed 3"),
+}
+WORKLOADS = sorted(FFT_WORKLOADS) + sorted(OP_WORKLOADS)
 
 
 def log(msg: str) -> None:
@@ -94,74 +109,321 @@ def host_cores() -> int:
         return os.cpu_count() or 1
 
 
-def cpu_baseline(np, x, dims, log_n, batch, steps, gpu_out, budget_s: float):
-    """Time the CPU oracle on this host (a reported baseline, never the target)
-    and use its result as the checker of the GPU output."""
-    import oracle  # test infrastructure: only the timed CPU baseline and checker
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
 
-    elems = (1 << log_n) if dims == 1 else (1 << (2 * log_n))
 
-    def run(buf, direction, normalize, threads):
-        if dims == 1:
-            return oracle.fft_1d(buf, log_n, direction, normalize, threads=threads)
-        if threads <= 1 or batch < 2:
-            return oracle.fft_2d(buf, log_n, direction, normalize)
-        imgs = buf.reshape(batch, -1)
-        out = np.empty_like(imgs)
-        bounds = np.linspace(0, batch, min(threads, batch) + 1).astype(int)
+def in_threads(n_items: int, threads: int, part) -> None:
+    """part(lo, hi) over [0, n_items) split across up to `threads` threads (the
+    oracle's C calls drop the GIL)."""
+    import numpy as np
 
-        def part(lo, hi):
-            out[lo:hi] = oracle.fft_2d(imgs[lo:hi], log_n, direction, normalize).reshape(hi - lo, -1)
+    bounds = np.linspace(0, n_items, min(threads, n_items) + 1).astype(int)
+    ts = [threading.Thread(target=part, args=(bounds[i], bounds[i + 1])) for i in range(len(bounds) - 1)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
 
-        ts = [threading.Thread(target=part, args=(bounds[i], bounds[i + 1])) for i in range(len(bounds) - 1)]
-        for t in ts:
-            t.start()
-        for t in ts:
-            t.join()
-        return out.reshape(-1)
 
-    def one_step(threads):
-        y = x
-        for direction, normalize in steps:
-            y = run(y, direction, normalize, threads)
+# ------------------------------------------------------------------ workloads
+#
+# A workload uploads its inputs, lists the kernels one step launches (with a
+# key per launch that groups repeated launches of the same plan position), runs
+# a step with an optional event after each launch, returns its output, and
+# computes the same output with the CPU oracle (timed for cpu_baseline).
+
+
+class FftWorkload:
+    def __init__(self, name, np, dev):
+        import ferrum_gpu
+        from ferrum_gpu.hip import DeviceBuffer
+
+        dims, log_n, batch, seed, dist, steps, layout, desc = FFT_WORKLOADS[name]
+        self.np, self.dev, self.desc = np, dev, desc
+        self.dims, self.log_n, self.batch, self.steps, self.layout = dims, log_n, batch, steps, layout
+        self.elems = (1 << log_n) if dims == 1 else (1 << (2 * log_n))
+        n = self.elems * batch
+        self.nbytes_io = 8 * n
+        self.algo_bytes = 2 * self.nbytes_io * len(steps)
+        self.flops = 5.0 * self.elems * (log_n if dims == 1 else 2 * log_n) * batch * len(steps)
+        self.exact = False
+        self.x = make_input(np, n, seed, dist)
+        self.plan = (ferrum_gpu.fft.Plan1D if dims == 1 else ferrum_gpu.fft.Plan2D)(log_n, batch, dev)
+        kernels = self.plan.kernel_names()
+        if layout == "split":
+            if self.plan.describe()["launches"] != 1:
+                raise SystemExit("bench.py: split workloads are single-pass plans")
+            kernels = [kernels[0] + "_split"]
+            # (re, im) per stage of the chain: inputs, then one output per step
+            self.parts = [(DeviceBuffer(dev, 4 * n), DeviceBuffer(dev, 4 * n)) for _ in range(len(steps) + 1)]
+            self.parts[0][0].copy_from_host(np.ascontiguousarray(self.x.real))
+            self.parts[0][1].copy_from_host(np.ascontiguousarray(self.x.imag))
+            self.copy_bufs = (self.parts[0][0], self.parts[1][0], 4 * n)
+        else:
+            self.bufs = [DeviceBuffer(dev, self.nbytes_io) for _ in range(len(steps) + 1)]
+            self.bufs[0].copy_from_host(self.x)
+            self.copy_bufs = (self.bufs[0], self.bufs[1], self.nbytes_io)
+        self.kernels = kernels
+        self.launch_names = kernels * len(steps)
+        self.launch_keys = [f"{i}:{k}" for _ in steps for i, k in enumerate(kernels)]
+        self.bytes_per_launch = 2 * self.nbytes_io  # each pass reads and writes the whole array once
+        self.describe = self.plan.describe()
+
+    def run(self, stream, events=None):
+        L = len(self.kernels)
+        for j, (direction, normalize) in enumerate(self.steps):
+            if self.layout == "split":
+                (ir, ii), (orr, oi) = self.parts[j], self.parts[j + 1]
+                self.plan.execute_split(ir, ii, orr, oi, direction, normalize, stream)
+                if events is not None:
+                    events[j].record(stream)
+            elif events is None:
+                self.plan.execute(self.bufs[j], self.bufs[j + 1], direction, normalize, stream)
+            else:
+                self.plan.execute_recording(self.bufs[j], self.bufs[j + 1], events[j * L:(j + 1) * L],
+                                            direction, normalize, stream)
+
+    def output(self):
+        np = self.np
+        n = self.elems * self.batch
+        if self.layout == "split":
+            re, im = np.empty(n, np.float32), np.empty(n, np.float32)
+            self.parts[-1][0].copy_to_host(re)
+            self.parts[-1][1].copy_to_host(im)
+            out = np.empty(n, np.complex64)
+            out.real, out.imag = re, im
+            return out
+        out = np.empty_like(self.x)
+        self.bufs[-1].copy_to_host(out)
+        return out
+
+    def cpu(self, threads: int):
+        import oracle  # test infrastructure: only the timed CPU baseline and checker
+
+        np = self.np
+
+        def run(buf, direction, normalize):
+            if self.dims == 1:
+                return oracle.fft_1d(buf, self.log_n, direction, normalize, threads=threads)
+            if threads <= 1 or self.batch < 2:
+                return oracle.fft_2d(buf, self.log_n, direction, normalize)
+            imgs = buf.reshape(self.batch, -1)
+            out = np.empty_like(imgs)
+
+            def part(lo, hi):
+                out[lo:hi] = oracle.fft_2d(imgs[lo:hi], self.log_n, direction, normalize).reshape(hi - lo, -1)
+
+            in_threads(self.batch, threads, part)
+            return out.reshape(-1)
+
+        y = self.x
+        for direction, normalize in self.steps:
+            y = run(y, direction, normalize)
         return y
 
+    def config(self):
+        layout = ("split re/im f32 arrays" if self.layout == "split" else "interleaved complex64") + \
+            ", device-resident"
+        return {"dims": self.dims, "log_n": self.log_n, "batch": self.batch,
+                "directions": [d for d, _ in self.steps], "layout": layout}
+
+    def sample(self):
+        return f"full workload ({self.batch} transforms x {len(self.steps)} direction(s))"
+
+
+class OpWorkload:
+    """One launch per step of a pointwise kernel or the transpose."""
+
+    def __init__(self, name, np, dev):
+        from ferrum_gpu.hip import DeviceBuffer
+
+        self.name, self.np, self.dev = name, np, dev
+        n, self.desc = OP_WORKLOADS[name]
+        self.n = n
+        self.exact = True
+        self.flops = 6.0 * n if name.startswith("cmul") else 0.0
+        a = make_input(np, n, 3, "normal")
+        self.inputs = [a]
+        # contiguous parts, prepared once for the split-layout kernels and the CPU leg
+        self.parts = [np.ascontiguousarray(a.real), np.ascontiguousarray(a.imag)]
+        f4 = 4 * n
+        if name == "cmul":
+            b = make_input(np, n, 13, "normal")
+            self.inputs.append(b)
+            self.d_in = [DeviceBuffer(dev, 8 * n), DeviceBuffer(dev, 8 * n)]
+            self.d_in[0].copy_from_host(a)
+            self.d_in[1].copy_from_host(b)
+            self.d_out = [DeviceBuffer(dev, 8 * n)]
+            self.algo_bytes = 24 * n
+            kernel = "fg_cmul_c64_vec"
+        elif name == "cmul_split":
+            b = make_input(np, n, 13, "normal")
+            self.inputs.append(b)
+            self.parts += [np.ascontiguousarray(b.real), np.ascontiguousarray(b.imag)]
+            self.d_in = [DeviceBuffer(dev, f4) for _ in range(4)]
+            for buf, part in zip(self.d_in, self.parts):
+                buf.copy_from_host(part)
+            self.d_out = [DeviceBuffer(dev, f4), DeviceBuffer(dev, f4)]
+            self.algo_bytes = 24 * n
+            kernel = "fg_cmul_split_vec"
+        elif name == "deinterleave":
+            self.d_in = [DeviceBuffer(dev, 8 * n)]
+            self.d_in[0].copy_from_host(a)
+            self.d_out = [DeviceBuffer(dev, f4), DeviceBuffer(dev, f4)]
+            self.algo_bytes = 16 * n
+            kernel = "fg_deinterleave_c64_vec"
+        elif name == "interleave":
+            self.d_in = [DeviceBuffer(dev, f4), DeviceBuffer(dev, f4)]
+            self.d_in[0].copy_from_host(self.parts[0])
+            self.d_in[1].copy_from_host(self.parts[1])
+            self.d_out = [DeviceBuffer(dev, 8 * n)]
+            self.algo_bytes = 16 * n
+            kernel = "fg_interleave_c64_vec"
+        else:  # transpose
+            self.side = 1 << 13
+            assert self.side * self.side == n
+            self.d_in = [DeviceBuffer(dev, 8 * n)]
+            self.d_in[0].copy_from_host(a)
+            self.d_out = [DeviceBuffer(dev, 8 * n)]
+            self.algo_bytes = 16 * n
+            kernel = "fg_transpose_c64"
+        self.kernels = [kernel]
+        self.launch_names = [kernel]
+        self.launch_keys = [f"0:{kernel}"]
+        self.bytes_per_launch = self.algo_bytes
+        self.copy_bufs = (self.d_in[0], self.d_out[0], (min(self.d_in[0].nbytes, self.d_out[0].nbytes) // 16) * 16)
+        self.describe = {"launches": 1, "main_kernel": kernel, "workspace_bytes": 0}
+
+    def run(self, stream, events=None):
+        import ferrum_gpu
+        from ferrum_gpu import pointwise
+
+        d, i, o = self.dev, self.d_in, self.d_out
+        if self.name == "cmul":
+            pointwise.cmul(d, i[0], i[1], o[0], self.n, stream)
+        elif self.name == "cmul_split":
+            pointwise.cmul_split(d, i[0], i[1], i[2], i[3], o[0], o[1], self.n, stream)
+        elif self.name == "deinterleave":
+            pointwise.deinterleave(d, i[0], o[0], o[1], self.n, stream)
+        elif self.name == "interleave":
+            pointwise.interleave(d, i[0], i[1], o[0], self.n, stream)
+        else:
+            ferrum_gpu.fft.transpose(d, i[0], o[0], self.side, self.side, 1, stream)
+        if events is not None:
+            events[0].record(stream)
+
+    def output(self):
+        np = self.np
+        if len(self.d_out) == 2:
+            outs = [np.empty(self.n, np.float32) for _ in range(2)]
+            for buf, h in zip(self.d_out, outs):
+                buf.copy_to_host(h)
+            return np.concatenate(outs)
+        out = np.empty(self.n, np.complex64)
+        self.d_out[0].copy_to_host(out)
+        return out
+
+    def cpu(self, threads: int):
+        import oracle  # test infrastructure: only the timed CPU baseline and checker
+
+        np = self.np
+        a = self.inputs[0]
+        if self.name == "transpose":
+            out = a.copy()
+            side = self.side
+            if threads <= 1:
+                oracle.transpose_square(out, side)
+                return out
+            # the oracle transposes one square in place; by threads, transpose
+            # row blocks out of place with the same element order
+            src, dst = a.reshape(side, side), out.reshape(side, side)
+
+            def part(lo, hi):
+                dst[:, lo:hi] = src[lo:hi, :].T
+
+            in_threads(side, threads, part)
+            return out
+        n = self.n
+        if self.name == "cmul":
+            fn = lambda lo, hi: oracle.cmul_interleaved(a[lo:hi], self.inputs[1][lo:hi])  # noqa: E731
+            res = np.empty(n, np.complex64)
+        elif self.name == "cmul_split":
+            ar, ai, br, bi = self.parts
+            res = np.empty(2 * n, np.float32)
+
+            def fn(lo, hi):
+                return oracle.cmul_split(ar[lo:hi], ai[lo:hi], br[lo:hi], bi[lo:hi])
+        elif self.name == "deinterleave":
+            res = np.empty(2 * n, np.float32)
+            fn = lambda lo, hi: oracle.deinterleave(a[lo:hi])  # noqa: E731
+        else:
+            res = np.empty(n, np.complex64)
+            fn = lambda lo, hi: oracle.interleave(self.parts[0][lo:hi], self.parts[1][lo:hi])  # noqa: E731
+
+        def part(lo, hi):
+            r = fn(lo, hi)
+            if isinstance(r, tuple):
+                res[lo:hi], res[n + lo:n + hi] = r
+            else:
+                res[lo:hi] = r
+
+        in_threads(n, max(1, threads), part)
+        return res
+
+    def config(self):
+        if self.name == "transpose":
+            return {"rows": self.side, "cols": self.side, "batch": 1, "layout": "interleaved complex64"}
+        return {"elements": self.n,
+                "layout": "split re/im f32 arrays" if self.name == "cmul_split" else "see workload"}
+
+    def sample(self):
+        if self.name == "transpose":
+            return f"full workload ({self.side}x{self.side}; one thread: a copy, then the oracle's in-place swap)"
+        return f"full workload ({self.n} elements)"
+
+
+def cpu_baseline(np, wl, gpu_out, budget_s: float):
+    """Time the CPU oracle on this host (a reported baseline, never the target)
+    and use its result as the checker of the GPU output."""
     t0 = time.perf_counter()
-    ref = one_step(1)
+    ref = wl.cpu(1)
     reps = [time.perf_counter() - t0]
     while sum(reps) < budget_s and len(reps) < 50:
         t0 = time.perf_counter()
-        one_step(1)
+        wl.cpu(1)
         reps.append(time.perf_counter() - t0)
     single = float(np.median(reps))
     threads = max(1, min(16, host_cores()))
     multi_reps = []
     for _ in range(3):
         t0 = time.perf_counter()
-        one_step(threads)
+        wl.cpu(threads)
         multi_reps.append(time.perf_counter() - t0)
     multi = float(np.median(multi_reps))
-    err = float(np.linalg.norm((gpu_out - ref).astype(np.complex128)) / np.linalg.norm(ref.astype(np.complex128)))
-    nbytes = 16 * elems * batch * len(steps)
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    if wl.exact:
+        err = 0.0 if np.array_equal(gpu_out, ref) else float(
+            np.max(np.abs(gpu_out.astype(np.complex128) - ref.astype(np.complex128))))
+    else:
+        err = float(np.linalg.norm((gpu_out - ref).astype(np.complex128)) /
+                    np.linalg.norm(ref.astype(np.complex128)))
     base = {
-        "value": round(nbytes / single / 1e9, 4),
+        "value": round(wl.algo_bytes / single / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"full workload ({batch} transforms x {len(steps)} direction(s)), median of {len(reps)} "
-                  f"passes, {single:.3f} s/pass, oracle/oracle.c -O3, one thread",
-        "cpu_model": cpu_model,
+        "sample": f"{wl.sample()}, median of {len(reps)} passes, {single:.3f} s/pass, "
+                  "oracle/oracle.c -O3, one thread",
+        "cpu_model": cpu_model(),
     }
-    multi_d = {"value": round(nbytes / multi / 1e9, 4), "unit": "GB/s", "cores": threads,
+    multi_d = {"value": round(wl.algo_bytes / multi / 1e9, 4), "unit": "GB/s", "cores": threads,
                "seconds_per_pass": round(multi, 4)}
     return base, multi_d, err
 
@@ -173,7 +435,7 @@ def main() -> int:
     # The GPU reaches steady clocks after ~100 back-to-back launches of the
     # config-3 kernel (~20 ms); fewer warmup steps time the ramp, not the kernel.
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="cfg3", choices=WORKLOADS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of single-thread CPU timing")
     args = ap.parse_args()
@@ -188,39 +450,20 @@ def main() -> int:
 
     import numpy as np
 
-    import ferrum_gpu
     from ferrum_gpu import _native as N
-    from ferrum_gpu.hip import Device, DeviceBuffer, Event
-
-    dims, log_n, batch, seed, dist, steps, desc = WORKLOADS[args.workload]
-    elems = (1 << log_n) if dims == 1 else (1 << (2 * log_n))
-    nbytes_io = 8 * elems * batch
-    algo_bytes = 2 * nbytes_io * len(steps)           # per step
-    flops_per_transform = 5.0 * elems * (log_n if dims == 1 else 2 * log_n)
-    flops = flops_per_transform * batch * len(steps)
+    from ferrum_gpu.hip import Device, Event
 
     dev = Device(0)
     info = dev.info()
     log(f"device {info}")
-    log(f"workload {args.workload}: {desc}")
-    x = make_input(np, elems * batch, seed, dist)
-    bufs = [DeviceBuffer(dev, nbytes_io) for _ in range(len(steps) + 1)]
-    bufs[0].copy_from_host(x)
-    plan = (ferrum_gpu.fft.Plan1D if dims == 1 else ferrum_gpu.fft.Plan2D)(log_n, batch, dev)
-    kernels = plan.kernel_names()
-    launches = len(kernels)
+    wl = (FftWorkload if args.workload in FFT_WORKLOADS else OpWorkload)(args.workload, np, dev)
+    log(f"workload {args.workload}: {wl.desc}")
     stream = dev.default_stream
-    log(f"plan {plan.describe()} kernels {kernels}")
-
-    def step(events=None):
-        for j, (direction, normalize) in enumerate(steps):
-            if events is None:
-                plan.execute(bufs[j], bufs[j + 1], direction, normalize, stream)
-            else:
-                plan.execute_recording(bufs[j], bufs[j + 1], events[j], direction, normalize, stream)
+    log(f"plan {wl.describe} kernels {wl.kernels}")
+    launches = len(wl.launch_names)
 
     for _ in range(args.warmup):
-        step()
+        wl.run(stream)
     dev.sync()
     log(f"warmup {args.warmup} done")
 
@@ -228,12 +471,12 @@ def main() -> int:
     # between consecutive events.  One marker per launch costs ~2 us of gap per
     # launch; a pair per launch measured ~6 us.
     start = Event(dev)
-    evs = [[[Event(dev) for _ in range(launches)] for _ in steps] for _ in range(args.steps)]
+    evs = [[Event(dev) for _ in range(launches)] for _ in range(args.steps)]
     dev.sync()
     t0 = time.perf_counter()
     start.record(stream)
     for k in range(args.steps):
-        step(evs[k])
+        wl.run(stream, evs[k])
     dev.sync()
     wall = time.perf_counter() - t0
     log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms")
@@ -241,44 +484,45 @@ def main() -> int:
     per_kernel: dict[str, list[float]] = {}
     prev = start
     for k in range(args.steps):
-        for j in range(len(steps)):
-            for i, name in enumerate(kernels):
-                per_kernel.setdefault(f"{i}:{name}", []).append(prev.elapsed_ms(evs[k][j][i]))
-                prev = evs[k][j][i]
+        for i, key in enumerate(wl.launch_keys):
+            per_kernel.setdefault(key, []).append(prev.elapsed_ms(evs[k][i]))
+            prev = evs[k][i]
     kernel_ms = {key: float(np.mean(v)) for key, v in per_kernel.items()}
+    kernel_med = {key: float(np.median(v)) for key, v in per_kernel.items()}
     dominant = max(kernel_ms, key=lambda key: kernel_ms[key] * len(per_kernel[key]))
     dom_name = dominant.split(":", 1)[1]
     dom_avg = kernel_ms[dominant]
-    bytes_per_launch = 2 * nbytes_io                  # each launch reads and writes the whole array once
-    achieved = bytes_per_launch / (dom_avg * 1e-3) / 1e9
+    achieved = wl.bytes_per_launch / (dom_avg * 1e-3) / 1e9
 
     ms_per_step = wall * 1e3 / args.steps
-    value = algo_bytes / (ms_per_step * 1e-3) / 1e9
+    value = wl.algo_bytes / (ms_per_step * 1e-3) / 1e9
 
     # HBM yardstick: the code object's plain copy kernel over the same bytes.
+    src, dst, nbytes = wl.copy_bufs
     c0, c1 = Event(dev), Event(dev)
     copy_ms = []
     for _ in range(20):
         c0.record(stream)
-        N.check(N.lib.fg_stream_copy(dev.handle, bufs[0]._p, bufs[1]._p, nbytes_io, stream))
+        N.check(N.lib.fg_stream_copy(dev.handle, src._p, dst._p, nbytes, stream))
         c1.record(stream)
         c1.synchronize()
         copy_ms.append(c0.elapsed_ms(c1))
-    copy_gbs = 2 * nbytes_io / (float(np.median(copy_ms)) * 1e-3) / 1e9
+    copy_gbs = 2 * nbytes / (float(np.median(copy_ms)) * 1e-3) / 1e9
 
-    # Output of one step (recomputed: the copy above overwrote bufs[1]).
-    step()
+    # Output of one step (recomputed: the copy above overwrote an output).
+    wl.run(stream)
     dev.sync()
-    out = np.empty_like(x)
-    bufs[-1].copy_to_host(out)
+    out = wl.output()
 
     base = multi = err = None
     if not args.no_cpu:
         log("cpu baseline ...")
-        base, multi, err = cpu_baseline(np, x, dims, log_n, batch, steps, out, args.cpu_budget)
+        base, multi, err = cpu_baseline(np, wl, out, args.cpu_budget)
         log(f"cpu baseline {base['value']} GB/s (1 core), {multi['value']} GB/s ({multi['cores']} cores); "
-            f"gpu-vs-cpu rel_l2 {err:.3e}")
+            f"gpu-vs-cpu {'max abs diff' if wl.exact else 'rel_l2'} {err:.3e}")
 
+    config = {"workload": wl.desc, "name": args.workload}
+    config.update(wl.config())
     result = {
         "metric": "batched C2C FFT GB/s (% HBM peak) + GFLOP/s (5Nlog2N), complex64",
         "value": round(value, 2),
@@ -292,11 +536,11 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": desc, "name": args.workload, "dims": dims, "log_n": log_n, "batch": batch,
-                   "directions": [d for d, _ in steps], "layout": "interleaved complex64, device-resident"},
+        "config": config,
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
-        "gflops": round(flops / (ms_per_step * 1e-3) / 1e9, 2),
+        "gflops": round(wl.flops / (ms_per_step * 1e-3) / 1e9, 2),
         "kernels_avg_ms": {key: round(v, 5) for key, v in kernel_ms.items()},
+        "kernels_median_ms": {key: round(v, 5) for key, v in kernel_med.items()},
         "stream_copy_gbs": round(copy_gbs, 1),
         "roofline": {
             "bound": "hbm",
@@ -306,12 +550,12 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_for(dom_name, args.workload),
-            "bytes_per_launch": bytes_per_launch,
+            "bytes_per_launch": wl.bytes_per_launch,
             "avg_launch_ms": round(dom_avg, 5),
         },
         "cpu_baseline": base,
         "cpu_baseline_all_cores": multi,
-        "rel_l2_vs_cpu": err,
+        ("max_abs_diff_vs_cpu" if wl.exact else "rel_l2_vs_cpu"): err,
         "device": info,
     }
     print(json.dumps(result), flush=True)

@@ -147,29 +147,30 @@ FG_TILE(10, 16, true, r)
 
 // ------------------------------------------------------------- pointwise
 //
-// fg_<op>_v4: four elements per thread step with 16-byte accesses (every
-// pointer 16-byte aligned); fg_<op>_v1: one element, any alignment.  n is the
-// number of complex elements.  256-thread workgroups, grid-stride.
+// fg_<op>_vec: 16-byte accesses (every pointer 16-byte aligned; W elements
+// per thread step: 2 on interleaved streams, 4 for cmul_split); fg_<op>_elem:
+// one element per thread step, any alignment.  n is the number of complex
+// elements.  256-thread workgroups, grid-stride.
 #include "pointwise.hpp"
 
-#define FG_POINTWISE(W)                                                                               \
-    extern "C" __global__ __launch_bounds__(256) void fg_cmul_c64_v##W(                              \
+#define FG_POINTWISE(SUFFIX, WC, WS)                                                                  \
+    extern "C" __global__ __launch_bounds__(256) void fg_cmul_c64_##SUFFIX(                          \
         const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out, uint64_t n) { \
-        cmul_c64_body<W>(a, b, out, n);                                                               \
+        cmul_c64_body<WC>(a, b, out, n);                                                              \
     }                                                                                                 \
-    extern "C" __global__ __launch_bounds__(256) void fg_cmul_split_v##W(                            \
+    extern "C" __global__ __launch_bounds__(256) void fg_cmul_split_##SUFFIX(                        \
         const float* __restrict__ a_re, const float* __restrict__ a_im, const float* __restrict__ b_re, \
         const float* __restrict__ b_im, float* __restrict__ o_re, float* __restrict__ o_im, uint64_t n) { \
-        cmul_split_body<W>(a_re, a_im, b_re, b_im, o_re, o_im, n);                                    \
+        cmul_split_body<WS>(a_re, a_im, b_re, b_im, o_re, o_im, n);                                   \
     }                                                                                                 \
-    extern "C" __global__ __launch_bounds__(256) void fg_deinterleave_c64_v##W(                      \
+    extern "C" __global__ __launch_bounds__(256) void fg_deinterleave_c64_##SUFFIX(                  \
         const float* __restrict__ in, float* __restrict__ re, float* __restrict__ im, uint64_t n) {   \
-        deinterleave_body<W>(in, re, im, n);                                                          \
+        deinterleave_body<WC>(in, re, im, n);                                                         \
     }                                                                                                 \
-    extern "C" __global__ __launch_bounds__(256) void fg_interleave_c64_v##W(                        \
+    extern "C" __global__ __launch_bounds__(256) void fg_interleave_c64_##SUFFIX(                    \
         const float* __restrict__ re, const float* __restrict__ im, float* __restrict__ out, uint64_t n) { \
-        interleave_body<W>(re, im, out, n);                                                           \
+        interleave_body<WC>(re, im, out, n);                                                          \
     }
 
-FG_POINTWISE(4)
-FG_POINTWISE(1)
+FG_POINTWISE(vec, 2, 4)
+FG_POINTWISE(elem, 1, 1)

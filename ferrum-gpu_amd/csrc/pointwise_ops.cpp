@@ -42,7 +42,7 @@ void launch(const HipBackend::DeviceHandle& dev, hipStream_t stream, HipBackend:
 
 Pointwise::Pointwise(const HipBackend::Module& mod) {
     for (int v = 0; v < 2; ++v) {
-        const std::string w = v ? "_v4" : "_v1";
+        const std::string w = v ? "_vec" : "_elem";
         cmul_c64_[v] = HipBackend::get_kernel(mod, ("fg_cmul_c64" + w).c_str());
         cmul_split_[v] = HipBackend::get_kernel(mod, ("fg_cmul_split" + w).c_str());
         deinterleave_[v] = HipBackend::get_kernel(mod, ("fg_deinterleave_c64" + w).c_str());
@@ -60,7 +60,7 @@ void Pointwise::cmul_c64(const HipBackend::DeviceHandle& dev, const void* a, con
         if (x != out && overlap(out, 8 * n, x, 8 * n)) invalid("cmul_c64: out partially overlaps an input");
     const int v = aligned16({a, b, out}) ? 1 : 0;
     void* args[] = {(void*)&a, (void*)&b, &out, &n};
-    launch(dev, stream, cmul_c64_[v], n, v ? 4 : 1, args);
+    launch(dev, stream, cmul_c64_[v], n, v ? 2 : 1, args);
 }
 
 void Pointwise::cmul_split(const HipBackend::DeviceHandle& dev, const void* a_re, const void* a_im,
@@ -93,7 +93,7 @@ void Pointwise::deinterleave(const HipBackend::DeviceHandle& dev, const void* in
         invalid("deinterleave: buffers overlap");
     const int v = aligned16({in, re, im}) ? 1 : 0;
     void* args[] = {(void*)&in, &re, &im, &n};
-    launch(dev, stream, deinterleave_[v], n, v ? 4 : 1, args);
+    launch(dev, stream, deinterleave_[v], n, v ? 2 : 1, args);
 }
 
 void Pointwise::interleave(const HipBackend::DeviceHandle& dev, const void* re, const void* im, void* out,
@@ -103,7 +103,7 @@ void Pointwise::interleave(const HipBackend::DeviceHandle& dev, const void* re, 
     if (overlap(out, 8 * n, re, 4 * n) || overlap(out, 8 * n, im, 4 * n)) invalid("interleave: buffers overlap");
     const int v = aligned16({re, im, out}) ? 1 : 0;
     void* args[] = {(void*)&re, (void*)&im, &out, &n};
-    launch(dev, stream, interleave_[v], n, v ? 4 : 1, args);
+    launch(dev, stream, interleave_[v], n, v ? 2 : 1, args);
 }
 
 }  // namespace fg

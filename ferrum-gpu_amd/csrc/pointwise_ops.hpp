@@ -34,7 +34,7 @@ public:
                     hipStream_t stream) const;
 
 private:
-    // [0]: one element per thread step, any alignment; [1]: four, 16-byte accesses.
+    // [0]: one element per thread step, any alignment; [1]: 16-byte accesses.
     HipBackend::KernelHandle cmul_c64_[2] = {nullptr, nullptr};
     HipBackend::KernelHandle cmul_split_[2] = {nullptr, nullptr};
     HipBackend::KernelHandle deinterleave_[2] = {nullptr, nullptr};

@@ -261,3 +261,12 @@ def interleave(re, im) -> np.ndarray:
     out = np.empty(r.size, np.complex64)
     lib().or_interleave(_fptr(r), _fptr(m), _fptr(out), r.size)
     return out
+
+
+def transpose_square(arr, n: int) -> np.ndarray:
+    """In-place transpose of an n x n complex64 matrix (cpu_2d.rs:67-73's swap loop)."""
+    a = arr if (isinstance(arr, np.ndarray) and arr.dtype == np.complex64 and arr.flags.c_contiguous) \
+        else _as_c64(arr)
+    assert a.size == n * n
+    lib().or_transpose_square(_fptr(a), n)
+    return a

@@ -91,14 +91,14 @@ def test_code_object_is_embedded_for_gfx950():
         assert k.encode() in data, k
 
 
-POINTWISE = [f"fg_{op}_v{w}" for op in ("cmul_c64", "cmul_split", "deinterleave_c64", "interleave_c64")
-             for w in (1, 4)]
+POINTWISE = [f"fg_{op}_{w}" for op in ("cmul_c64", "cmul_split", "deinterleave_c64", "interleave_c64")
+             for w in ("vec", "elem")]
 
 
 def test_pointwise_kernels_are_instantiated():
     src = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
-    widths = re.findall(r"^FG_POINTWISE\((\d+)\)", src, flags=re.M)
-    assert sorted(widths) == ["1", "4"]
+    variants = re.findall(r"^FG_POINTWISE\((\w+), ", src, flags=re.M)
+    assert sorted(variants) == ["elem", "vec"]
     host = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "pointwise_ops.cpp")).read()
     for op in ("cmul_c64", "cmul_split", "deinterleave_c64", "interleave_c64"):
         assert f'"fg_{op}"' in host
