@@ -390,6 +390,33 @@ class OpWorkload:
         return f"full workload ({self.n} elements)"
 
 
+def host_path_rate(np, wl, dev, reps: int = 5):
+    """The same step through the host-array entry points (fft_1d_c2c_pow2 /
+    fft_2d_c2c_pow2 on numpy arrays): host-to-device copy, kernels, copy back.
+    Reported beside `value`, never as it."""
+    import ferrum_gpu
+
+    x = wl.x if wl.dims == 1 else wl.x.reshape(wl.batch, 1 << wl.log_n, 1 << wl.log_n)
+    fn = ferrum_gpu.fft.fft_1d_c2c_pow2 if wl.dims == 1 else ferrum_gpu.fft.fft_2d_c2c_pow2
+
+    def step():
+        y = x
+        for direction, normalize in wl.steps:
+            y = fn(y, wl.log_n, direction, normalize, device=dev)
+        return y
+
+    step()  # plan and staging buffers are created on the first call
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    return {"value": round(wl.algo_bytes / t / 1e9, 2), "unit": "GB/s", "ms_per_step": round(t * 1e3, 3),
+            "note": "numpy in, numpy out: includes both PCIe copies and the output allocation; median of "
+                    f"{reps} steps"}
+
+
 def cpu_baseline(np, wl, gpu_out, budget_s: float):
     """Time the CPU oracle on this host (a reported baseline, never the target)
     and use its result as the checker of the GPU output."""
@@ -438,6 +465,8 @@ def main() -> int:
     ap.add_argument("--workload", default="cfg3", choices=WORKLOADS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of single-thread CPU timing")
+    ap.add_argument("--no-host-path", action="store_true",
+                    help="skip timing the host-array entry points (PCIe-inclusive)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -514,6 +543,11 @@ def main() -> int:
     dev.sync()
     out = wl.output()
 
+    host = None
+    if not args.no_host_path and isinstance(wl, FftWorkload) and wl.layout == "interleaved":
+        host = host_path_rate(np, wl, dev)
+        log(f"host path {host['value']} GB/s ({host['ms_per_step']} ms per step)")
+
     base = multi = err = None
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -542,6 +576,7 @@ def main() -> int:
         "kernels_avg_ms": {key: round(v, 5) for key, v in kernel_ms.items()},
         "kernels_median_ms": {key: round(v, 5) for key, v in kernel_med.items()},
         "stream_copy_gbs": round(copy_gbs, 1),
+        "stream_copy_bytes": nbytes,
         "roofline": {
             "bound": "hbm",
             "kernel": dom_name,
@@ -555,6 +590,7 @@ def main() -> int:
         },
         "cpu_baseline": base,
         "cpu_baseline_all_cores": multi,
+        "host_path": host,
         ("max_abs_diff_vs_cpu" if wl.exact else "rel_l2_vs_cpu"): err,
         "device": info,
     }
