@@ -75,16 +75,19 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def make_input(np, size, seed, dist):
-    rng = np.random.default_rng(seed)
-    if dist == "normal":
-        re = rng.standard_normal(size, dtype=np.float32)
-        im = rng.standard_normal(size, dtype=np.float32)
-    else:
-        re = rng.uniform(-1, 1, size).astype(np.float32)
-        im = rng.uniform(-1, 1, size).astype(np.float32)
+def make_input(np, dev, size, seed, dist):
+    """`size` complex64 values from the library's seeded generator (splitmix64;
+    uniform in [-1, 1) or standard normal), generated on the device and copied
+    to the host, where the CPU baseline reads them."""
+    from ferrum_gpu import synthetic
+    from ferrum_gpu.hip import DeviceBuffer
+
+    buf = DeviceBuffer(dev, 8 * size)
+    (synthetic.normal if dist == "normal" else synthetic.uniform)(dev, buf, size, seed)
+    dev.sync()
     x = np.empty(size, np.complex64)
-    x.real, x.imag = re, im
+    buf.copy_to_host(x)
+    buf.free()
     return x
 
 
@@ -155,7 +158,7 @@ class FftWorkload:
         self.algo_bytes = 2 * self.nbytes_io * len(steps)
         self.flops = 5.0 * self.elems * (log_n if dims == 1 else 2 * log_n) * batch * len(steps)
         self.exact = False
-        self.x = make_input(np, n, seed, dist)
+        self.x = make_input(np, dev, n, seed, dist)
         self.plan = (ferrum_gpu.fft.Plan1D if dims == 1 else ferrum_gpu.fft.Plan2D)(log_n, batch, dev)
         kernels = self.plan.kernel_names()
         if layout == "split":
@@ -250,13 +253,13 @@ class OpWorkload:
         self.n = n
         self.exact = True
         self.flops = 6.0 * n if name.startswith("cmul") else 0.0
-        a = make_input(np, n, 3, "normal")
+        a = make_input(np, dev, n, 3, "normal")
         self.inputs = [a]
         # contiguous parts, prepared once for the split-layout kernels and the CPU leg
         self.parts = [np.ascontiguousarray(a.real), np.ascontiguousarray(a.imag)]
         f4 = 4 * n
         if name == "cmul":
-            b = make_input(np, n, 13, "normal")
+            b = make_input(np, dev, n, 13, "normal")
             self.inputs.append(b)
             self.d_in = [DeviceBuffer(dev, 8 * n), DeviceBuffer(dev, 8 * n)]
             self.d_in[0].copy_from_host(a)
@@ -265,7 +268,7 @@ class OpWorkload:
             self.algo_bytes = 24 * n
             kernel = "fg_cmul_c64_vec"
         elif name == "cmul_split":
-            b = make_input(np, n, 13, "normal")
+            b = make_input(np, dev, n, 13, "normal")
             self.inputs.append(b)
             self.parts += [np.ascontiguousarray(b.real), np.ascontiguousarray(b.imag)]
             self.d_in = [DeviceBuffer(dev, f4) for _ in range(4)]

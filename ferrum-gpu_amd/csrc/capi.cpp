@@ -595,6 +595,20 @@ int fg_interleave_c64(fg_device_t dev, const void* re, const void* im, void* out
     });
 }
 
+int fg_fill_uniform_c64(fg_device_t dev, void* d_out, size_t n, uint64_t seed, fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        dev->pointwise.fill_c64(dev->dev->handle(), d_out, n, seed, false, (hipStream_t)stream);
+    });
+}
+
+int fg_fill_normal_c64(fg_device_t dev, void* d_out, size_t n, uint64_t seed, fg_stream_t stream) {
+    return guarded([&] {
+        need(dev, "device");
+        dev->pointwise.fill_c64(dev->dev->handle(), d_out, n, seed, true, (hipStream_t)stream);
+    });
+}
+
 int fg_stream_copy(fg_device_t dev, const void* d_in, void* d_out, size_t bytes, fg_stream_t stream) {
     return guarded([&] {
         need(dev, "device");

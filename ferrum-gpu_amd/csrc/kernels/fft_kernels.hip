@@ -174,3 +174,14 @@ FG_TILE(10, 16, true, r)
 
 FG_POINTWISE(vec, 2, 4)
 FG_POINTWISE(elem, 1, 1)
+
+// ------------------------------------------------------------- synthetic data
+//
+// fg_fill_c64: n seeded complex64 values, uniform in [-1, 1) or standard normal
+// (the generator is defined in fill.hpp).  256-thread workgroups, grid-stride.
+#include "fill.hpp"
+
+extern "C" __global__ __launch_bounds__(256) void fg_fill_c64(float2* __restrict__ out, uint64_t n, uint64_t seed,
+                                                             uint32_t normal) {
+    fill_c64_body(out, n, seed, normal);
+}

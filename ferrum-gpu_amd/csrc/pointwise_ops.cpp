@@ -48,6 +48,7 @@ Pointwise::Pointwise(const HipBackend::Module& mod) {
         deinterleave_[v] = HipBackend::get_kernel(mod, ("fg_deinterleave_c64" + w).c_str());
         interleave_[v] = HipBackend::get_kernel(mod, ("fg_interleave_c64" + w).c_str());
     }
+    fill_ = HipBackend::get_kernel(mod, "fg_fill_c64");
 }
 
 void Pointwise::cmul_c64(const HipBackend::DeviceHandle& dev, const void* a, const void* b, void* out, uint64_t n,
@@ -104,6 +105,16 @@ void Pointwise::interleave(const HipBackend::DeviceHandle& dev, const void* re, 
     const int v = aligned16({re, im, out}) ? 1 : 0;
     void* args[] = {(void*)&re, (void*)&im, &out, &n};
     launch(dev, stream, interleave_[v], n, v ? 2 : 1, args);
+}
+
+void Pointwise::fill_c64(const HipBackend::DeviceHandle& dev, void* out, uint64_t n, uint64_t seed, bool normal,
+                         hipStream_t stream) const {
+    if (n == 0) return;
+    need_ptrs("fill_c64", {out});
+    if (reinterpret_cast<uintptr_t>(out) & 7u) invalid("fill_c64: out must be 8-byte aligned (complex64)");
+    uint32_t nrm = normal ? 1u : 0u;
+    void* args[] = {&out, &n, &seed, &nrm};
+    launch(dev, stream, fill_, n, 1, args);
 }
 
 }  // namespace fg

@@ -1,7 +1,8 @@
 // pointwise_ops.hpp -- host launchers of the elementwise complex kernels
 // (kernels/pointwise.hpp): the reference's cmul_interleaved, cmul_split,
 // deinterleave and interleave (kernels_body.rs:1612-1672), which it defines
-// for its split-layout study and never launches from the FFT path.
+// for its split-layout study and never launches from the FFT path; and the
+// seeded synthetic-data generator (kernels/fill.hpp).
 //
 // n counts complex elements.  Each launcher picks the 16-byte-access kernel
 // when every pointer is 16-byte aligned and the element-wise one otherwise;
@@ -32,6 +33,10 @@ public:
     // out[i] = (re[i], im[i]).  The output must not alias the inputs.
     void interleave(const HipBackend::DeviceHandle& dev, const void* re, const void* im, void* out, uint64_t n,
                     hipStream_t stream) const;
+    // n seeded complex64 values (kernels/fill.hpp): uniform in [-1, 1), or
+    // standard normal when `normal`.  out must be 8-byte aligned.
+    void fill_c64(const HipBackend::DeviceHandle& dev, void* out, uint64_t n, uint64_t seed, bool normal,
+                  hipStream_t stream) const;
 
 private:
     // [0]: one element per thread step, any alignment; [1]: 16-byte accesses.
@@ -39,6 +44,7 @@ private:
     HipBackend::KernelHandle cmul_split_[2] = {nullptr, nullptr};
     HipBackend::KernelHandle deinterleave_[2] = {nullptr, nullptr};
     HipBackend::KernelHandle interleave_[2] = {nullptr, nullptr};
+    HipBackend::KernelHandle fill_ = nullptr;
 };
 
 }  // namespace fg

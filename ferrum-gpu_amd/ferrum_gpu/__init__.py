@@ -5,6 +5,6 @@ Package layout mirrors the reference's python/ferrum_gpu/__init__.py:3-6
 """
 
 from ferrum_gpu._native import version
-from ferrum_gpu import hip, fft, pointwise
+from ferrum_gpu import hip, fft, pointwise, synthetic
 
-__all__ = ["version", "hip", "fft", "pointwise"]
+__all__ = ["version", "hip", "fft", "pointwise", "synthetic"]

@@ -117,6 +117,8 @@ _sig("fg_cmul_c64", _vp, _vp, _vp, _vp, _sz, _vp)
 _sig("fg_cmul_split", _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp)
 _sig("fg_deinterleave_c64", _vp, _vp, _vp, _vp, _sz, _vp)
 _sig("fg_interleave_c64", _vp, _vp, _vp, _vp, _sz, _vp)
+_sig("fg_fill_uniform_c64", _vp, _vp, _sz, ctypes.c_uint64, _vp)
+_sig("fg_fill_normal_c64", _vp, _vp, _sz, ctypes.c_uint64, _vp)
 
 
 def last_error() -> str:

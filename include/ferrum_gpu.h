@@ -222,6 +222,21 @@ FG_API int fg_deinterleave_c64(fg_device_t dev, const void *d_in, void *d_re, vo
 FG_API int fg_interleave_c64(fg_device_t dev, const void *d_re, const void *d_im, void *d_out, size_t n,
                              fg_stream_t stream);
 
+/* Seeded synthetic data: n complex64 values written to d_out (8-byte aligned),
+ * the same array for a given seed on any device, and equal to the CPU
+ * restatement in oracle/ (uniform: bit for bit).  Float j of the output
+ * (2i: real part of element i, 2i+1: imaginary part) uses the splitmix64
+ * output z(j) for the state seed + (j+1) * 0x9E3779B97F4A7C15:
+ *   uniform: (z(j) >> 40) * 2^-23 - 1, exactly representable, in [-1, 1);
+ *   normal:  Box-Muller in f64 on (z(2i), z(2i+1)), rounded to f32.
+ * The input generator the benchmark's configurations name ("seed = config
+ * index"); it replaces the reference's per-example input loops
+ * (e.g. examples/fft-1d-c2c/src/main.rs:131).  Stream-ordered, asynchronous. */
+FG_API int fg_fill_uniform_c64(fg_device_t dev, void *d_out, size_t n, uint64_t seed,
+                               fg_stream_t stream);
+FG_API int fg_fill_normal_c64(fg_device_t dev, void *d_out, size_t n, uint64_t seed,
+                              fg_stream_t stream);
+
 /* Streaming device copy of `bytes` (a multiple of 16) with the code object's
  * copy kernel: the HBM yardstick reported beside the FFT. */
 FG_API int fg_stream_copy(fg_device_t dev, const void *d_in, void *d_out, size_t bytes,

@@ -21,6 +21,9 @@ Parity pins (what checks each function against something it did not produce):
   or_cmul_interleaved / or_cmul_split -- numpy float32 elementwise products
       (each product and the sum rounded to f32), i*i = -1, z*conj(z) = |z|^2.
   or_deinterleave / or_interleave -- numpy .real/.imag views, and each other's inverse.
+  or_splitmix64_at / or_fill_* -- splitmix64's published first outputs for
+      seed 0, a pure-Python splitmix64, exact value grid and moments (uniform),
+      Box-Muller evaluated in Python floats and moments / tails (normal).
 """
 
 from __future__ import annotations
@@ -82,6 +85,10 @@ def lib() -> ctypes.CDLL:
             L.or_cmul_split.argtypes = [fp, fp, fp, fp, fp, fp, sz]
             L.or_deinterleave.argtypes = [fp, fp, fp, sz]
             L.or_interleave.argtypes = [fp, fp, fp, sz]
+            L.or_splitmix64_at.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+            L.or_splitmix64_at.restype = ctypes.c_uint64
+            L.or_fill_uniform_c64.argtypes = [fp, sz, ctypes.c_uint64]
+            L.or_fill_normal_c64.argtypes = [fp, sz, ctypes.c_uint64]
             _lib = L
     return _lib
 
@@ -270,3 +277,19 @@ def transpose_square(arr, n: int) -> np.ndarray:
     assert a.size == n * n
     lib().or_transpose_square(_fptr(a), n)
     return a
+
+
+def splitmix64_at(seed: int, j: int) -> int:
+    return int(lib().or_splitmix64_at(seed & (2**64 - 1), j & (2**64 - 1)))
+
+
+def fill_uniform_c64(n: int, seed: int) -> np.ndarray:
+    out = np.empty(n, np.complex64)
+    lib().or_fill_uniform_c64(_fptr(out), n, seed & (2**64 - 1))
+    return out
+
+
+def fill_normal_c64(n: int, seed: int) -> np.ndarray:
+    out = np.empty(n, np.complex64)
+    lib().or_fill_normal_c64(_fptr(out), n, seed & (2**64 - 1))
+    return out

@@ -442,3 +442,30 @@ void or_interleave(const float *re, const float *im, float *out, size_t n) {
         out[2 * i + 1] = im[i];
     }
 }
+
+/* ---- seeded synthetic data ------------------------------------------------- */
+
+uint64_t or_splitmix64_at(uint64_t seed, uint64_t j) {
+    uint64_t z = seed + (j + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void or_fill_uniform_c64(float *out, size_t n, uint64_t seed) {
+    for (size_t j = 0; j < 2 * n; ++j) {
+        uint32_t u = (uint32_t)(or_splitmix64_at(seed, j) >> 40);
+        out[j] = (float)u * 0x1p-23f - 1.0f;
+    }
+}
+
+void or_fill_normal_c64(float *out, size_t n, uint64_t seed) {
+    for (size_t i = 0; i < n; ++i) {
+        double u1 = (double)((or_splitmix64_at(seed, 2 * i) >> 11) + 1) * 0x1p-53;
+        double u2 = (double)(or_splitmix64_at(seed, 2 * i + 1) >> 11) * 0x1p-53;
+        double r = sqrt(-2.0 * log(u1));
+        double a = 6.283185307179586476925286766559 * u2;
+        out[2 * i] = (float)(r * cos(a));
+        out[2 * i + 1] = (float)(r * sin(a));
+    }
+}

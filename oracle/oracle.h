@@ -92,6 +92,14 @@ void or_deinterleave(const float *in, float *re, float *im, size_t n);
 /* out[2i], out[2i+1] = re[i], im[i] (interleave, :1661-1671). */
 void or_interleave(const float *re, const float *im, float *out, size_t n);
 
+/* ---- seeded synthetic data (the generator of the benchmark configurations) --
+ * Float j of the output uses splitmix64 at state seed + (j+1)*0x9E3779B97F4A7C15
+ * (Steele, Lea, Flood, OOPSLA 2014; Vigna's splitmix64.c constants).
+ * uniform: (z >> 40) * 2^-23 - 1; normal: f64 Box-Muller on (z(2i), z(2i+1)). */
+uint64_t or_splitmix64_at(uint64_t seed, uint64_t j);
+void or_fill_uniform_c64(float *out, size_t n, uint64_t seed);
+void or_fill_normal_c64(float *out, size_t n, uint64_t seed);
+
 #ifdef __cplusplus
 }
 #endif

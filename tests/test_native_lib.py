@@ -87,7 +87,8 @@ def test_code_object_is_embedded_for_gfx950():
     data = open(N.LIB_PATH, "rb").read()
     assert data.count(b"\x7fELF") >= 2
     assert b"gfx950" in data
-    for k in sorted(instantiated_kernels()) + ["fg_copy_f4", "fg_vector_add", "fg_transpose_c64"] + POINTWISE:
+    for k in sorted(instantiated_kernels()) + ["fg_copy_f4", "fg_vector_add", "fg_transpose_c64", "fg_fill_c64"] \
+            + POINTWISE:
         assert k.encode() in data, k
 
 
@@ -169,6 +170,9 @@ def test_split_and_pointwise_validation_without_device():
     for fn, nptrs in (("fg_cmul_c64", 3), ("fg_cmul_split", 6), ("fg_deinterleave_c64", 3),
                       ("fg_interleave_c64", 3)):
         rc = getattr(N.lib, fn)(None, *([None] * nptrs), 16, None)
+        assert rc == N.FG_ERR_INVALID_ARGUMENT and "device is null" in N.last_error(), fn
+    for fn in ("fg_fill_uniform_c64", "fg_fill_normal_c64"):
+        rc = getattr(N.lib, fn)(None, None, 16, 1, None)
         assert rc == N.FG_ERR_INVALID_ARGUMENT and "device is null" in N.last_error(), fn
 
 

@@ -382,3 +382,70 @@ def test_pointwise_checks_reject_planted_mistakes():
         assert not (np.array_equal(w.real, re) and np.array_equal(w.imag, im))
     sw_re, sw_im = oracle.deinterleave(a)
     assert not np.array_equal(oracle.interleave(sw_im, sw_re), a)   # re/im swapped
+
+
+# ------------------------------------------------------- synthetic data
+
+M64 = 2**64 - 1
+
+
+def _splitmix64_py(seed, j):
+    z = (seed + (j + 1) * 0x9E3779B97F4A7C15) & M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M64
+    return z ^ (z >> 31)
+
+
+def test_splitmix64_known_answers():
+    # the generator's published first outputs for seed 0 (splitmix64.c)
+    assert [oracle.splitmix64_at(0, j) for j in range(4)] == [
+        0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
+    rng = np.random.default_rng(0)
+    for seed, j in zip(rng.integers(0, 2**63, 20), rng.integers(0, 2**40, 20)):
+        assert oracle.splitmix64_at(int(seed), int(j)) == _splitmix64_py(int(seed), int(j))
+
+
+def test_fill_uniform_grid_and_moments():
+    x = oracle.fill_uniform_c64(1000, 7).view(np.float32)
+    exp = np.array([(_splitmix64_py(7, j) >> 40) * 2.0**-23 - 1 for j in range(2000)])
+    assert np.array_equal(x.astype(np.float64), exp)       # exact: 24-bit values on a 2^-23 grid
+    big = oracle.fill_uniform_c64(1 << 20, 1).view(np.float32).astype(np.float64)
+    assert big.min() >= -1 and big.max() < 1
+    assert abs(big.mean()) < 5 * np.sqrt(1 / 3 / big.size)
+    assert abs(big.var() - 1 / 3) < 0.002
+
+
+def test_fill_normal_box_muller_and_moments():
+    import math
+
+    x = oracle.fill_normal_c64(500, 3)
+    for i in range(500):
+        u1 = ((_splitmix64_py(3, 2 * i) >> 11) + 1) * 2.0**-53
+        u2 = (_splitmix64_py(3, 2 * i + 1) >> 11) * 2.0**-53
+        r = math.sqrt(-2.0 * math.log(u1))
+        assert x[i].real == np.float32(r * math.cos(2 * math.pi * u2))
+        assert x[i].imag == np.float32(r * math.sin(2 * math.pi * u2))
+    big = oracle.fill_normal_c64(1 << 20, 4).view(np.float32).astype(np.float64)
+    assert abs(big.mean()) < 5 / np.sqrt(big.size)
+    assert abs(big.var() - 1) < 0.005
+    assert abs(np.mean(np.abs(big) > 3) - 0.0026998) < 0.0005   # two-sided 3-sigma tail
+
+
+def test_fill_checks_reject_planted_mistakes():
+    known = 0xE220A8397B1DCDAF
+
+    def mix(z, s1=30, s2=27, s3=31):
+        z = ((z ^ (z >> s1)) * 0xBF58476D1CE4E5B9) & M64
+        z = ((z ^ (z >> s2)) * 0x94D049BB133111EB) & M64
+        return z ^ (z >> s3)
+
+    gamma = 0x9E3779B97F4A7C15
+    assert mix(gamma) == known                                   # the formula as restated
+    assert mix(0) != known                                       # counter j instead of j + 1
+    assert mix(gamma, 31, 27, 30) != known                       # shifts swapped
+    assert mix((gamma << 1) & M64) != known                      # stride doubled (interleaving bug)
+    # uniform mapping: a 23-bit field or a missing offset leaves the grid / range
+    z = oracle.splitmix64_at(7, 0)
+    good = (z >> 40) * 2.0**-23 - 1
+    assert oracle.fill_uniform_c64(1, 7).real[0] == np.float32(good)
+    assert (z >> 41) * 2.0**-23 - 1 != good and (z >> 40) * 2.0**-23 != good
