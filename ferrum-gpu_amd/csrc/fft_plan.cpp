@@ -62,8 +62,14 @@ std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e) {
         const uint32_t logl = s * log_e;
         const uint32_t logr = (s < nfull) ? log_e : rem;
         const uint64_t L = 1ull << logl, R = 1ull << logr, M = L * R;
+        // Row exponents (kernels/fft_stockham.hpp, tw_row_len): factored rows
+        // for radix 16 and 8, full rows below.
+        std::vector<uint64_t> ps;
+        if (R == 16) ps = {1, 2, 3, 4, 8, 12};
+        else if (R == 8) ps = {1, 2, 3, 4};
+        else for (uint64_t p = 0; p < R; ++p) ps.push_back(p);
         for (uint64_t k = 0; k < L; ++k)
-            for (uint64_t p = 0; p < R; ++p) {
+            for (uint64_t p : ps) {
                 const uint64_t e = (p * k) % M;
                 const double ang = 2.0 * M_PI * (double)e / (double)M;
                 t.push_back(Cf32{(float)cos(ang), (float)-sin(ang)});

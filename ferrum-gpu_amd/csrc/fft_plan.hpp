@@ -124,8 +124,10 @@ private:
 // ---- host-side pieces exposed for the CPU tests of the plan logic ----------
 
 // Mixed-radix Stockham table for N = 2^log_n with 2^log_e elements per thread:
-// per stage s >= 1 (L = 2^(s*log_e), R = that stage's radix) the block
-// [k][p] = W_{L*R}^{p*k}, k < L, p < R, computed in fp64 and rounded to f32.
+// per stage s >= 1 (L = 2^(s*log_e), R = that stage's radix) one row per k < L
+// of W_{L*R}^{p*k} for p in {1,2,3,4,8,12} (R = 16), {1,2,3,4} (R = 8) or
+// [0, R) (R <= 4), computed in fp64 and rounded to f32 (the kernels form the
+// remaining exponents as products; kernels/fft_stockham.hpp).
 std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e);
 // Two-level root table: [j] = W_4096^j, [4096 + j] = W_{2^24}^j, j < 4096.
 std::vector<Cf32> big_twiddles();

@@ -7,7 +7,7 @@
 // E = 2^LOGE elements held in VGPRs per thread:
 //   stage s, radix R, L = product of earlier radices, butterfly b = j*L + k:
 //     gather  src[b + p*(N/R)]              p in [0, R)
-//     twiddle t_p = W_{L*R}^{p*k} * src_p    (table; none when L == 1)
+//     twiddle t_p = W_{L*R}^{p*k} * src_p    (factored table; none when L == 1)
 //     DFT-R   X = DFT_R(t)
 //     scatter dst[j*L*R + k + q*L] = X_q    q in [0, R)
 // Thread t of a transform always gathers positions t + T*m (m in [0, E)), so
@@ -39,18 +39,61 @@ struct StockhamShape {
 // Padded LDS slot of logical position p.
 __device__ __forceinline__ int lds_pos(int p) { return p + (p >> 4); }
 
-// Offset (in complex entries) of stage s's block in the twiddle table built by
-// the host for this radix list; stage 0 has no block.  Block of stage s holds
-// L*R entries [k][p] = W_{L*R}^{p*k}.
+// Stage twiddle table, built by the host for this radix list (stage 0 has no
+// block).  The block of stage s (radix R, L = product of earlier radices,
+// M = L*R) holds one row per k < L of W_M^{p*k} for the exponents
+//   R = 16: p in {1, 2, 3, 4, 8, 12}   (the other nine are one product each,
+//           W^{k*p} = W^{k*(p & 3)} * W^{k*4*(p >> 2)}, following the 4 x 4
+//           split of the radix-16 butterfly)
+//   R = 8:  p in {1, 2, 3, 4}          (p = 5..7: W^{k*(p-4)} * W^{4k})
+//   R <= 4: p in [0, R)                (the full row)
+// Rows are 16-byte multiples so they load as float4 pairs.  The factored rows
+// keep a radix-16 stage's table at 6/16 of the full [k][p] block: at N = 4096
+// the last stage's 32 KB table fell out of L1 and cost 19 % of the kernel time
+// against 12 KB factored.
+__host__ __device__ constexpr int tw_row_len(int R) { return R == 16 ? 6 : (R == 8 ? 4 : R); }
+
 template <int LOGN, int LOGE>
 __host__ __device__ constexpr int stockham_tw_offset(int s) {
     int off = 0;
     for (int i = 1; i < s; ++i) {
         int logl = i * LOGE;
         int logr = (i < LOGN / LOGE) ? LOGE : (LOGN % LOGE);
-        off += 1 << (logl + logr);
+        off += (1 << logl) * tw_row_len(1 << logr);
     }
     return off;
+}
+
+// Multiplies input p of a radix-R butterfly by W^{p*k}, p >= 1, reading the
+// row w of the table above.
+template <int R>
+__device__ __forceinline__ void apply_stage_twiddles(float2* u, const float2* __restrict__ w) {
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    if constexpr (R == 16 || R == 8) {
+        const float4 a = w4[0], b = w4[1];
+        const float2 lo[4] = {make_float2(1.f, 0.f), make_float2(a.x, a.y), make_float2(a.z, a.w),
+                              make_float2(b.x, b.y)};
+        float2 hi[4] = {make_float2(1.f, 0.f), make_float2(b.z, b.w), make_float2(1.f, 0.f),
+                        make_float2(1.f, 0.f)};
+        if constexpr (R == 16) {
+            const float4 c = w4[2];
+            hi[2] = make_float2(c.x, c.y);
+            hi[3] = make_float2(c.z, c.w);
+        }
+#pragma unroll
+        for (int p = 1; p < R; ++p) {
+            const int pl = p & 3, ph = p >> 2;
+            const float2 wp = (pl == 0) ? hi[ph] : (ph == 0 ? lo[pl] : cmul(lo[pl], hi[ph]));
+            u[p] = cmul(u[p], wp);
+        }
+    } else if constexpr (R >= 2) {
+#pragma unroll
+        for (int p2 = 0; p2 < R / 2; ++p2) {
+            const float4 ww = w4[p2];
+            if (p2 > 0) u[2 * p2] = cmul(u[2 * p2], make_float2(ww.x, ww.y));
+            u[2 * p2 + 1] = cmul(u[2 * p2 + 1], make_float2(ww.z, ww.w));
+        }
+    }
 }
 
 // Processes one stage's butterflies for a thread: x holds the E gathered
@@ -72,17 +115,7 @@ __device__ __forceinline__ void stockham_stage_regs(float2* x, int t, const floa
         if constexpr (L > 1) {
             const int b = t + Sh::T * i;
             const int k = b & (L - 1);
-            const float2* w = tw + stockham_tw_offset<LOGN, LOGE>(S) + k * R;
-            if constexpr (R >= 2 && (R % 2) == 0) {
-                // Rows are R-aligned, so pairs of entries load as 16-byte vectors.
-                const float4* w4 = reinterpret_cast<const float4*>(w);
-#pragma unroll
-                for (int p2 = 0; p2 < R / 2; ++p2) {
-                    float4 ww = w4[p2];
-                    if (p2 > 0) u[2 * p2] = cmul(u[2 * p2], make_float2(ww.x, ww.y));
-                    u[2 * p2 + 1] = cmul(u[2 * p2 + 1], make_float2(ww.z, ww.w));
-                }
-            }
+            apply_stage_twiddles<R>(u, tw + stockham_tw_offset<LOGN, LOGE>(S) + k * tw_row_len(R));
         }
         Dft<R>::run(u);
 #pragma unroll

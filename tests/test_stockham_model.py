@@ -23,6 +23,11 @@ GEOM = {2: (2, 64), 3: (3, 64), 4: (4, 64), 5: (4, 32), 6: (4, 16), 7: (4, 8), 8
         9: (4, 2), 10: (4, 1), 11: (4, 1), 12: (4, 1)}
 
 
+def row_exponents(r):
+    """Exponents p of W^{p*k} stored per table row for a radix-r stage."""
+    return [1, 2, 3, 4, 8, 12] if r == 16 else [1, 2, 3, 4] if r == 8 else list(range(r))
+
+
 def stockham_table(log_n, log_e):
     nfull, rem = divmod(log_n, log_e)
     nst = nfull + (1 if rem else 0)
@@ -30,11 +35,29 @@ def stockham_table(log_n, log_e):
     for s in range(1, nst):
         logl, logr = s * log_e, (log_e if s < nfull else rem)
         L, R = 1 << logl, 1 << logr
-        k, p = np.meshgrid(np.arange(L), np.arange(R), indexing="ij")
+        ps = np.array(row_exponents(R))
+        k, p = np.meshgrid(np.arange(L), ps, indexing="ij")
         e = (p * k) % (L * R)
         out.append(np.exp(-2j * np.pi * e / (L * R)).astype(np.complex64).reshape(-1))
-        offs.append(offs[-1] + L * R)
+        offs.append(offs[-1] + L * len(ps))
     return (np.concatenate(out) if out else np.ones(1, np.complex64)), offs
+
+
+def stage_twiddles(tw, off, k, r):
+    """(T, r) twiddles W^{p*k} as the kernel forms them from the table rows at
+    off + k * row_len: a stored entry, or for radix 16 / 8 the product
+    W^{k*(p & 3)} * W^{k*4*(p >> 2)} of two stored entries."""
+    ps = row_exponents(r)
+    rows = tw[off + k[:, None] * len(ps) + np.arange(len(ps))[None, :]].astype(np.complex128)
+    if r not in (8, 16):
+        return rows
+    ent = {p: rows[:, i] for i, p in enumerate(ps)}
+    ent[0] = np.ones(k.shape, np.complex128)
+    cols = []
+    for p in range(r):
+        lo, hi = p & 3, 4 * (p >> 2)
+        cols.append(ent[p] if (lo == 0 or hi == 0) else ent[lo] * ent[hi])
+    return np.stack(cols, axis=1)
 
 
 def lds_pos(p):
@@ -62,7 +85,8 @@ def model(x, log_n, log_e):
             b = t + t_per * i
             k = b & (L - 1)
             if L > 1:
-                w = tw[offs[s] + k[:, None] * r + np.arange(r)[None, :]]
+                w = stage_twiddles(tw, offs[s], k, r)
+                assert offs[s] + (k.max() + 1) * len(row_exponents(r)) <= offs[s + 1] <= tw.size
                 u = u * w[None, :, :]
             y = np.fft.fft(u, axis=2)
             j = b >> (s * log_e)
@@ -103,11 +127,34 @@ def test_model_other_radices(log_n, log_e):
 
 
 def test_twiddle_rows_are_16_byte_aligned():
-    # The kernel loads table rows as float4 pairs: every row start k*R + offset
-    # must be even (8-byte entries -> 16-byte aligned).
+    # The kernel loads table rows as float4 pairs: every block offset and row
+    # length must be even (8-byte entries -> 16-byte aligned rows).
     for log_n, (log_e, _) in GEOM.items():
         _, offs = stockham_table(log_n, log_e)
         assert all(o % 2 == 0 for o in offs), log_n
+    assert all(len(row_exponents(r)) % 2 == 0 for r in (2, 4, 8, 16))
+
+
+def test_factored_twiddles_equal_the_full_rows():
+    # the products the kernel forms reproduce W^{p*k} for every p (to f32 rounding)
+    for log_n, log_e in [(12, 4), (11, 4), (10, 4), (9, 3), (12, 3)]:
+        tw, offs = stockham_table(log_n, log_e)
+        nfull, rem = divmod(log_n, log_e)
+        for s in range(1, nfull + (1 if rem else 0)):
+            L, R = 1 << (s * log_e), 1 << (log_e if s < nfull else rem)
+            k = np.arange(L)
+            w = stage_twiddles(tw, offs[s], k, R)
+            exact = np.exp(-2j * np.pi * ((k[:, None] * np.arange(R)[None, :]) % (L * R)) / (L * R))
+            assert np.max(np.abs(w - exact)) < 3e-7, (log_n, s)
+
+
+def test_stage_table_sizes():
+    # N = 4096, radix 16: stage 1 holds 16 rows, stage 2 256 rows of 6 entries
+    _, offs = stockham_table(12, 4)
+    assert offs == [0, 0, 16 * 6, 16 * 6 + 256 * 6]
+    # N = 1024 (16, 16, 4): 16 rows of 6, then 256 full rows of 4
+    _, offs = stockham_table(10, 4)
+    assert offs == [0, 0, 96, 96 + 1024]
 
 
 def test_staged_block_mapping_covers_each_element_once():
