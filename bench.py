@@ -14,7 +14,9 @@ A "step" is one pass of the workload over its batch (for cfg2: the forward and
 the normalised inverse transform).  W untimed warmup steps, then K timed steps
 between two device synchronisations.  Every kernel launch of the timed steps
 is followed by a HIP event recorded on the stream it runs on (plus one event
-before the first), which gives each kernel's duration for the roofline.
+before the first), which gives each kernel's duration for the roofline.  With
+--graph G the steps are recorded G at a time into a HIP graph and the timed
+steps run as K / G replays (for the launch-bound configurations 1 and 2).
 
 Prints ONE JSON line on stdout (progress goes to stderr):
   value        = algorithmic bytes per step / wall time per step, GB/s (FFT:
@@ -470,6 +472,9 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of single-thread CPU timing")
     ap.add_argument("--no-host-path", action="store_true",
                     help="skip timing the host-array entry points (PCIe-inclusive)")
+    ap.add_argument("--graph", type=int, default=0, metavar="G",
+                    help="record G steps into one HIP graph and time replays of it (for launch-bound "
+                         "workloads); --steps must be a multiple of G.  0: one host launch per kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -479,11 +484,14 @@ def main() -> int:
     if args.steps < 1 or args.warmup < 0:
         print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
+    if args.graph < 0 or (args.graph and args.steps % args.graph):
+        print("bench.py: --graph G needs G >= 1 dividing --steps", file=sys.stderr)
+        return 2
 
     import numpy as np
 
     from ferrum_gpu import _native as N
-    from ferrum_gpu.hip import Device, Event
+    from ferrum_gpu.hip import Capture, Device, Event
 
     dev = Device(0)
     info = dev.info()
@@ -494,31 +502,57 @@ def main() -> int:
     log(f"plan {wl.describe} kernels {wl.kernels}")
     launches = len(wl.launch_names)
 
-    for _ in range(args.warmup):
-        wl.run(stream)
-    dev.sync()
-    log(f"warmup {args.warmup} done")
-
-    # One event after every launch (plus one before the first): launch i ran
-    # between consecutive events.  One marker per launch costs ~2 us of gap per
-    # launch; a pair per launch measured ~6 us.
-    start = Event(dev)
-    evs = [[Event(dev) for _ in range(launches)] for _ in range(args.steps)]
-    dev.sync()
-    t0 = time.perf_counter()
-    start.record(stream)
-    for k in range(args.steps):
-        wl.run(stream, evs[k])
-    dev.sync()
-    wall = time.perf_counter() - t0
-    log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms")
-
     per_kernel: dict[str, list[float]] = {}
-    prev = start
-    for k in range(args.steps):
-        for i, key in enumerate(wl.launch_keys):
-            per_kernel.setdefault(key, []).append(prev.elapsed_ms(evs[k][i]))
-            prev = evs[k][i]
+    if not args.graph:
+        for _ in range(args.warmup):
+            wl.run(stream)
+        dev.sync()
+        log(f"warmup {args.warmup} done")
+
+        # One event after every launch (plus one before the first): launch i ran
+        # between consecutive events.  One marker per launch costs ~2 us of gap per
+        # launch; a pair per launch measured ~6 us.
+        start = Event(dev)
+        evs = [[Event(dev) for _ in range(launches)] for _ in range(args.steps)]
+        dev.sync()
+        t0 = time.perf_counter()
+        start.record(stream)
+        for k in range(args.steps):
+            wl.run(stream, evs[k])
+        dev.sync()
+        wall = time.perf_counter() - t0
+        log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms")
+        prev = start
+        for k in range(args.steps):
+            for i, key in enumerate(wl.launch_keys):
+                per_kernel.setdefault(key, []).append(prev.elapsed_ms(evs[k][i]))
+                prev = evs[k][i]
+    else:
+        # G steps per graph, replayed steps / G times between two events: the
+        # GPU time per launch is the replay time over all the launches in it
+        # (for single-kernel steps: the kernel plus the in-graph dispatch gap).
+        with Capture(dev, keep=[wl]) as cap:
+            for _ in range(args.graph):
+                wl.run(cap.stream)
+        graph = cap.graph
+        for _ in range(-(-args.warmup // args.graph)):
+            graph.launch(stream)
+        dev.sync()
+        log(f"warmup {args.warmup} steps as graph replays done ({graph.node_count} nodes per graph)")
+        start, end = Event(dev), Event(dev)
+        dev.sync()
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(args.steps // args.graph):
+            graph.launch(stream)
+        end.record(stream)
+        dev.sync()
+        wall = time.perf_counter() - t0
+        per_launch = start.elapsed_ms(end) / (args.steps * launches)
+        log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms as {args.steps // args.graph} graph replays")
+        for key in wl.launch_keys:
+            per_kernel.setdefault(key, []).extend([per_launch] * args.steps)
+        graph.destroy()
     kernel_ms = {key: float(np.mean(v)) for key, v in per_kernel.items()}
     kernel_med = {key: float(np.median(v)) for key, v in per_kernel.items()}
     dominant = max(kernel_ms, key=lambda key: kernel_ms[key] * len(per_kernel[key]))
@@ -597,6 +631,11 @@ def main() -> int:
         ("max_abs_diff_vs_cpu" if wl.exact else "rel_l2_vs_cpu"): err,
         "device": info,
     }
+    if args.graph:
+        result["launch_mode"] = f"HIP graph of {args.graph} steps per replay"
+    else:
+        result["launch_mode"] = "one host launch per kernel, one event after each"
+
     print(json.dumps(result), flush=True)
     return 0
 

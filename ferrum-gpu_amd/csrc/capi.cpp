@@ -6,6 +6,7 @@
 #include <hip/hip_runtime_api.h>
 #include <string.h>
 
+#include <atomic>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -55,6 +56,13 @@ struct fg_event {
 struct fg_fft_plan {
     std::unique_ptr<FftPlan> plan;
     fg_device* dev = nullptr;
+    std::atomic<int> graphs{0};  // live fg_graph objects that replay this plan
+};
+
+struct fg_graph {
+    HipBackend::Graph g;
+    fg_device* dev = nullptr;
+    fg_fft_plan* plan = nullptr;  // fg_fft_graph_create: the plan it replays (else null)
 };
 
 namespace {
@@ -424,7 +432,12 @@ int fg_fft_plan_2d(fg_device_t dev, uint32_t log_n, size_t batch, fg_fft_plan_t*
 }
 
 int fg_fft_plan_destroy(fg_fft_plan_t plan) {
-    return guarded([&] { delete plan; });
+    return guarded([&] {
+        if (plan && plan->graphs.load() > 0)
+            fg::invalid("plan still has " + std::to_string(plan->graphs.load()) +
+                        " graph(s); destroy them first");
+        delete plan;
+    });
 }
 
 int fg_fft_exec(fg_fft_plan_t plan, const void* d_in, void* d_out, int direction, int normalize,
@@ -463,6 +476,73 @@ int fg_fft_exec_events(fg_fft_plan_t plan, const void* d_in, void* d_out, int di
             evs[i] = events[i]->ev;
         }
         p.exec(d_in, d_out, parse_dir(direction), normalize != 0, (hipStream_t)stream, evs.data());
+    });
+}
+
+int fg_fft_graph_create(fg_fft_plan_t plan, const void* d_in, void* d_out, int direction, int normalize,
+                        int reps, fg_graph_t* out) {
+    return guarded([&] {
+        need(plan, "plan");
+        need(d_in, "d_in");
+        need(d_out, "d_out");
+        need(out, "out");
+        *out = nullptr;
+        const FftPlan& p = *plan->plan;
+        const Direction dir = parse_dir(direction);
+        if (reps < 1 || (int64_t)reps * p.launches() > 65536)
+            fg::invalid("fg_fft_graph_create: reps must be in [1, " + std::to_string(65536 / p.launches()) +
+                        "], got " + std::to_string(reps));
+        std::unique_ptr<fg_graph> g(new fg_graph);
+        g->g = HipBackend::capture(plan->dev->dev->handle(), [&](hipStream_t s) {
+            for (int r = 0; r < reps; ++r) p.exec(d_in, d_out, dir, normalize != 0, s);
+        });
+        g->dev = plan->dev;
+        g->plan = plan;
+        plan->graphs.fetch_add(1);
+        *out = g.release();
+    });
+}
+
+int fg_graph_capture_begin(fg_device_t dev, fg_stream_t* capture_stream) {
+    return guarded([&] {
+        need(dev, "device");
+        need(capture_stream, "capture_stream");
+        *capture_stream = (fg_stream_t)HipBackend::begin_capture(dev->dev->handle());
+    });
+}
+
+int fg_graph_capture_end(fg_device_t dev, fg_stream_t capture_stream, fg_graph_t* out) {
+    return guarded([&] {
+        need(dev, "device");
+        need(out, "out");
+        *out = nullptr;
+        std::unique_ptr<fg_graph> g(new fg_graph);
+        g->g = HipBackend::end_capture(dev->dev->handle(), (hipStream_t)capture_stream);
+        g->dev = dev;
+        *out = g.release();
+    });
+}
+
+int fg_graph_launch(fg_graph_t graph, fg_stream_t stream) {
+    return guarded([&] {
+        need(graph, "graph");
+        HipBackend::launch_graph(graph->dev->dev->handle(), graph->g, (hipStream_t)stream);
+    });
+}
+
+int fg_graph_node_count(fg_graph_t graph, size_t* nodes) {
+    return guarded([&] {
+        need(graph, "graph");
+        need(nodes, "nodes");
+        *nodes = graph->g->nodes;
+    });
+}
+
+int fg_graph_destroy(fg_graph_t graph) {
+    return guarded([&] {
+        if (!graph) return;
+        if (graph->plan) graph->plan->graphs.fetch_sub(1);
+        delete graph;
     });
 }
 

@@ -32,6 +32,14 @@ HipModuleState::~HipModuleState() {
     }
 }
 
+HipGraphState::~HipGraphState() {
+    (void)hipSetDevice(ordinal);
+    // A replay may still be in flight on any stream of the device.
+    if (exec) (void)hipDeviceSynchronize();
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+}
+
 int HipBackend::device_count() {
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
@@ -158,6 +166,53 @@ void HipBackend::destroy_stream(const DeviceHandle& dev, Stream s) {
     bind(dev);
     hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
     hip_check(hipStreamDestroy(s), "hipStreamDestroy");
+}
+
+HipBackend::Stream HipBackend::begin_capture(const DeviceHandle& dev) {
+    bind(dev);
+    hipStream_t s = nullptr;
+    hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    hipError_t began = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (began != hipSuccess) {
+        (void)hipStreamDestroy(s);
+        hip_check(began, "hipStreamBeginCapture");
+    }
+    return s;
+}
+
+HipBackend::Graph HipBackend::end_capture(const DeviceHandle& dev, Stream s) {
+    if (!s) invalid("end of capture on a null stream");
+    bind(dev);
+    auto g = std::make_shared<HipGraphState>();
+    g->ordinal = dev->ordinal;
+    hipError_t ended = hipStreamEndCapture(s, &g->graph);
+    (void)hipStreamDestroy(s);
+    hip_check(ended, "hipStreamEndCapture");
+    if (!g->graph) invalid("stream capture produced no graph");
+    hip_check(hipGraphGetNodes(g->graph, nullptr, &g->nodes), "hipGraphGetNodes");
+    hip_check(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    return g;
+}
+
+HipBackend::Graph HipBackend::capture(const DeviceHandle& dev, const std::function<void(Stream)>& record) {
+    hipStream_t s = begin_capture(dev);
+    try {
+        record(s);
+    } catch (...) {
+        hipGraph_t partial = nullptr;
+        (void)hipStreamEndCapture(s, &partial);
+        if (partial) (void)hipGraphDestroy(partial);
+        (void)hipStreamDestroy(s);
+        throw;
+    }
+    return end_capture(dev, s);
+}
+
+void HipBackend::launch_graph(const DeviceHandle& dev, const Graph& g, Stream stream) {
+    if (!g || !g->exec) invalid("launch of an empty graph");
+    if (g->ordinal != dev->ordinal) invalid("graph belongs to another device");
+    bind(dev);
+    hip_check(hipGraphLaunch(g->exec, stream ? stream : dev->stream), "hipGraphLaunch");
 }
 
 }  // namespace fg

@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <functional>
 #include <memory>
 #include <string>
 
@@ -34,11 +35,21 @@ struct HipModuleState {
     ~HipModuleState();
 };
 
+// A captured launch sequence: the graph and its executable instance.
+struct HipGraphState {
+    int ordinal = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    size_t nodes = 0;
+    ~HipGraphState();
+};
+
 struct HipBackend {
     using DeviceHandle = std::shared_ptr<HipDeviceState>;
     using Stream = hipStream_t;
     using Module = std::shared_ptr<HipModuleState>;
     using KernelHandle = hipFunction_t;
+    using Graph = std::shared_ptr<HipGraphState>;
 
     static BackendId id() { return BackendId::Hip; }
 
@@ -72,6 +83,20 @@ struct HipBackend {
 
     static Stream create_stream(const DeviceHandle& dev);
     static void destroy_stream(const DeviceHandle& dev, Stream s);
+
+    // Runs `record` on a private stream under thread-local stream capture and
+    // instantiates what it enqueued as one executable graph; nothing executes
+    // until launch_graph.  `record` may enqueue kernel launches and event
+    // records only (no memsets, no allocation).
+    static Graph capture(const DeviceHandle& dev, const std::function<void(Stream)>& record);
+    // The two halves of capture() for callers that record across calls:
+    // begin_capture returns a new stream in thread-local capture mode;
+    // end_capture ends it, destroys the stream and instantiates the graph
+    // (or throws, also destroying the stream, if the capture failed).
+    static Stream begin_capture(const DeviceHandle& dev);
+    static Graph end_capture(const DeviceHandle& dev, Stream s);
+    // Enqueues one replay of the graph on `stream` (nullptr: the default stream).
+    static void launch_graph(const DeviceHandle& dev, const Graph& g, Stream stream);
 };
 
 // Throws fg::Error(FG_ERR_DRIVER or a closer code) naming the failed call.

@@ -119,6 +119,12 @@ _sig("fg_deinterleave_c64", _vp, _vp, _vp, _vp, _sz, _vp)
 _sig("fg_interleave_c64", _vp, _vp, _vp, _vp, _sz, _vp)
 _sig("fg_fill_uniform_c64", _vp, _vp, _sz, ctypes.c_uint64, _vp)
 _sig("fg_fill_normal_c64", _vp, _vp, _sz, ctypes.c_uint64, _vp)
+_sig("fg_fft_graph_create", _vp, _vp, _vp, _i, _i, _i, _P(_vp))
+_sig("fg_graph_launch", _vp, _vp)
+_sig("fg_graph_capture_begin", _vp, _P(_vp))
+_sig("fg_graph_capture_end", _vp, _vp, _P(_vp))
+_sig("fg_graph_node_count", _vp, _P(_sz))
+_sig("fg_graph_destroy", _vp)
 
 
 def last_error() -> str:

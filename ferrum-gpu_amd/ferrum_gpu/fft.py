@@ -17,9 +17,9 @@ import operator
 import numpy as np
 
 from ferrum_gpu import _native as _n
-from ferrum_gpu.hip import Device, DeviceBuffer
+from ferrum_gpu.hip import Device, DeviceBuffer, Graph
 
-__all__ = ["fft_1d_c2c_pow2", "fft_2d_c2c_pow2", "fft2_c2c_pow2", "Plan1D", "Plan2D", "transpose",
+__all__ = ["fft_1d_c2c_pow2", "fft_2d_c2c_pow2", "fft2_c2c_pow2", "Plan1D", "Plan2D", "Graph", "transpose",
            "MIN_LOG_N", "MAX_LOG_N", "MIN_LOG_N_2D", "MAX_LOG_N_2D"]
 
 MIN_LOG_N, MAX_LOG_N = 2, 24
@@ -163,6 +163,18 @@ class _Plan:
         _n.check(_n.lib.fg_fft_exec_split(self._p, _ptr(in_re), _ptr(in_im), _ptr(out_re), _ptr(out_im), d,
                                           int(bool(normalize)), ctypes.c_void_p(stream or None)))
 
+    def capture_graph(self, d_in, d_out, direction="forward", normalize=False, reps: int = 1) -> "Graph":
+        """A HIP graph of ``reps`` back-to-back ``execute(d_in, d_out, ...)``
+        calls, replayed with one submission by ``Graph.launch``.  The graph
+        uses the buffers by address: keep them alive while it is launched
+        (the Graph holds a reference to this plan, and the plan cannot be
+        destroyed while the graph exists)."""
+        d = _direction(direction)
+        g = ctypes.c_void_p()
+        _n.check(_n.lib.fg_fft_graph_create(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),
+                                            int(reps), ctypes.byref(g)))
+        return Graph(self.device, g, keep=(self,))
+
     def kernel_names(self) -> list[str]:
         names = []
         for i in range(self.describe()["launches"]):
@@ -179,8 +191,9 @@ class _Plan:
         return {"launches": launches.value, "main_kernel": name.value.decode(), "workspace_bytes": ws.value}
 
     def destroy(self) -> None:
+        """Free the plan; refused (FerrumGpuError) while graphs of it exist."""
         if getattr(self, "_p", None) is not None and self._p.value:
-            _n.lib.fg_fft_plan_destroy(self._p)
+            _n.check(_n.lib.fg_fft_plan_destroy(self._p))
         self._p = ctypes.c_void_p()
 
     def __del__(self):  # pragma: no cover

@@ -16,7 +16,7 @@ import numpy as np
 
 from ferrum_gpu import _native as _n
 
-__all__ = ["Device", "DeviceBuffer", "Event", "Module", "Kernel", "device_count"]
+__all__ = ["Device", "DeviceBuffer", "Event", "Stream", "Graph", "Capture", "Module", "Kernel", "device_count"]
 
 
 def device_count() -> int:
@@ -114,6 +114,112 @@ class DeviceBuffer:
             self.free()
         except Exception:
             pass
+
+
+class Stream:
+    """A stream of the device at the default priority (Backend stream handle,
+    crates/ferrum-gpu-core/src/backend.rs:73-76); ``handle`` is what the
+    ``stream=`` arguments take."""
+
+    def __init__(self, device: Device):
+        s = ctypes.c_void_p()
+        _n.check(_n.lib.fg_stream_create(device.handle, ctypes.byref(s)))
+        self.device = device
+        self._s = s
+
+    @property
+    def handle(self) -> int:
+        return self._s.value or 0
+
+    def sync(self) -> None:
+        _n.check(_n.lib.fg_stream_sync(self.device.handle, self._s))
+
+    def destroy(self) -> None:
+        """Waits for the stream's work, then destroys it."""
+        if getattr(self, "_s", None) is not None and self._s.value:
+            _n.check(_n.lib.fg_stream_destroy(self.device.handle, self._s))
+        self._s = ctypes.c_void_p()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class Graph:
+    """An executable HIP graph: a captured sequence of stream-ordered calls
+    replayed by ``launch`` with one submission.  ``keep`` holds the objects
+    (plans) the recorded calls use, so they outlive the graph."""
+
+    def __init__(self, device: Device, handle: ctypes.c_void_p, keep=()):
+        self.device = device
+        self._g = handle
+        self._keep = tuple(keep)
+
+    def launch(self, stream: int = 0) -> None:
+        """Enqueue one replay on ``stream`` (0: the device default stream)."""
+        if not self._g.value:
+            raise ValueError("graph is destroyed")
+        _n.check(_n.lib.fg_graph_launch(self._g, ctypes.c_void_p(stream or None)))
+
+    @property
+    def node_count(self) -> int:
+        n = ctypes.c_size_t()
+        _n.check(_n.lib.fg_graph_node_count(self._g, ctypes.byref(n)))
+        return n.value
+
+    def destroy(self) -> None:
+        """Waits for the device's work, then frees the graph."""
+        if getattr(self, "_g", None) is not None and self._g.value:
+            _n.check(_n.lib.fg_graph_destroy(self._g))
+        self._g = ctypes.c_void_p()
+        self._keep = ()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class Capture:
+    """Records the stream-ordered calls made on ``stream`` inside the block
+    into a Graph instead of running them::
+
+        with Capture(dev, keep=[plan]) as cap:
+            plan.execute(a, b, "forward", stream=cap.stream)
+            plan.execute(b, c, "inverse", True, stream=cap.stream)
+        cap.graph.launch()
+
+    Calls must come from the capturing thread; the caller keeps the buffers
+    the recorded calls use alive while the graph is launched."""
+
+    def __init__(self, device: Device, keep=()):
+        self.device = device
+        self._keep = tuple(keep)
+        self._s = ctypes.c_void_p()
+        self.graph: Graph | None = None
+
+    @property
+    def stream(self) -> int:
+        return self._s.value or 0
+
+    def __enter__(self) -> "Capture":
+        _n.check(_n.lib.fg_graph_capture_begin(self.device.handle, ctypes.byref(self._s)))
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> bool:
+        g = ctypes.c_void_p()
+        rc = _n.lib.fg_graph_capture_end(self.device.handle, self._s, ctypes.byref(g))
+        self._s = ctypes.c_void_p()
+        if exc_type is not None:
+            if rc == _n.FG_OK and g.value:
+                _n.lib.fg_graph_destroy(g)
+            return False
+        _n.check(rc)
+        self.graph = Graph(self.device, g, self._keep)
+        return False
 
 
 class Event:

@@ -156,6 +156,38 @@ FG_API int fg_fft_exec(fg_fft_plan_t plan, const void *d_in, void *d_out, int di
  * per launch keeps the marker overhead between back-to-back launches to one. */
 FG_API int fg_fft_exec_events(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction,
                               int normalize, fg_stream_t stream, fg_event_t *events, int nevents);
+/* HIP graphs of plan executions.  No counterpart in the reference, whose host
+ * runner submits every kernel from the host on each call
+ * (crates/ferrum-gpu-py/src/lib.rs:142-233); for callers whose loop is bound
+ * by launch latency (small batches, serving loops).
+ * fg_fft_graph_create captures `reps` back-to-back fg_fft_exec(plan, d_in,
+ * d_out, direction, normalize) into one executable graph (reps * launches
+ * kernel nodes, at most 65536; kernel launches only: no memset, copy or
+ * allocation nodes).  Nothing runs at creation.  The graph keeps d_in, d_out
+ * and the plan's tables and workspace by address: the buffers must stay
+ * allocated while it is used, and fg_fft_plan_destroy refuses a plan that
+ * still has graphs.  fg_graph_launch enqueues one replay on `stream` (NULL =
+ * the device default stream), stream-ordered and asynchronous; replays on one
+ * stream run one after another, and replays that overlap on different streams
+ * race on the same buffers. */
+typedef struct fg_graph *fg_graph_t;
+FG_API int fg_fft_graph_create(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction,
+                               int normalize, int reps, fg_graph_t *out);
+FG_API int fg_graph_launch(fg_graph_t graph, fg_stream_t stream);
+/* General capture: fg_graph_capture_begin returns a new stream of the device
+ * in thread-local capture mode; stream-ordered fg_* calls made on it from the
+ * calling thread (fg_fft_exec, the elementwise kernels, fg_transpose_c64, ...)
+ * are recorded instead of run, and fg_graph_capture_end turns them into one
+ * graph and destroys the stream.  Make calls that allocate (the first
+ * fg_fft_exec_split of a multi-launch plan) once before capturing.  The caller
+ * keeps every plan and buffer the recorded calls use alive while the graph is
+ * launched.  fg_graph_capture_end must be called once per begin, also after
+ * a failed call. */
+FG_API int fg_graph_capture_begin(fg_device_t dev, fg_stream_t *capture_stream);
+FG_API int fg_graph_capture_end(fg_device_t dev, fg_stream_t capture_stream, fg_graph_t *out);
+/* Number of nodes in the captured graph. */
+FG_API int fg_graph_node_count(fg_graph_t graph, size_t *nodes);
+FG_API int fg_graph_destroy(fg_graph_t graph);
 /* Kernel name of launch `index` of an execution. */
 FG_API int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char *name, size_t cap);
 /* Number of kernel launches per execution and the name of the kernel that

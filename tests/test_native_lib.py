@@ -176,6 +176,21 @@ def test_split_and_pointwise_validation_without_device():
         assert rc == N.FG_ERR_INVALID_ARGUMENT and "device is null" in N.last_error(), fn
 
 
+def test_graph_validation_without_device():
+    out = ctypes.c_void_p()
+    rc = N.lib.fg_fft_graph_create(None, None, None, 1, 0, 1, ctypes.byref(out))
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "plan is null" in N.last_error()
+    rc = N.lib.fg_graph_launch(None, None)
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "graph is null" in N.last_error()
+    rc = N.lib.fg_graph_node_count(None, ctypes.byref(ctypes.c_size_t()))
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "graph is null" in N.last_error()
+    rc = N.lib.fg_graph_capture_begin(None, ctypes.byref(ctypes.c_void_p()))
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "device is null" in N.last_error()
+    rc = N.lib.fg_graph_capture_end(None, None, ctypes.byref(out))
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "device is null" in N.last_error()
+    assert N.lib.fg_graph_destroy(None) == N.FG_OK
+
+
 def test_last_error_is_thread_local():
     import threading
 
