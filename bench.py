@@ -176,11 +176,18 @@ class FftWorkload:
             self.bufs = [DeviceBuffer(dev, self.nbytes_io) for _ in range(len(steps) + 1)]
             self.bufs[0].copy_from_host(self.x)
             self.copy_bufs = (self.bufs[0], self.bufs[1], self.nbytes_io)
+        self.describe = self.plan.describe()
+        # Multi-launch plans run pass after pass over one chunk of transforms
+        # (images) at a time: launch i is pass i % passes of a chunk, and each
+        # launch reads and writes one chunk once.
+        passes = 1 if layout == "split" else self.describe["passes"]
+        units = batch if layout == "split" else self.describe["units_per_chunk"]
+        if batch % units:
+            raise SystemExit("bench.py: workload batch is not a whole number of chunks")
         self.kernels = kernels
         self.launch_names = kernels * len(steps)
-        self.launch_keys = [f"{i}:{k}" for _ in steps for i, k in enumerate(kernels)]
-        self.bytes_per_launch = 2 * self.nbytes_io  # each pass reads and writes the whole array once
-        self.describe = self.plan.describe()
+        self.launch_keys = [f"{i % passes}:{k}" for _ in steps for i, k in enumerate(kernels)]
+        self.bytes_per_launch = 16 * self.elems * units
 
     def run(self, stream, events=None):
         L = len(self.kernels)

@@ -559,6 +559,28 @@ int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char* name, size_t cap) {
     });
 }
 
+int fg_fft_set_chunk_bytes(size_t bytes) {
+    return guarded([&] { fg::set_chunk_limit_bytes(bytes); });
+}
+
+int fg_fft_get_chunk_bytes(size_t* bytes) {
+    return guarded([&] {
+        need(bytes, "bytes");
+        *bytes = fg::chunk_limit_bytes();
+    });
+}
+
+int fg_fft_plan_chunking(fg_fft_plan_t plan, int* passes, size_t* units_per_chunk, int* chunks, int* cached) {
+    return guarded([&] {
+        need(plan, "plan");
+        const FftPlan& p = *plan->plan;
+        if (passes) *passes = p.passes();
+        if (units_per_chunk) *units_per_chunk = p.chunk_units();
+        if (chunks) *chunks = (int)p.chunks();
+        if (cached) *cached = p.cache_resident() ? 1 : 0;
+    });
+}
+
 int fg_fft_plan_describe(fg_fft_plan_t plan, int* launches, char* main_kernel, size_t cap,
                          size_t* workspace_bytes) {
     return guarded([&] {

@@ -6,6 +6,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <fstream>
 #include <iterator>
 
@@ -115,10 +116,52 @@ bool split_2d_columns(uint32_t log_rows) { return log_rows > 10; }
 
 namespace {
 
+size_t initial_chunk_limit() {
+    // 128 MiB: a chunk's intermediate array plus the streams in and out of it
+    // stay within the 256 MB Infinity Cache.  Measured on gfx950 with a copy
+    // over a working set of 2 x S: 8.4 TB/s at S = 128 MiB, 6.1 TB/s at 160.
+    size_t mib = 128;
+    if (const char* e = getenv("FERRUM_GPU_CHUNK_MIB")) {
+        char* end = nullptr;
+        const unsigned long long v = strtoull(e, &end, 10);
+        if (end != e && *end == 0 && v <= (1ull << 20)) mib = (size_t)v;
+    }
+    return mib << 20;
+}
+
+std::atomic<size_t>& chunk_limit_ref() {
+    static std::atomic<size_t> limit{initial_chunk_limit()};
+    return limit;
+}
+
+}  // namespace
+
+size_t chunk_limit_bytes() { return chunk_limit_ref().load(); }
+void set_chunk_limit_bytes(size_t bytes) { chunk_limit_ref().store(bytes); }
+
+size_t chunk_units_for(uint64_t unit_bytes, size_t batch, size_t limit, bool* cached) {
+    if (limit == 0 || unit_bytes == 0 || unit_bytes > limit) {
+        *cached = false;
+        return batch;
+    }
+    *cached = true;
+    return (size_t)std::min<uint64_t>(limit / unit_bytes, batch);
+}
+
+void FftPlan::choose_chunk() { chunk_ = chunk_units_for(8ull * elems(), batch_, chunk_limit_bytes(), &cached_); }
+
+const char* FftPlan::policy(size_t i, size_t n) const {
+    if (!cached_) return "";
+    if (i == 0) return "_sc";
+    return i + 1 == n ? "_cs" : "_cc";
+}
+
+namespace {
+
 uint32_t elems_per_thread_log(uint32_t log_l) { return log_l < 4 ? log_l : 4; }
 
-std::string tile_name(uint32_t log_l, uint32_t g, bool rowwise) {
-    return "fg_tile_l" + std::to_string(log_l) + "_g" + std::to_string(g) + (rowwise ? "_r" : "_c");
+std::string tile_name(uint32_t log_l, uint32_t g, bool rowwise, const char* policy) {
+    return "fg_tile_l" + std::to_string(log_l) + "_g" + std::to_string(g) + (rowwise ? "_r" : "_c") + policy;
 }
 
 }  // namespace
@@ -142,38 +185,39 @@ const void* FftPlan::big_table() {
     return big_.data();
 }
 
-void FftPlan::add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t count, Buf src, Buf dst) {
+void FftPlan::add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t per_unit, Buf src, Buf dst,
+                           const char* policy) {
     const StockhamGeom g = kStockham[log_l];
     Step s;
-    s.name = "fg_fft_n" + std::to_string(log_l);
+    s.name = "fg_fft_n" + std::to_string(log_l) + policy;
     s.fn = HipBackend::get_kernel(mod, s.name.c_str());
-    const uint64_t blocks = (count + g.fpb - 1) / g.fpb;
+    const uint64_t blocks = (per_unit * chunk_ + g.fpb - 1) / g.fpb;
     if (blocks > 0x7fffffffull) invalid("batch too large for one launch");
-    s.grid = Dim3((uint32_t)blocks);
     s.block = Dim3(((1u << log_l) >> g.log_e) * g.fpb);
+    s.fpb = g.fpb;
     s.src = src;
     s.dst = dst;
     s.tw = stage_table(log_l);
-    s.count = count;
+    s.per_unit = per_unit;
     steps_.push_back(s);
 }
 
 void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g, bool rowwise,
-                       const TileGeom& geom, uint64_t tiles, Buf src, Buf dst) {
+                       const TileGeom& geom, uint64_t tiles_per_unit, Buf src, Buf dst, const char* policy) {
     // The kernel reads columns at stride 1 (column-wise) or elements at stride
     // 1 (row-wise) and always writes columns at stride 1.
     if ((rowwise ? geom.ies : geom.ics) != 1 || geom.ocs != 1) fail(FG_ERR_INTERNAL, "tile geometry not unit-stride");
-    if (tiles == 0 || tiles > 0x7fffffffull) invalid("too many tiles for one launch");
+    if (tiles_per_unit == 0 || tiles_per_unit * chunk_ > 0x7fffffffull) invalid("too many tiles for one launch");
     Step s;
     s.tile = true;
-    s.name = tile_name(log_l, g, rowwise);
+    s.name = tile_name(log_l, g, rowwise, policy);
     s.fn = HipBackend::get_kernel(mod, s.name.c_str());
-    s.grid = Dim3((uint32_t)tiles);
     s.block = Dim3(g * ((1u << log_l) >> elems_per_thread_log(log_l)));
     s.src = src;
     s.dst = dst;
     s.tw = stage_table(log_l);
     s.geom = geom;
+    s.per_unit = tiles_per_unit;
     steps_.push_back(s);
 }
 
@@ -185,7 +229,7 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
     if (batch == 0) invalid("batch must be positive");
     if (log_n <= kMaxLogNSingle) {
         std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::Stockham1D, log_n, 0, batch));
-        p->add_stockham(mod, log_n, batch, Buf::In, Buf::Out);
+        p->add_stockham(mod, log_n, 1, Buf::In, Buf::Out);
         p->main_kernel_ = p->steps_[0].name;
         p->split_fn_ = HipBackend::get_kernel(mod, (p->main_kernel_ + "_split").c_str());
         p->pw_ = Pointwise(mod);
@@ -201,7 +245,8 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
     S[0] = N;
     for (size_t i = 1; i <= P; ++i) S[i] = S[i - 1] >> logs[i - 1];
     if (N * batch > (1ull << 40)) invalid("transform too large");
-    p->work_ = dev.alloc<Cf32>(N * batch);
+    p->choose_chunk();
+    p->work_ = dev.alloc<Cf32>(N * p->chunk_);
     const void* big = p->big_table();
     (void)big;
     // Passes 1..P-1: DFT over digit i for every value of the faster digits
@@ -223,8 +268,8 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         t.tw0 = g;
         t.tw1 = 0;
         t.log_m = (uint32_t)__builtin_ctzll(S[i - 1]);
-        p->add_tile(mod, log_l, g, false, t, (uint64_t)t.t0n * t.t1n * batch, i == 1 ? Buf::In : Buf::Work,
-                    Buf::Work);
+        p->add_tile(mod, log_l, g, false, t, (uint64_t)t.t0n * t.t1n, i == 1 ? Buf::In : Buf::Work, Buf::Work,
+                    p->policy(i - 1, P));
     }
     // Pass P: contiguous rows of N_P for each (k_1, k_2..k_{P-1}); G' rows of
     // consecutive k_1 per tile, stored to the digit-reversed output position
@@ -247,7 +292,7 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         t.os2 = N;
         t.ocs = 1;
         t.oes = N / L;
-        p->add_tile(mod, log_l, g, true, t, (uint64_t)t.t0n * t.t1n * batch, Buf::Work, Buf::Out);
+        p->add_tile(mod, log_l, g, true, t, (uint64_t)t.t0n * t.t1n, Buf::Work, Buf::Out, p->policy(P - 1, P));
     }
     p->main_kernel_ = p->steps_[0].name;
     p->pw_ = Pointwise(mod);
@@ -264,9 +309,11 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::TwoD, log_cols, log_rows, batch));
     const uint64_t R = 1ull << log_rows, C = 1ull << log_cols, RC = R * C;
     const bool split = split_2d_columns(log_rows);
-    if (split) p->work_ = dev.alloc<Cf32>(RC * batch);
-    // Row pass (the reference's K1 row FFT, py lib.rs:325-336): R*batch rows of C.
-    p->add_stockham(mod, log_cols, R * batch, Buf::In, split ? Buf::Work : Buf::Out);
+    const size_t npass = split ? 3 : 2;
+    p->choose_chunk();
+    if (split) p->work_ = dev.alloc<Cf32>(RC * p->chunk_);
+    // Row pass (the reference's K1 row FFT, py lib.rs:325-336): R rows of C per image.
+    p->add_stockham(mod, log_cols, R, Buf::In, split ? Buf::Work : Buf::Out, p->policy(0, npass));
     if (!split) {
         // Column pass, in place: G adjacent columns of length R per tile.
         const uint32_t g = (uint32_t)std::min<uint64_t>(tile_columns(log_rows), C);
@@ -278,7 +325,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         t.is2 = t.os2 = RC;
         t.ics = t.ocs = 1;
         t.ies = t.oes = C;
-        p->add_tile(mod, log_rows, g, false, t, (uint64_t)t.t0n * batch, Buf::Out, Buf::Out);
+        p->add_tile(mod, log_rows, g, false, t, (uint64_t)t.t0n, Buf::Out, Buf::Out, p->policy(1, npass));
     } else {
         // Column FFT of length R = R_1 * R_2 over the slow axis, as two column
         // passes over G = min(64, C) adjacent columns.
@@ -298,7 +345,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         a.tw1 = 1;
         a.log_m = log_rows;
         p->big_table();
-        p->add_tile(mod, l1, g, false, a, (uint64_t)a.t0n * a.t1n * batch, Buf::Work, Buf::Work);
+        p->add_tile(mod, l1, g, false, a, (uint64_t)a.t0n * a.t1n, Buf::Work, Buf::Work, p->policy(1, npass));
         TileGeom b{};
         b.t0n = (uint32_t)(C / g);
         b.t1n = (uint32_t)R1;
@@ -312,7 +359,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         b.os2 = RC;
         b.ocs = 1;
         b.oes = R1 * C;
-        p->add_tile(mod, l2, g, false, b, (uint64_t)b.t0n * b.t1n * batch, Buf::Work, Buf::Out);
+        p->add_tile(mod, l2, g, false, b, (uint64_t)b.t0n * b.t1n, Buf::Work, Buf::Out, p->policy(2, npass));
     }
     p->main_kernel_ = p->steps_.back().name;
     p->pw_ = Pointwise(mod);
@@ -342,7 +389,8 @@ void transpose_c64(HipDevice& dev, const HipBackend::Module& mod, const void* in
 
 std::vector<std::string> FftPlan::kernel_names() const {
     std::vector<std::string> v;
-    for (const Step& s : steps_) v.push_back(s.name);
+    for (size_t c = 0; c < chunks(); ++c)
+        for (const Step& s : steps_) v.push_back(s.name);
     return v;
 }
 
@@ -360,34 +408,43 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
     const float scale = scale_for(dir, normalize);
     const void* big = big_.data();
     hipStream_t st = stream ? stream : dev_->default_stream();
-    for (size_t i = 0; i < steps_.size(); ++i) {
-        const Step& s = steps_[i];
-        uint32_t flags = 0;
-        if (inverse && i == 0) flags |= FG_PASS_CONJ_IN;
-        if (inverse && i + 1 == steps_.size()) flags |= FG_PASS_CONJ_SCALE_OUT;
+    const uint64_t unit = elems();
+    size_t launch = 0;
+    for (uint64_t u0 = 0; u0 < batch_; u0 += chunk_) {
+        const uint64_t units = std::min<uint64_t>(chunk_, batch_ - u0);
+        // The caller's arrays are offset to the chunk; the workspace holds one chunk.
         auto bind = [&](Buf b) -> void* {
             switch (b) {
-                case Buf::In: return const_cast<void*>(in);
-                case Buf::Out: return out;
+                case Buf::In: return const_cast<Cf32*>(static_cast<const Cf32*>(in)) + u0 * unit;
+                case Buf::Out: return static_cast<Cf32*>(out) + u0 * unit;
                 default: return work_.data();
             }
         };
-        void* src = bind(s.src);
-        void* dst = bind(s.dst);
-        const void* tw = s.tw;
-        if (!s.tile) {
-            uint64_t count = s.count;
-            float sc = scale;
-            void* args[] = {&src, &dst, (void*)&tw, &count, &sc, &flags};
-            HipBackend::launch(dev_->handle(), stream, s.fn, s.grid, s.block, 0, args);
-        } else {
-            TileGeom g = s.geom;
-            g.flags = flags;
-            g.scale = scale;
-            void* args[] = {&src, &dst, (void*)&tw, (void*)&big, &g};
-            HipBackend::launch(dev_->handle(), stream, s.fn, s.grid, s.block, 0, args);
+        for (size_t i = 0; i < steps_.size(); ++i) {
+            const Step& s = steps_[i];
+            uint32_t flags = 0;
+            if (inverse && i == 0) flags |= FG_PASS_CONJ_IN;
+            if (inverse && i + 1 == steps_.size()) flags |= FG_PASS_CONJ_SCALE_OUT;
+            void* src = bind(s.src);
+            void* dst = bind(s.dst);
+            const void* tw = s.tw;
+            if (!s.tile) {
+                uint64_t count = s.per_unit * units;
+                float sc = scale;
+                void* args[] = {&src, &dst, (void*)&tw, &count, &sc, &flags};
+                const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
+                HipBackend::launch(dev_->handle(), stream, s.fn, grid, s.block, 0, args);
+            } else {
+                TileGeom g = s.geom;
+                g.flags = flags;
+                g.scale = scale;
+                void* args[] = {&src, &dst, (void*)&tw, (void*)&big, &g};
+                HipBackend::launch(dev_->handle(), stream, s.fn, Dim3((uint32_t)(s.per_unit * units)), s.block, 0,
+                                   args);
+            }
+            if (events) hip_check(hipEventRecord(events[launch], st), "hipEventRecord");
+            ++launch;
         }
-        if (events) hip_check(hipEventRecord(events[i], st), "hipEventRecord");
     }
 }
 
@@ -409,9 +466,10 @@ void FftPlan::exec_split(const void* in_re, const void* in_im, void* out_re, voi
         uint32_t flags = dir == Direction::Inverse ? (FG_PASS_CONJ_IN | FG_PASS_CONJ_SCALE_OUT) : 0u;
         float sc = scale_for(dir, normalize);
         const void* tw = s.tw;
-        uint64_t count = s.count;
+        uint64_t count = s.per_unit * batch_;
         void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, &count, &sc, &flags};
-        HipBackend::launch(dev_->handle(), stream, split_fn_, s.grid, s.block, 0, args);
+        const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
+        HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
         return;
     }
     {

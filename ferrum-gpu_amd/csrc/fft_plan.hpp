@@ -51,6 +51,9 @@ public:
                                             uint32_t log_cols, size_t batch);
 
     // Forward or inverse transform of batch transforms from in to out (may alias).
+    // Multi-launch plans run chunk by chunk: every pass over chunk_units()
+    // transforms (images) before the next chunk, so a chunk's intermediate
+    // array stays in the Infinity Cache (chunk_bytes()).
     // With `events` (launches() of them), events[i] is recorded on the stream
     // right after launch i.
     void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
@@ -73,7 +76,13 @@ public:
     size_t batch() const { return batch_; }
     // Complex elements per transform (N, or N*N for 2D).
     size_t elems() const { return size_t(1) << (log_n_ + log_rows_); }
-    int launches() const { return (int)steps_.size(); }
+    // Kernel launches per execution: passes() per chunk, chunks() chunks.
+    int launches() const { return (int)(steps_.size() * chunks()); }
+    int passes() const { return (int)steps_.size(); }
+    size_t chunk_units() const { return chunk_; }
+    size_t chunks() const { return (batch_ + chunk_ - 1) / chunk_; }
+    // Whether intermediate arrays are kept cached (chunk fits the cache limit).
+    bool cache_resident() const { return cached_; }
     const std::string& main_kernel() const { return main_kernel_; }
     size_t workspace_bytes() const { return work_.bytes(); }
     // Kernel names in launch order.
@@ -87,29 +96,39 @@ private:
         bool tile = false;                      // tile pass (else single-pass Stockham)
         std::string name;
         HipBackend::KernelHandle fn = nullptr;
-        Dim3 grid, block;
+        Dim3 block;
+        uint32_t fpb = 1;                       // Stockham: transforms per workgroup
         Buf src = Buf::In, dst = Buf::Out;
         const void* tw = nullptr;               // Stockham stage table
-        uint64_t count = 0;                     // Stockham: transforms in the launch
+        // Per unit (one transform, or one 2D image): Stockham transforms, or
+        // tiles of a tile pass.  A launch over u units has per_unit * u of them.
+        uint64_t per_unit = 0;
         TileGeom geom{};                        // tile: addressing (flags/scale set at exec)
     };
 
     FftPlan(HipDevice& dev, Kind kind, uint32_t log_n, uint32_t log_rows, size_t batch)
-        : dev_(&dev), kind_(kind), log_n_(log_n), log_rows_(log_rows), batch_(batch) {}
+        : dev_(&dev), kind_(kind), log_n_(log_n), log_rows_(log_rows), batch_(batch), chunk_(batch) {}
 
     // Stage table for a length-2^log_l Stockham transform (uploaded once per plan).
     float scale_for(Direction dir, bool normalize) const;
     const void* stage_table(uint32_t log_l);
     const void* big_table();
-    void add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t count, Buf src, Buf dst);
+    void add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t per_unit, Buf src, Buf dst,
+                      const char* policy = "");
     void add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g, bool rowwise, const TileGeom& geom,
-                  uint64_t tiles, Buf src, Buf dst);
+                  uint64_t tiles_per_unit, Buf src, Buf dst, const char* policy);
+    // Chunking of a multi-launch plan (sets chunk_ and cached_) and the cache
+    // policy suffix of pass i of n.
+    void choose_chunk();
+    const char* policy(size_t i, size_t n) const;
 
     HipDevice* dev_;
     Kind kind_;
     uint32_t log_n_;
     uint32_t log_rows_;  // 0 for 1D
     size_t batch_;
+    size_t chunk_;         // units per chunk (batch_ when not chunked)
+    bool cached_ = false;  // intermediates kept cached (else every pass streams)
     std::vector<Step> steps_;
     std::vector<std::pair<uint32_t, Buffer<Cf32, HipBackend>>> stage_tables_;
     Buffer<Cf32, HipBackend> big_;
@@ -137,6 +156,15 @@ std::vector<uint32_t> split_1d(uint32_t log_n);
 uint32_t tile_columns(uint32_t log_l);
 // Whether the column FFT of an image with 2^log_rows rows runs as two passes.
 bool split_2d_columns(uint32_t log_rows);
+// Largest chunk (bytes of one chunk's array) a multi-launch plan created from
+// now on runs with its intermediates cached: FERRUM_GPU_CHUNK_MIB at load, else
+// 128 MiB (half the 256 MB Infinity Cache).  0 = no chunking: one chunk of
+// the whole batch, every pass streaming.
+size_t chunk_limit_bytes();
+void set_chunk_limit_bytes(size_t bytes);
+// Units per chunk for `unit_bytes` per transform (image), and whether the
+// chunk's intermediates are kept cached, under the given limit.
+size_t chunk_units_for(uint64_t unit_bytes, size_t batch, size_t limit, bool* cached);
 // Launch the tiled transpose out[b][c][r] = in[b][r][c] on `stream`.
 void transpose_c64(HipDevice& dev, const HipBackend::Module& mod, const void* in, void* out, uint32_t rows,
                    uint32_t cols, size_t batch, hipStream_t stream);

@@ -31,6 +31,18 @@ using namespace fg;
                                            scale, flags);                                     \
     }
 
+// fg_fft_n<L>_sc: the same transform with the input streamed and the output
+// stored cached -- the first launch of a 2D plan's chunk, whose output the
+// column passes read next (fft_common.hpp, gload/gstore).
+#define FG_STOCKHAM_SC(LOGN, LOGE, FPB)                                                        \
+    extern "C" __global__ __launch_bounds__(FPB * ((1 << LOGN) >> LOGE)) void                  \
+        fg_fft_n##LOGN##_sc(const float2* __restrict__ in, float2* __restrict__ out,           \
+                            const float2* __restrict__ tw, uint64_t batch, float scale,       \
+                            uint32_t flags) {                                                 \
+        fft_stockham_body<LOGN, LOGE, FPB>(InterleavedIOT<false, true>{in, out}, tw, batch,   \
+                                           scale, flags);                                     \
+    }
+
 FG_STOCKHAM(2, 2, 64)    // N=4:    1 thread  / transform, 64 per wave
 FG_STOCKHAM(3, 3, 64)    // N=8:    1 thread  / transform
 FG_STOCKHAM(4, 4, 64)    // N=16:   1 thread  / transform
@@ -42,6 +54,15 @@ FG_STOCKHAM(9, 4, 2)     // N=512:  32 threads
 FG_STOCKHAM(10, 4, 1)    // N=1024: 64 threads (one wave per transform)
 FG_STOCKHAM(11, 4, 1)    // N=2048: 128 threads
 FG_STOCKHAM(12, 4, 1)    // N=4096: 256 threads
+FG_STOCKHAM_SC(4, 4, 64)
+FG_STOCKHAM_SC(5, 4, 32)
+FG_STOCKHAM_SC(6, 4, 16)
+FG_STOCKHAM_SC(7, 4, 8)
+FG_STOCKHAM_SC(8, 4, 4)
+FG_STOCKHAM_SC(9, 4, 2)
+FG_STOCKHAM_SC(10, 4, 1)
+FG_STOCKHAM_SC(11, 4, 1)
+FG_STOCKHAM_SC(12, 4, 1)
 
 // ---------------------------------------------------------------- utilities
 
@@ -105,19 +126,27 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
 
 // ------------------------------------------------------- multi-pass tiles
 //
-// fg_tile_l<LOGL>_g<G>_<c|r>: one pass over G columns of length 2^LOGL per
-// workgroup (G * 2^LOGL / 16 threads).  'c': columns contiguous in memory
-// (column passes); 'r': rows contiguous (the last 1D pass, which transposes
-// through LDS).  Mirrored on the host by kTileTable in fft_plan.cpp.
+// fg_tile_l<LOGL>_g<G>_<c|r>[_<policy>]: one pass over G columns of length
+// 2^LOGL per workgroup (G * 2^LOGL / 16 threads).  'c': columns contiguous in
+// memory (column passes); 'r': rows contiguous (the last 1D pass, which
+// transposes through LDS).  Policy (fft_common.hpp, gload/gstore): none =
+// stream in and out; _sc = stream in, cached out (a chunk's first pass); _cc
+// (middle passes); _cs = cached in, stream out (last pass).  The host picks
+// the names in fft_plan.cpp (tile_name).
 #include "fft_tile.hpp"
 
-#define FG_TILE(LOGL, G, RW, TAG)                                                                    \
+#define FG_TILE_P(LOGL, G, RW, TAG, LC, SC)                                                          \
     extern "C" __global__ __launch_bounds__(G * ((1 << LOGL) >> (LOGL < 4 ? LOGL : 4))) void        \
         fg_tile_l##LOGL##_g##G##_##TAG(const float2* __restrict__ in, float2* __restrict__ out,     \
                                        const float2* __restrict__ tw, const float2* __restrict__ big, \
                                        TileGeom g) {                                                  \
-        fft_tile_body<LOGL, (LOGL < 4 ? LOGL : 4), G, RW, true>(in, out, tw, big, g);                \
+        fft_tile_body<LOGL, (LOGL < 4 ? LOGL : 4), G, RW, true, LC, SC>(in, out, tw, big, g);        \
     }
+#define FG_TILE(LOGL, G, RW, TAG)                  \
+    FG_TILE_P(LOGL, G, RW, TAG, false, false)      \
+    FG_TILE_P(LOGL, G, RW, TAG##_cs, true, false)  \
+    FG_TILE_P(LOGL, G, RW, TAG##_sc, false, true)  \
+    FG_TILE_P(LOGL, G, RW, TAG##_cc, true, true)
 
 // Column passes: 1D digits of 128..1024 points (G = 64/32/16 by length), and
 // 2D column FFTs of 16..1024 points (or the 2048/4096 splits into 64 x 32 and

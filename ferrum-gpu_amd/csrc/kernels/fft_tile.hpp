@@ -89,7 +89,8 @@ struct TileStages {
 // matrix), so loads run along elements and the tile is transposed into LDS
 // first; otherwise columns are contiguous (ics == 1) and each thread loads its
 // own Stockham positions straight into VGPRs.  Output always has ocs == 1.
-template <int LOGL, int LOGE, int G, bool ROWWISE, bool TWREC = false>
+// LOAD_CACHED / STORE_CACHED select the pass's cache policy (gload/gstore).
+template <int LOGL, int LOGE, int G, bool ROWWISE, bool TWREC, bool LOAD_CACHED, bool STORE_CACHED>
 __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, float2* __restrict__ out,
                                               const float2* __restrict__ tw, const float2* __restrict__ big,
                                               const TileGeom& g) {
@@ -117,14 +118,14 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
             const int li = tid + THREADS * m;
             const int cc = li >> LOGL;
             const int n = li & (Sh::N - 1);
-            lds[n * P + cc] = load_stream(in + ib + (uint64_t)cc * g.ics + n);
+            lds[n * P + cc] = gload<LOAD_CACHED>(in + ib + (uint64_t)cc * g.ics + n);
         }
         __syncthreads();
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) x[m] = lds[(q + Sh::T * m) * P + c];
     } else {
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = load_stream(in + ib + c + (uint64_t)(q + Sh::T * m) * g.ies);
+        for (int m = 0; m < Sh::E; ++m) x[m] = gload<LOAD_CACHED>(in + ib + c + (uint64_t)(q + Sh::T * m) * g.ies);
     }
     if (g.flags & FG_PASS_CONJ_IN) {
 #pragma unroll
@@ -142,7 +143,7 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
         const int k = q + Sh::T * m;
         float2 v = x[m];
         if (cs) v = cscale(cconj(v), g.scale);
-        store_stream(out + ob + c + (uint64_t)k * g.oes, v);
+        gstore<STORE_CACHED>(out + ob + c + (uint64_t)k * g.oes, v);
     }
 }
 

@@ -188,7 +188,12 @@ class _Plan:
         name = ctypes.create_string_buffer(128)
         ws = ctypes.c_size_t()
         _n.check(_n.lib.fg_fft_plan_describe(self._p, ctypes.byref(launches), name, 128, ctypes.byref(ws)))
-        return {"launches": launches.value, "main_kernel": name.value.decode(), "workspace_bytes": ws.value}
+        passes, units, chunks, cached = ctypes.c_int(), ctypes.c_size_t(), ctypes.c_int(), ctypes.c_int()
+        _n.check(_n.lib.fg_fft_plan_chunking(self._p, ctypes.byref(passes), ctypes.byref(units),
+                                             ctypes.byref(chunks), ctypes.byref(cached)))
+        return {"launches": launches.value, "main_kernel": name.value.decode(), "workspace_bytes": ws.value,
+                "passes": passes.value, "units_per_chunk": units.value, "chunks": chunks.value,
+                "cache_resident": bool(cached.value)}
 
     def destroy(self) -> None:
         """Free the plan; refused (FerrumGpuError) while graphs of it exist."""
@@ -260,3 +265,22 @@ def transpose(device: Device, d_in, d_out, rows: int, cols: int, batch: int = 1,
     the device (stream-ordered; in and out must not alias)."""
     _n.check(_n.lib.fg_transpose_c64(device.handle, _ptr(d_in), _ptr(d_out), int(rows), int(cols), int(batch),
                                      ctypes.c_void_p(stream or None)))
+
+
+def set_chunk_bytes(nbytes: int) -> None:
+    """Chunk limit, in bytes, for multi-launch plans (1D N > 4096, 2D) created
+    from now on, process-wide.  Such a plan runs every pass over one chunk of
+    whole transforms (images) of at most ``nbytes`` before the next chunk, so
+    the chunk's intermediate array stays in the GPU's Infinity Cache.  0 turns
+    chunking off (one chunk, every pass streaming).  Default 128 MiB, or
+    FERRUM_GPU_CHUNK_MIB at library load."""
+    if int(nbytes) < 0:
+        raise ValueError(f"chunk bytes must be >= 0, got {nbytes}")
+    _n.check(_n.lib.fg_fft_set_chunk_bytes(int(nbytes)))
+
+
+def get_chunk_bytes() -> int:
+    """The current chunk limit for new multi-launch plans (set_chunk_bytes)."""
+    v = ctypes.c_size_t()
+    _n.check(_n.lib.fg_fft_get_chunk_bytes(ctypes.byref(v)))
+    return v.value

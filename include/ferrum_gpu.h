@@ -188,6 +188,22 @@ FG_API int fg_graph_capture_end(fg_device_t dev, fg_stream_t capture_stream, fg_
 /* Number of nodes in the captured graph. */
 FG_API int fg_graph_node_count(fg_graph_t graph, size_t *nodes);
 FG_API int fg_graph_destroy(fg_graph_t graph);
+/* Chunked execution of multi-launch plans (1D N > 4096, every 2D plan).  No
+ * counterpart in the reference, whose GPU path has no multi-pass plans
+ * (crates/ferrum-gpu-fft/src/plan.rs:58).  Such a plan runs all of its passes
+ * over one chunk of at most `bytes` (whole transforms or images) before the
+ * next, keeping the chunk's intermediate array cached (in the 256 MB
+ * Infinity Cache) instead of moving it through HBM.  The limit applies to
+ * plans created afterwards, process-wide; 0 disables chunking (one chunk of
+ * the whole batch, every pass streaming).  Default: FERRUM_GPU_CHUNK_MIB from
+ * the environment when the library loads, else 128 MiB. */
+FG_API int fg_fft_set_chunk_bytes(size_t bytes);
+FG_API int fg_fft_get_chunk_bytes(size_t *bytes);
+/* How a plan executes: passes per chunk, transforms (2D: images) per chunk,
+ * number of chunks (launches = passes * chunks), and whether intermediates
+ * are kept cached (1) or every pass streams (0). */
+FG_API int fg_fft_plan_chunking(fg_fft_plan_t plan, int *passes, size_t *units_per_chunk, int *chunks,
+                                int *cached);
 /* Kernel name of launch `index` of an execution. */
 FG_API int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char *name, size_t cap);
 /* Number of kernel launches per execution and the name of the kernel that

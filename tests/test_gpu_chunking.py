@@ -1,0 +1,149 @@
+"""Chunked execution of multi-launch plans (1D N > 4096 and every 2D plan).
+
+A multi-launch plan runs all of its passes over one chunk of whole
+transforms (images) before the next, keeping the chunk's intermediate array
+cached; the chunk limit is process-wide (ferrum_gpu.fft.set_chunk_bytes) and
+read when a plan is created.  Chunking changes only which transforms a launch
+covers and the cache hints of its accesses, never the arithmetic, so every
+chunking of a plan must give bit-identical output -- and the oracle's result
+within 1e-4.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import normal_c64, rel_l2, uniform_c64
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+MIB = 1 << 20
+
+
+@pytest.fixture
+def chunk_limit():
+    """Sets the process-wide chunk limit for the test and restores it after."""
+    import ferrum_gpu
+
+    saved = ferrum_gpu.fft.get_chunk_bytes()
+    yield ferrum_gpu.fft.set_chunk_bytes
+    ferrum_gpu.fft.set_chunk_bytes(saved)
+
+
+def _run(dev, x, log_n, batch, two_d, direction="forward", normalize=False, in_place=False):
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer
+
+    plan = (ferrum_gpu.fft.Plan2D if two_d else ferrum_gpu.fft.Plan1D)(log_n, batch, dev)
+    d = plan.describe()
+    a = DeviceBuffer(dev, plan.nbytes)
+    b = a if in_place else DeviceBuffer(dev, plan.nbytes)
+    a.copy_from_host(x)
+    plan.execute(a, b, direction, normalize)
+    dev.sync()
+    out = np.empty_like(x)
+    b.copy_to_host(out)
+    names = plan.kernel_names()
+    plan.destroy()
+    return out, d, names
+
+
+# (two_d, log_n, batch): transform sizes 64 KiB .. 128 MiB, batches that
+# do and do not divide into chunks.
+CASES = [
+    (False, 13, 37),
+    (False, 16, 64),
+    (False, 20, 3),
+    (True, 4, 1000),
+    (True, 10, 9),
+    (True, 11, 3),
+]
+
+
+@pytest.mark.parametrize("two_d,log_n,batch", CASES)
+def test_every_chunking_gives_the_same_bits(gpu_device, chunk_limit, two_d, log_n, batch):
+    elems = 1 << (2 * log_n if two_d else log_n)
+    unit = 8 * elems
+    rng = np.random.default_rng(900 + log_n)
+    x = uniform_c64(rng, batch * elems)
+    ref = oracle.fft_2d(x, log_n) if two_d else oracle.fft_1d(x, log_n, threads=8)
+    outs = {}
+    # 0: one chunk, every pass streaming; one unit per chunk; a few units per
+    # chunk; the default 128 MiB.
+    for limit in (0, unit, 3 * unit, 128 * MIB):
+        chunk_limit(limit)
+        print(f"[case] two_d={two_d} log_n={log_n} batch={batch} chunk_limit={limit}", flush=True)
+        got, d, names = _run(gpu_device, x, log_n, batch, two_d)
+        assert rel_l2(got, ref) <= TOL
+        if limit == 0:
+            assert d["chunks"] == 1 and not d["cache_resident"] and d["units_per_chunk"] == batch
+            assert not any(n.endswith(("_sc", "_cc", "_cs")) for n in names)
+        else:
+            per = min(batch, limit // unit)
+            assert d["cache_resident"] and d["units_per_chunk"] == per
+            assert d["chunks"] == -(-batch // per)
+            # first pass streams in, last streams out, middle passes stay cached
+            assert names[0].endswith("_sc") and names[d["passes"] - 1].endswith("_cs")
+            assert all(n.endswith("_cc") for n in names[1:d["passes"] - 1])
+        assert d["launches"] == d["passes"] * d["chunks"] == len(names)
+        outs[limit] = got
+    for limit, got in outs.items():
+        assert np.array_equal(got, outs[0]), f"chunk limit {limit} changed the output bits"
+
+
+@pytest.mark.parametrize("two_d,log_n,batch", [(False, 16, 10), (True, 11, 3)])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_chunked_inverse_and_in_place(gpu_device, chunk_limit, two_d, log_n, batch, normalize):
+    elems = 1 << (2 * log_n if two_d else log_n)
+    chunk_limit(2 * 8 * elems)  # two units per chunk: the last chunk is partial for odd batches
+    rng = np.random.default_rng(950 + log_n)
+    x = normal_c64(rng, batch * elems)
+    ref = (oracle.fft_2d(x, log_n, "inverse", normalize) if two_d
+           else oracle.fft_1d(x, log_n, "inverse", normalize, threads=8))
+    got, d, _ = _run(gpu_device, x, log_n, batch, two_d, "inverse", normalize)
+    assert d["chunks"] == -(-batch // 2)
+    assert rel_l2(got, ref) <= TOL
+    got_ip, _, _ = _run(gpu_device, x, log_n, batch, two_d, "inverse", normalize, in_place=True)
+    assert np.array_equal(got_ip, got)
+
+
+def test_chunked_split_layout(gpu_device, chunk_limit):
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer
+
+    log_n, batch = 14, 12
+    n = batch << log_n
+    chunk_limit(4 * 8 << log_n)
+    rng = np.random.default_rng(977)
+    x = uniform_c64(rng, n)
+    plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
+    assert plan.describe()["chunks"] == 3
+    parts = [DeviceBuffer(gpu_device, 4 * n) for _ in range(4)]
+    parts[0].copy_from_host(np.ascontiguousarray(x.real))
+    parts[1].copy_from_host(np.ascontiguousarray(x.imag))
+    plan.execute_split(parts[0], parts[1], parts[2], parts[3])
+    gpu_device.sync()
+    re, im = np.empty(n, np.float32), np.empty(n, np.float32)
+    parts[2].copy_to_host(re)
+    parts[3].copy_to_host(im)
+    assert rel_l2(re + 1j * im, oracle.fft_1d(x, log_n, threads=8)) <= TOL
+    plan.destroy()
+
+
+def test_chunk_limit_applies_to_new_plans_only(gpu_device, chunk_limit):
+    import ferrum_gpu
+
+    chunk_limit(128 * MIB)
+    a = ferrum_gpu.fft.Plan1D(16, 512, gpu_device)  # 256 MiB: two chunks of 256 transforms
+    chunk_limit(0)
+    b = ferrum_gpu.fft.Plan1D(16, 512, gpu_device)
+    assert a.describe()["chunks"] == 2 and a.describe()["units_per_chunk"] == 256
+    assert b.describe()["chunks"] == 1 and not b.describe()["cache_resident"]
+    # single-launch plans never chunk
+    c = ferrum_gpu.fft.Plan1D(10, 65536, gpu_device)
+    assert c.describe()["chunks"] == 1 and c.describe()["passes"] == 1
+    for p in (a, b, c):
+        p.destroy()

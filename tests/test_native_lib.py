@@ -47,6 +47,20 @@ def test_library_exports_nothing_undeclared():
     assert exported == declared_symbols()
 
 
+def test_chunk_limit_round_trip():
+    # Process-wide; read by plans when they are created (no device needed).
+    saved = ferrum_gpu.fft.get_chunk_bytes()
+    try:
+        assert saved == 128 << 20 or os.environ.get("FERRUM_GPU_CHUNK_MIB")
+        for v in (0, 1, 64 << 20, 1 << 40):
+            ferrum_gpu.fft.set_chunk_bytes(v)
+            assert ferrum_gpu.fft.get_chunk_bytes() == v
+        with pytest.raises(ValueError):
+            ferrum_gpu.fft.set_chunk_bytes(-1)
+    finally:
+        ferrum_gpu.fft.set_chunk_bytes(saved)
+
+
 def test_version_and_backend():
     assert ferrum_gpu.version() == "0.3.0"          # crates/ferrum-gpu-py/src/lib.rs:420-423
     assert N.backend_id() == N.FG_BACKEND_HIP == 3  # BackendId with Hip added
@@ -56,8 +70,10 @@ def instantiated_kernels():
     src = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
     names = {f"fg_fft_n{m.group(1)}" for m in re.finditer(r"^FG_STOCKHAM\((\d+),", src, flags=re.M)}
     names |= {f"{n}_split" for n in names}
+    names |= {f"fg_fft_n{m.group(1)}_sc" for m in re.finditer(r"^FG_STOCKHAM_SC\((\d+),", src, flags=re.M)}
     for m in re.finditer(r"^FG_TILE\((\d+), (\d+), (true|false), ([cr])\)", src, flags=re.M):
-        names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_{m.group(4)}")
+        base = f"fg_tile_l{m.group(1)}_g{m.group(2)}_{m.group(4)}"
+        names |= {base + pol for pol in ("", "_sc", "_cc", "_cs")}  # cache policies (FG_TILE_P)
     return names
 
 
@@ -65,14 +81,23 @@ def planned_kernels():
     """Every kernel name FftPlan can request (mirrors fft_plan.cpp via the CPU models)."""
     from test_multipass_model import tile_geometry_1d, tile_geometry_2d
 
+    def policies(i, n):
+        # unchunked: every pass streams; chunked: first _sc, middle _cc, last _cs
+        return ("", "_sc" if i == 0 else ("_cs" if i == n - 1 else "_cc"))
+
     names = {f"fg_fft_n{l}" for l in range(2, 13)} | {f"fg_fft_n{l}_split" for l in range(2, 13)}
     for log_n in range(13, 25):
-        for p in tile_geometry_1d(log_n, 1):
-            names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}")
+        passes = tile_geometry_1d(log_n, 1)
+        for i, p in enumerate(passes):
+            for pol in policies(i, len(passes)):
+                names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}{pol}")
     for lr in range(4, 13):
         for lc in range(4, 13):
-            for p in tile_geometry_2d(lr, 1, lc):
-                names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}")
+            passes = tile_geometry_2d(lr, 1, lc)   # column passes; the row pass comes first
+            names |= {f"fg_fft_n{lc}", f"fg_fft_n{lc}_sc"}
+            for i, p in enumerate(passes):
+                for pol in policies(i + 1, len(passes) + 1):
+                    names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}{pol}")
     return names
 
 
