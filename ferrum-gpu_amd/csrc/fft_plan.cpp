@@ -112,7 +112,14 @@ uint32_t tile_columns(uint32_t log_l) {
     return g;
 }
 
-bool split_2d_columns(uint32_t log_rows) { return log_rows > 10; }
+bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }
+
+uint32_t column_tile_width(uint32_t log_rows) {
+    // Up to 1024 rows: the 1D column widths (>= 16 columns, 128-byte row
+    // segments).  2048 / 4096 rows: 8 / 4 columns, the most a 136 KB LDS tile
+    // holds, read in XCD-aware order (kernels/fft_tile.hpp).
+    return log_rows <= 10 ? tile_columns(log_rows) : (16384u >> log_rows);
+}
 
 namespace {
 
@@ -316,7 +323,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     p->add_stockham(mod, log_cols, R, Buf::In, split ? Buf::Work : Buf::Out, p->policy(0, npass));
     if (!split) {
         // Column pass, in place: G adjacent columns of length R per tile.
-        const uint32_t g = (uint32_t)std::min<uint64_t>(tile_columns(log_rows), C);
+        const uint32_t g = (uint32_t)std::min<uint64_t>(column_tile_width(log_rows), C);
         TileGeom t{};
         t.t0n = (uint32_t)(C / g);
         t.t1n = 1;
@@ -325,7 +332,14 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         t.is2 = t.os2 = RC;
         t.ics = t.ocs = 1;
         t.ies = t.oes = C;
-        p->add_tile(mod, log_rows, g, false, t, (uint64_t)t.t0n, Buf::Out, Buf::Out, p->policy(1, npass));
+        // Narrow tiles (g < 16: 32- or 64-byte pieces of each 128-byte line)
+        // load and store through the caches whatever the chunking, so a line's
+        // pieces from neighbouring tiles merge in their XCD's L2; nontemporal
+        // stores of such pieces measured 5x slower.
+        const bool narrow = g < 16;
+        p->add_tile(mod, log_rows, g, false, t, (uint64_t)t.t0n, Buf::Out, Buf::Out,
+                    narrow ? "_cc" : p->policy(1, npass));
+        p->steps_.back().xcd_remap = narrow;
     } else {
         // Column FFT of length R = R_1 * R_2 over the slow axis, as two column
         // passes over G = min(64, C) adjacent columns.
@@ -438,6 +452,8 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
                 TileGeom g = s.geom;
                 g.flags = flags;
                 g.scale = scale;
+                const uint64_t tiles = s.per_unit * units;
+                g.remap = (s.xcd_remap && tiles % 8 == 0) ? 1u : 0u;
                 void* args[] = {&src, &dst, (void*)&tw, (void*)&big, &g};
                 HipBackend::launch(dev_->handle(), stream, s.fn, Dim3((uint32_t)(s.per_unit * units)), s.block, 0,
                                    args);

@@ -103,7 +103,8 @@ private:
         // Per unit (one transform, or one 2D image): Stockham transforms, or
         // tiles of a tile pass.  A launch over u units has per_unit * u of them.
         uint64_t per_unit = 0;
-        TileGeom geom{};                        // tile: addressing (flags/scale set at exec)
+        bool xcd_remap = false;                 // tile: XCD-aware tile order when the grid allows
+        TileGeom geom{};                        // tile: addressing (flags/scale/remap set at exec)
     };
 
     FftPlan(HipDevice& dev, Kind kind, uint32_t log_n, uint32_t log_rows, size_t batch)
@@ -156,6 +157,8 @@ std::vector<uint32_t> split_1d(uint32_t log_n);
 uint32_t tile_columns(uint32_t log_l);
 // Whether the column FFT of an image with 2^log_rows rows runs as two passes.
 bool split_2d_columns(uint32_t log_rows);
+// Columns per tile of a 2D image's one-pass column FFT over 2^log_rows rows.
+uint32_t column_tile_width(uint32_t log_rows);
 // Largest chunk (bytes of one chunk's array) a multi-launch plan created from
 // now on runs with its intermediates cached: FERRUM_GPU_CHUNK_MIB at load, else
 // 128 MiB (half the 256 MB Infinity Cache).  0 = no chunking: one chunk of

@@ -167,6 +167,10 @@ FG_TILE(8, 16, false, c)
 FG_TILE(8, 32, false, c)
 FG_TILE(9, 16, false, c)
 FG_TILE(10, 16, false, c)
+// 2D column FFTs of 2048 / 4096 rows in one pass: 8 / 4 columns per tile
+// (1024 threads, 136 KB of LDS), read in XCD-aware tile order.
+FG_TILE(11, 8, false, c)
+FG_TILE(12, 4, false, c)
 // Row passes (last 1D digit: rows contiguous, transposed store).
 FG_TILE(6, 64, true, r)
 FG_TILE(7, 64, true, r)

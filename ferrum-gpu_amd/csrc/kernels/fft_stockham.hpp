@@ -206,13 +206,19 @@ template <int LOGN, int LOGE, int FPB, class IO>
 __device__ __forceinline__ void fft_stockham_body(const IO io, const float2* __restrict__ tw,
                                                   uint64_t batch, float scale, uint32_t flags) {
     using Sh = StockhamShape<LOGN, LOGE>;
-    constexpr bool ONE_WAVE = (Sh::T * FPB) <= 64;
+    constexpr int BLOCK = FPB * Sh::T;
+    // Whole workgroup in one wave: its block-wide LDS staging needs only
+    // wave-scope ordering.
+    constexpr bool ONE_WAVE = BLOCK <= 64;
+    // Each transform's T threads lie in one wave (T <= 64 divides the 64
+    // lanes), so its stage exchanges need only wave-scope ordering, however
+    // many transforms the workgroup holds.
+    constexpr bool WAVE_LOCAL = Sh::T <= 64;
     // With fewer than 8 threads per transform a thread's positions t + T*m
     // give each wave only T*8-byte pieces per load; such sizes move the
     // workgroup's FPB contiguous transforms through LDS instead, 64 lanes x 8
     // contiguous bytes per instruction.
     constexpr bool STAGED = Sh::T < 8 && FPB > 1;  // measured: N = 128 (T = 8) is faster direct
-    constexpr int BLOCK = FPB * Sh::T;
     __shared__ float2 lds_all[FPB][Sh::LDS_ELEMS];
     const int tid = threadIdx.x;
     const int slot = tid / Sh::T;
@@ -247,7 +253,7 @@ __device__ __forceinline__ void fft_stockham_body(const IO io, const float2* __r
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) x[m] = cconj(x[m]);
     }
-    StockhamStages<LOGN, LOGE, 0>::template run<ONE_WAVE>(x, t, tw, lds_all[slot]);
+    StockhamStages<LOGN, LOGE, 0>::template run<WAVE_LOCAL>(x, t, tw, lds_all[slot]);
     if constexpr (STAGED) {
         if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
 #pragma unroll

@@ -52,11 +52,21 @@ __device__ __forceinline__ void apply_pass_twiddle(float2* x, const float2* __re
     }
 }
 
-// LDS row pitch of the [position][column] layout: one pad column keeps the
-// row-wise staging writes (lanes along positions) off a single bank.
-template <int G>
-struct TilePitch {
-    static constexpr int value = G + 1;
+// LDS layout of a tile, [position][column].  G >= 16: row pitch G + 1 (one
+// pad column keeps the row-wise staging writes, lanes along positions, off a
+// single bank).  G < 16 (long columns, 4 or 8 per tile): pitch G with one pad
+// row per 16 positions (lds_pos), which spreads the stride-16 scatter of a
+// radix-16 stage over the banks and keeps a 4 x 4096 tile at 136 KB (a pad
+// column would take all 160 KB of the CU's LDS).
+template <int LOGL, int G>
+struct TileLayout {
+    static constexpr bool PADPOS = G < 16;
+    static constexpr int N = 1 << LOGL;
+    static constexpr int ELEMS = PADPOS ? (N + N / 16) * G : N * (G + 1);
+    __device__ __forceinline__ static int at(int pos, int c) {
+        if constexpr (PADPOS) return lds_pos(pos) * G + c;
+        else return pos * (G + 1) + c;
+    }
 };
 
 // Stockham stages on a [position][column] LDS tile: thread (c, q) holds
@@ -64,7 +74,7 @@ struct TilePitch {
 template <int LOGL, int LOGE, int G, int S>
 struct TileStages {
     using Sh = StockhamShape<LOGL, LOGE>;
-    static constexpr int P = TilePitch<G>::value;
+    using Lay = TileLayout<LOGL, G>;
     __device__ __forceinline__ static void run(float2* x, int q, int c, const float2* __restrict__ tw,
                                                float2* __restrict__ lds) {
         stockham_stage_regs<LOGL, LOGE, S>(x, q, tw);
@@ -76,10 +86,10 @@ struct TileStages {
 #pragma unroll
             for (int i = 0; i < NB; ++i)
 #pragma unroll
-                for (int r = 0; r < R; ++r) lds[stockham_dst<LOGL, LOGE, S>(q, i, r) * P + c] = x[i + NB * r];
+                for (int r = 0; r < R; ++r) lds[Lay::at(stockham_dst<LOGL, LOGE, S>(q, i, r), c)] = x[i + NB * r];
             __syncthreads();
 #pragma unroll
-            for (int m = 0; m < Sh::E; ++m) x[m] = lds[(q + Sh::T * m) * P + c];
+            for (int m = 0; m < Sh::E; ++m) x[m] = lds[Lay::at(q + Sh::T * m, c)];
             TileStages<LOGL, LOGE, G, S + 1>::run(x, q, c, tw, lds);
         }
     }
@@ -95,14 +105,22 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
                                               const float2* __restrict__ tw, const float2* __restrict__ big,
                                               const TileGeom& g) {
     using Sh = StockhamShape<LOGL, LOGE>;
-    constexpr int P = TilePitch<G>::value;
+    using Lay = TileLayout<LOGL, G>;
     constexpr int THREADS = G * Sh::T;
-    __shared__ float2 lds[Sh::N * P];
+    __shared__ float2 lds[Lay::ELEMS];
 
     const int tid = threadIdx.x;
     const int c = tid % G;
     const int q = tid / G;
     uint32_t b = blockIdx.x;
+    if (g.remap) {
+        // XCD-aware order: workgroups are dealt round-robin over the 8 XCDs,
+        // so XCD x (blockIdx % 8) takes the contiguous tile range
+        // [x * grid/8, (x + 1) * grid/8).  Narrow tiles (4 or 8 columns, 32 or
+        // 64 bytes of a 128-byte line) then share each line fill of their
+        // XCD's L2 instead of each XCD fetching it (host: grid % 8 == 0).
+        b = (b & 7u) * (gridDim.x >> 3) + (b >> 3);
+    }
     const uint32_t t0 = b % g.t0n;
     b /= g.t0n;
     const uint32_t t1 = b % g.t1n;
@@ -118,11 +136,11 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
             const int li = tid + THREADS * m;
             const int cc = li >> LOGL;
             const int n = li & (Sh::N - 1);
-            lds[n * P + cc] = gload<LOAD_CACHED>(in + ib + (uint64_t)cc * g.ics + n);
+            lds[Lay::at(n, cc)] = gload<LOAD_CACHED>(in + ib + (uint64_t)cc * g.ics + n);
         }
         __syncthreads();
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = lds[(q + Sh::T * m) * P + c];
+        for (int m = 0; m < Sh::E; ++m) x[m] = lds[Lay::at(q + Sh::T * m, c)];
     } else {
 #pragma unroll
         for (int m = 0; m < Sh::E; ++m) x[m] = gload<LOAD_CACHED>(in + ib + c + (uint64_t)(q + Sh::T * m) * g.ies);

@@ -25,7 +25,7 @@ typedef struct TileGeom {
     uint32_t log_m;         /* twiddle W_M^(r*k), M = 2^log_m; 0 = none */
     uint32_t flags;         /* FG_PASS_* */
     float scale;
-    uint32_t pad_;
+    uint32_t remap;         /* 1: XCD-aware tile order (grid a multiple of 8; fft_tile.hpp) */
 } TileGeom;
 
 #ifdef __cplusplus

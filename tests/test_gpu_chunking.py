@@ -80,13 +80,16 @@ def test_every_chunking_gives_the_same_bits(gpu_device, chunk_limit, two_d, log_
         assert rel_l2(got, ref) <= TOL
         if limit == 0:
             assert d["chunks"] == 1 and not d["cache_resident"] and d["units_per_chunk"] == batch
-            assert not any(n.endswith(("_sc", "_cc", "_cs")) for n in names)
+            assert not any(n.endswith(("_sc", "_cs")) for n in names)
         else:
             per = min(batch, limit // unit)
             assert d["cache_resident"] and d["units_per_chunk"] == per
             assert d["chunks"] == -(-batch // per)
-            # first pass streams in, last streams out, middle passes stay cached
-            assert names[0].endswith("_sc") and names[d["passes"] - 1].endswith("_cs")
+            # first pass streams in, last streams out (except a narrow 2D column
+            # pass, which stays cached), middle passes stay cached
+            narrow = two_d and log_n > 10
+            assert names[0].endswith("_sc")
+            assert names[d["passes"] - 1].endswith("_cc" if narrow else "_cs")
             assert all(n.endswith("_cc") for n in names[1:d["passes"] - 1])
         assert d["launches"] == d["passes"] * d["chunks"] == len(names)
         outs[limit] = got

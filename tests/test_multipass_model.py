@@ -76,33 +76,39 @@ def tile_geometry_1d(log_n, batch):
     return passes
 
 
+def column_tile_width(log_rows):
+    """Columns per tile of the one-pass 2D column FFT (column_tile_width in fft_plan.cpp)."""
+    return tile_columns(log_rows) if log_rows <= 10 else 16384 >> log_rows
+
+
 def tile_geometry_2d(log_n, batch, log_cols=None):
     """Column FFT of each R x C image after the row pass, as FftPlan::make_2d builds it
-    (R = 2^log_n rows, C = 2^log_cols columns, square by default): one pass up to
-    1024 rows, else R = R_1 * R_2 in two passes over min(64, C) columns."""
+    (R = 2^log_n rows, C = 2^log_cols columns, square by default): one tile pass over
+    min(column_tile_width(R), C) adjacent columns of length R, in place."""
     R = 1 << log_n
     C = R if log_cols is None else 1 << log_cols
-    if log_n <= 10:                   # split_2d_columns in fft_plan.cpp
-        g = min(tile_columns(log_n), C)
-        return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
-                     is0=g, is1=0, is2=R * C, ics=1, ies=C,
-                     os0=g, os1=0, os2=R * C, ocs=1, oes=C,
-                     twc=0, tw0=0, tw1=0, log_m=0)]
-    l1 = log_n - log_n // 2
-    l2 = log_n // 2
-    R1, R2 = 1 << l1, 1 << l2
-    g = min(64, C)
-    # pass 1: DFT over the slow row digit n_hi (rows n_lo + R2*n_hi) for each (n_lo, column)
-    p1 = dict(log_l=l1, g=g, rowwise=False, t0n=C // g, t1n=R2,
-              is0=g, is1=C, is2=R * C, ics=1, ies=R2 * C,
-              os0=g, os1=C, os2=R * C, ocs=1, oes=R2 * C,
-              twc=0, tw0=0, tw1=1, log_m=log_n)
-    # pass 2: DFT over n_lo (rows R2*k_hi + n_lo) for each (k_hi, column); output row k_hi + R1*k_lo
-    p2 = dict(log_l=l2, g=g, rowwise=False, t0n=C // g, t1n=R1,
-              is0=g, is1=R2 * C, is2=R * C, ics=1, ies=C,
-              os0=g, os1=C, os2=R * C, ocs=1, oes=R1 * C,
-              twc=0, tw0=0, tw1=0, log_m=0)
-    return [p1, p2]
+    g = min(column_tile_width(log_n), C)
+    return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
+                 is0=g, is1=0, is2=R * C, ics=1, ies=C,
+                 os0=g, os1=0, os2=R * C, ocs=1, oes=C,
+                 twc=0, tw0=0, tw1=0, log_m=0)]
+
+
+def xcd_remap(b, grid):
+    """Tile handled by workgroup b under the XCD-aware order (kernels/fft_tile.hpp)."""
+    return (b & 7) * (grid >> 3) + (b >> 3)
+
+
+def tile_lds_index(log_l, g, pos, c):
+    """TileLayout<LOGL, G>::at: position-padded for g < 16, column-padded otherwise."""
+    if g < 16:
+        return (pos + (pos >> 4)) * g + c
+    return pos * (g + 1) + c
+
+
+def tile_lds_elems(log_l, g):
+    n = 1 << log_l
+    return (n + n // 16) * g if g < 16 else n * (g + 1)
 
 
 def run_geometry(buf_in, passes, batch, elems):
@@ -157,7 +163,7 @@ def test_1d_three_pass_small():
     assert rel_l2(got, np.fft.fft(x.astype(np.complex128))) < 1e-5
 
 
-@pytest.mark.parametrize("log_n", [4, 5, 6, 8, 10, 11])
+@pytest.mark.parametrize("log_n", [4, 5, 6, 8, 10, 11, 12])
 def test_2d_column_passes_match_oracle(log_n):
     rng = np.random.default_rng(log_n + 100)
     n = 1 << log_n
@@ -176,6 +182,33 @@ def test_2d_rectangular_column_passes(lr, lc):
     rows = np.fft.fft(x.astype(np.complex128), axis=2).reshape(-1)
     got = run_geometry(rows, tile_geometry_2d(lr, 1, lc), 1, R * C).reshape(1, R, C)
     assert rel_l2(got, np.fft.fft2(x.astype(np.complex128))) < 1e-5
+
+
+@pytest.mark.parametrize("grid", [8, 16, 64, 1024, 4096, 8 * 1000])
+def test_xcd_remap_is_a_permutation_grouping_neighbours(grid):
+    tiles = [xcd_remap(b, grid) for b in range(grid)]
+    assert sorted(tiles) == list(range(grid))
+    per = grid // 8
+    for b in range(grid):
+        # every tile of XCD b % 8 lies in that XCD's contiguous range
+        assert (b & 7) * per <= tiles[b] < ((b & 7) + 1) * per
+
+
+@pytest.mark.parametrize("log_l,g", [(12, 4), (11, 8), (10, 16), (8, 32), (6, 64)])
+def test_tile_lds_layout_is_injective_and_fits(log_l, g):
+    n = 1 << log_l
+    pos, c = np.meshgrid(np.arange(n), np.arange(g), indexing="ij")
+    idx = tile_lds_index(log_l, g, pos, c)
+    assert len(np.unique(idx)) == n * g
+    assert idx.max() < tile_lds_elems(log_l, g)
+    assert tile_lds_elems(log_l, g) * 8 <= 160 * 1024   # one CU's LDS
+
+
+def test_long_column_widths():
+    # 2048 / 4096-row columns: 8 / 4 per tile, 1024 threads of 16 elements
+    for log_n, g in ((11, 8), (12, 4)):
+        assert column_tile_width(log_n) == g
+        assert g * (1 << log_n) // 16 == 1024
 
 
 def test_split_sizes_fit_the_tile_kernel():

@@ -96,7 +96,9 @@ def planned_kernels():
             passes = tile_geometry_2d(lr, 1, lc)   # column passes; the row pass comes first
             names |= {f"fg_fft_n{lc}", f"fg_fft_n{lc}_sc"}
             for i, p in enumerate(passes):
-                for pol in policies(i + 1, len(passes) + 1):
+                # narrow tiles (g < 16) always load and store cached
+                pols = ("_cc",) if p["g"] < 16 else policies(i + 1, len(passes) + 1)
+                for pol in pols:
                     names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}{pol}")
     return names
 
