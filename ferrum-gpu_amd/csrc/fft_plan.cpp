@@ -28,7 +28,7 @@ struct StockhamGeom {
 };
 constexpr StockhamGeom kStockham[kMaxLogNSingle + 1] = {
     {0, 0}, {0, 0},          // log_n 0, 1: unsupported
-    {2, 64}, {3, 64}, {4, 64}, {4, 32}, {4, 16}, {4, 8}, {4, 4}, {4, 2}, {4, 1}, {4, 1}, {4, 1},
+    {2, 64}, {3, 64}, {4, 64}, {4, 32}, {4, 16}, {4, 8}, {4, 4}, {4, 2}, {4, 2}, {4, 1}, {4, 1},
 };
 
 std::string file_image;  // backing store when FERRUM_GPU_CODE_OBJECT is set
@@ -92,8 +92,10 @@ std::vector<Cf32> big_twiddles() {
 }
 
 std::vector<uint32_t> split_1d(uint32_t log_n) {
-    // Two passes while each digit's tile still spans >= 16 columns
-    // (L * G <= 16384 complex of LDS), three passes beyond 2^20.
+    // Two passes while both digits fit wide tiles (>= 16 columns, L * G <=
+    // 16384 complex of LDS), three passes beyond 2^20.  Narrow tiles (2048 /
+    // 4096-point digits) are for cache-resident data only: reading the input
+    // from HBM in 32-byte pieces measured 2.9x slower than 256-byte ones.
     if (log_n <= 20) {
         const uint32_t a = log_n / 2;
         return {log_n - a, a};
@@ -103,9 +105,13 @@ std::vector<uint32_t> split_1d(uint32_t log_n) {
 }
 
 uint32_t tile_columns(uint32_t log_l) {
-    // Measured on gfx950 at 2^24 = 256^3: 32 columns of 256 points (two
-    // 66 KB workgroups per CU) beat 64 (one 133 KB workgroup); fewer than 16
-    // columns (128-byte segments) loses HBM efficiency, so the floor is 16.
+    // Up to 1024 points: measured on gfx950 at 2^24 = 256^3, 32 columns of 256
+    // points (two 66 KB workgroups per CU) beat 64 (one 133 KB workgroup);
+    // fewer than 16 columns (128-byte segments) loses HBM efficiency, so the
+    // floor is 16.  2048 / 4096 points (2D columns only): 8 / 4 columns, the
+    // most a 136 KB LDS tile holds -- narrow tiles, which are read in
+    // XCD-aware order through the caches (add_tile).
+    if (log_l > 10) return 16384u >> log_l;
     uint32_t g = 8192u >> log_l;
     if (g > 64) g = 64;
     if (g < 16) g = 16;
@@ -113,13 +119,6 @@ uint32_t tile_columns(uint32_t log_l) {
 }
 
 bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }
-
-uint32_t column_tile_width(uint32_t log_rows) {
-    // Up to 1024 rows: the 1D column widths (>= 16 columns, 128-byte row
-    // segments).  2048 / 4096 rows: 8 / 4 columns, the most a 136 KB LDS tile
-    // holds, read in XCD-aware order (kernels/fft_tile.hpp).
-    return log_rows <= 10 ? tile_columns(log_rows) : (16384u >> log_rows);
-}
 
 namespace {
 
@@ -215,8 +214,15 @@ void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g
     // 1 (row-wise) and always writes columns at stride 1.
     if ((rowwise ? geom.ies : geom.ics) != 1 || geom.ocs != 1) fail(FG_ERR_INTERNAL, "tile geometry not unit-stride");
     if (tiles_per_unit == 0 || tiles_per_unit * chunk_ > 0x7fffffffull) invalid("too many tiles for one launch");
+    // Narrow tiles (g < 16: 32- or 64-byte pieces of each 128-byte line) load
+    // and store through the caches whatever the chunking, in XCD-aware tile
+    // order, so the pieces of a line from neighbouring tiles meet in one
+    // XCD's L2; nontemporal access to such pieces measured 5x slower.
+    const bool narrow = g < 16;
+    if (narrow) policy = "_cc";
     Step s;
     s.tile = true;
+    s.xcd_remap = narrow;
     s.name = tile_name(log_l, g, rowwise, policy);
     s.fn = HipBackend::get_kernel(mod, s.name.c_str());
     s.block = Dim3(g * ((1u << log_l) >> elems_per_thread_log(log_l)));
@@ -323,7 +329,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     p->add_stockham(mod, log_cols, R, Buf::In, split ? Buf::Work : Buf::Out, p->policy(0, npass));
     if (!split) {
         // Column pass, in place: G adjacent columns of length R per tile.
-        const uint32_t g = (uint32_t)std::min<uint64_t>(column_tile_width(log_rows), C);
+        const uint32_t g = (uint32_t)std::min<uint64_t>(tile_columns(log_rows), C);
         TileGeom t{};
         t.t0n = (uint32_t)(C / g);
         t.t1n = 1;
@@ -332,14 +338,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         t.is2 = t.os2 = RC;
         t.ics = t.ocs = 1;
         t.ies = t.oes = C;
-        // Narrow tiles (g < 16: 32- or 64-byte pieces of each 128-byte line)
-        // load and store through the caches whatever the chunking, so a line's
-        // pieces from neighbouring tiles merge in their XCD's L2; nontemporal
-        // stores of such pieces measured 5x slower.
-        const bool narrow = g < 16;
-        p->add_tile(mod, log_rows, g, false, t, (uint64_t)t.t0n, Buf::Out, Buf::Out,
-                    narrow ? "_cc" : p->policy(1, npass));
-        p->steps_.back().xcd_remap = narrow;
+        p->add_tile(mod, log_rows, g, false, t, (uint64_t)t.t0n, Buf::Out, Buf::Out, p->policy(1, npass));
     } else {
         // Column FFT of length R = R_1 * R_2 over the slow axis, as two column
         // passes over G = min(64, C) adjacent columns.

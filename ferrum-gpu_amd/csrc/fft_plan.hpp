@@ -116,6 +116,7 @@ private:
     const void* big_table();
     void add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t per_unit, Buf src, Buf dst,
                       const char* policy = "");
+    // Narrow tiles (g < 16) override `policy` with "_cc" (fft_plan.cpp).
     void add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g, bool rowwise, const TileGeom& geom,
                   uint64_t tiles_per_unit, Buf src, Buf dst, const char* policy);
     // Chunking of a multi-launch plan (sets chunk_ and cached_) and the cache
@@ -157,8 +158,6 @@ std::vector<uint32_t> split_1d(uint32_t log_n);
 uint32_t tile_columns(uint32_t log_l);
 // Whether the column FFT of an image with 2^log_rows rows runs as two passes.
 bool split_2d_columns(uint32_t log_rows);
-// Columns per tile of a 2D image's one-pass column FFT over 2^log_rows rows.
-uint32_t column_tile_width(uint32_t log_rows);
 // Largest chunk (bytes of one chunk's array) a multi-launch plan created from
 // now on runs with its intermediates cached: FERRUM_GPU_CHUNK_MIB at load, else
 // 128 MiB (half the 256 MB Infinity Cache).  0 = no chunking: one chunk of

@@ -51,7 +51,7 @@ FG_STOCKHAM(6, 4, 16)    // N=64:   4 threads
 FG_STOCKHAM(7, 4, 8)     // N=128:  8 threads
 FG_STOCKHAM(8, 4, 4)     // N=256:  16 threads
 FG_STOCKHAM(9, 4, 2)     // N=512:  32 threads
-FG_STOCKHAM(10, 4, 1)    // N=1024: 64 threads (one wave per transform)
+FG_STOCKHAM(10, 4, 2)    // N=1024: 64 threads (one wave) per transform, 2 per workgroup
 FG_STOCKHAM(11, 4, 1)    // N=2048: 128 threads
 FG_STOCKHAM(12, 4, 1)    // N=4096: 256 threads
 FG_STOCKHAM_SC(4, 4, 64)
@@ -60,7 +60,7 @@ FG_STOCKHAM_SC(6, 4, 16)
 FG_STOCKHAM_SC(7, 4, 8)
 FG_STOCKHAM_SC(8, 4, 4)
 FG_STOCKHAM_SC(9, 4, 2)
-FG_STOCKHAM_SC(10, 4, 1)
+FG_STOCKHAM_SC(10, 4, 2)
 FG_STOCKHAM_SC(11, 4, 1)
 FG_STOCKHAM_SC(12, 4, 1)
 
@@ -168,7 +168,7 @@ FG_TILE(8, 32, false, c)
 FG_TILE(9, 16, false, c)
 FG_TILE(10, 16, false, c)
 // 2D column FFTs of 2048 / 4096 rows in one pass: 8 / 4 columns per tile
-// (1024 threads, 136 KB of LDS), read in XCD-aware tile order.
+// (1024 threads, 136 KB of LDS), XCD-aware tile order.
 FG_TILE(11, 8, false, c)
 FG_TILE(12, 4, false, c)
 // Row passes (last 1D digit: rows contiguous, transposed store).

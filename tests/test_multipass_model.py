@@ -25,7 +25,10 @@ from conftest import rel_l2, uniform_c64
 
 
 def tile_columns(log_l):
-    """Columns per tile (tile_columns in fft_plan.cpp)."""
+    """Columns per tile (tile_columns in fft_plan.cpp): 16..64 up to 1024 points,
+    8 / 4 (narrow tiles) for 2048 / 4096."""
+    if log_l > 10:
+        return 16384 >> log_l
     return max(16, min(64, 8192 >> log_l))
 
 
@@ -76,18 +79,13 @@ def tile_geometry_1d(log_n, batch):
     return passes
 
 
-def column_tile_width(log_rows):
-    """Columns per tile of the one-pass 2D column FFT (column_tile_width in fft_plan.cpp)."""
-    return tile_columns(log_rows) if log_rows <= 10 else 16384 >> log_rows
-
-
 def tile_geometry_2d(log_n, batch, log_cols=None):
     """Column FFT of each R x C image after the row pass, as FftPlan::make_2d builds it
     (R = 2^log_n rows, C = 2^log_cols columns, square by default): one tile pass over
-    min(column_tile_width(R), C) adjacent columns of length R, in place."""
+    min(tile_columns(R), C) adjacent columns of length R, in place."""
     R = 1 << log_n
     C = R if log_cols is None else 1 << log_cols
-    g = min(column_tile_width(log_n), C)
+    g = min(tile_columns(log_n), C)
     return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
                  is0=g, is1=0, is2=R * C, ics=1, ies=C,
                  os0=g, os1=0, os2=R * C, ocs=1, oes=C,
@@ -205,9 +203,9 @@ def test_tile_lds_layout_is_injective_and_fits(log_l, g):
 
 
 def test_long_column_widths():
-    # 2048 / 4096-row columns: 8 / 4 per tile, 1024 threads of 16 elements
+    # 2048 / 4096-point digits: 8 / 4 columns per tile, 1024 threads of 16 elements
     for log_n, g in ((11, 8), (12, 4)):
-        assert column_tile_width(log_n) == g
+        assert tile_columns(log_n) == g
         assert g * (1 << log_n) // 16 == 1024
 
 
@@ -215,4 +213,4 @@ def test_split_sizes_fit_the_tile_kernel():
     for log_n in range(13, 25):
         logs = split_1d(log_n)
         assert sum(logs) == log_n
-        assert all(4 <= l <= 11 for l in logs), (log_n, logs)
+        assert all(4 <= l <= 10 for l in logs), (log_n, logs)   # wide tiles only

@@ -89,7 +89,8 @@ def planned_kernels():
     for log_n in range(13, 25):
         passes = tile_geometry_1d(log_n, 1)
         for i, p in enumerate(passes):
-            for pol in policies(i, len(passes)):
+            # narrow tiles (g < 16) always load and store cached
+            for pol in (("_cc",) if p["g"] < 16 else policies(i, len(passes))):
                 names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}{pol}")
     for lr in range(4, 13):
         for lc in range(4, 13):

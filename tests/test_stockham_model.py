@@ -20,7 +20,7 @@ from conftest import rel_l2, uniform_c64
 
 # kStockham in fft_plan.cpp / FG_STOCKHAM in fft_kernels.hip: (log_e, fpb)
 GEOM = {2: (2, 64), 3: (3, 64), 4: (4, 64), 5: (4, 32), 6: (4, 16), 7: (4, 8), 8: (4, 4),
-        9: (4, 2), 10: (4, 1), 11: (4, 1), 12: (4, 1)}
+        9: (4, 2), 10: (4, 2), 11: (4, 1), 12: (4, 1)}
 
 
 def row_exponents(r):
