@@ -172,13 +172,16 @@ std::string tile_name(uint32_t log_l, uint32_t g, bool rowwise, const char* poli
 
 }  // namespace
 
-const void* FftPlan::stage_table(uint32_t log_l) {
+const void* FftPlan::stage_table(uint32_t log_l, uint32_t log_e) {
+    // One table per (length, elements per thread): the radix list, and so the
+    // table, depends on both.
+    const uint32_t key = log_l * 64 + log_e;
     for (auto& e : stage_tables_)
-        if (e.first == log_l) return e.second.data();
-    auto tw = stockham_twiddles(log_l, elems_per_thread_log(log_l));
+        if (e.first == key) return e.second.data();
+    auto tw = stockham_twiddles(log_l, log_e);
     Buffer<Cf32, HipBackend> b = dev_->alloc<Cf32>(tw.size());
     b.copy_from_host(tw.data(), tw.size());
-    stage_tables_.emplace_back(log_l, std::move(b));
+    stage_tables_.emplace_back(key, std::move(b));
     return stage_tables_.back().second.data();
 }
 
@@ -203,7 +206,7 @@ void FftPlan::add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64
     s.fpb = g.fpb;
     s.src = src;
     s.dst = dst;
-    s.tw = stage_table(log_l);
+    s.tw = stage_table(log_l, g.log_e);
     s.per_unit = per_unit;
     steps_.push_back(s);
 }
@@ -228,7 +231,7 @@ void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g
     s.block = Dim3(g * ((1u << log_l) >> elems_per_thread_log(log_l)));
     s.src = src;
     s.dst = dst;
-    s.tw = stage_table(log_l);
+    s.tw = stage_table(log_l, elems_per_thread_log(log_l));
     s.geom = geom;
     s.per_unit = tiles_per_unit;
     steps_.push_back(s);

@@ -110,9 +110,10 @@ private:
     FftPlan(HipDevice& dev, Kind kind, uint32_t log_n, uint32_t log_rows, size_t batch)
         : dev_(&dev), kind_(kind), log_n_(log_n), log_rows_(log_rows), batch_(batch), chunk_(batch) {}
 
-    // Stage table for a length-2^log_l Stockham transform (uploaded once per plan).
     float scale_for(Direction dir, bool normalize) const;
-    const void* stage_table(uint32_t log_l);
+    // Stage table for a length-2^log_l Stockham transform with 2^log_e elements
+    // per thread (uploaded once per plan).
+    const void* stage_table(uint32_t log_l, uint32_t log_e);
     const void* big_table();
     void add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t per_unit, Buf src, Buf dst,
                       const char* policy = "");
