@@ -30,6 +30,15 @@ constexpr StockhamGeom kStockham[kMaxLogNSingle + 1] = {
     {0, 0}, {0, 0},          // log_n 0, 1: unsupported
     {2, 64}, {3, 64}, {4, 64}, {4, 32}, {4, 16}, {4, 8}, {4, 4}, {4, 2}, {4, 2}, {4, 1}, {4, 1},
 };
+// Latency geometry (fg_fft_n<L>_lat, one transform per workgroup, fewer
+// elements per thread: more threads per transform, shorter serial chains),
+// for single-pass plans too small to fill the GPU.  {0, 0}: none.  Measured
+// with graph replay at batch 256: N = 256 5.75 -> 4.58 us per launch pair,
+// N = 1024 3.94 -> 3.65 us, N = 4096 10.94 -> 10.69 us.
+constexpr StockhamGeom kStockhamLatency[kMaxLogNSingle + 1] = {
+    {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0},
+    {2, 1}, {0, 0}, {3, 1}, {0, 0}, {3, 1},
+};
 
 std::string file_image;  // backing store when FERRUM_GPU_CODE_OBJECT is set
 
@@ -194,11 +203,18 @@ const void* FftPlan::big_table() {
     return big_.data();
 }
 
+bool use_latency_geometry(uint32_t log_n, uint64_t count, int cu_count) {
+    // The throughput geometry would give fewer than two workgroups per CU.
+    const StockhamGeom t = kStockham[log_n], l = kStockhamLatency[log_n];
+    return l.fpb != 0 && (count + t.fpb - 1) / t.fpb < 2ull * (uint64_t)cu_count;
+}
+
 void FftPlan::add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t per_unit, Buf src, Buf dst,
-                           const char* policy) {
-    const StockhamGeom g = kStockham[log_l];
+                           const char* policy, bool latency) {
+    const StockhamGeom g = latency ? kStockhamLatency[log_l] : kStockham[log_l];
+    if (g.fpb == 0) fail(FG_ERR_INTERNAL, "no latency geometry for this length");
     Step s;
-    s.name = "fg_fft_n" + std::to_string(log_l) + policy;
+    s.name = "fg_fft_n" + std::to_string(log_l) + (latency ? "_lat" : "") + policy;
     s.fn = HipBackend::get_kernel(mod, s.name.c_str());
     const uint64_t blocks = (per_unit * chunk_ + g.fpb - 1) / g.fpb;
     if (blocks > 0x7fffffffull) invalid("batch too large for one launch");
@@ -245,7 +261,8 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
     if (batch == 0) invalid("batch must be positive");
     if (log_n <= kMaxLogNSingle) {
         std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::Stockham1D, log_n, 0, batch));
-        p->add_stockham(mod, log_n, 1, Buf::In, Buf::Out);
+        const bool latency = use_latency_geometry(log_n, batch, dev.handle()->cu_count);
+        p->add_stockham(mod, log_n, 1, Buf::In, Buf::Out, "", latency);
         p->main_kernel_ = p->steps_[0].name;
         p->split_fn_ = HipBackend::get_kernel(mod, (p->main_kernel_ + "_split").c_str());
         p->pw_ = Pointwise(mod);
@@ -480,7 +497,7 @@ void FftPlan::exec_split(const void* in_re, const void* in_im, void* out_re, voi
         (out_re != in_re && overlap(out_re, in_re)) || (out_im != in_im && overlap(out_im, in_im)))
         invalid("fft exec_split: overlapping buffers (only out_re == in_re and out_im == in_im may alias)");
     if (split_fn_) {
-        const Step& s = steps_[0];
+        const Step& s = steps_[0];  // the split twin has the same geometry and table
         uint32_t flags = dir == Direction::Inverse ? (FG_PASS_CONJ_IN | FG_PASS_CONJ_SCALE_OUT) : 0u;
         float sc = scale_for(dir, normalize);
         const void* tw = s.tw;

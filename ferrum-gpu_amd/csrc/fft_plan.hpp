@@ -116,7 +116,7 @@ private:
     const void* stage_table(uint32_t log_l, uint32_t log_e);
     const void* big_table();
     void add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64_t per_unit, Buf src, Buf dst,
-                      const char* policy = "");
+                      const char* policy = "", bool latency = false);
     // Narrow tiles (g < 16) override `policy` with "_cc" (fft_plan.cpp).
     void add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g, bool rowwise, const TileGeom& geom,
                   uint64_t tiles_per_unit, Buf src, Buf dst, const char* policy);
@@ -137,7 +137,7 @@ private:
     Buffer<Cf32, HipBackend> big_;
     Buffer<Cf32, HipBackend> work_;
     std::string main_kernel_;
-    HipBackend::KernelHandle split_fn_ = nullptr;  // single-pass plans: the split-layout kernel
+    HipBackend::KernelHandle split_fn_ = nullptr;  // single-pass plans: the split-layout twin
     Pointwise pw_;
     mutable std::mutex stage_mu_;                   // guards the lazy allocation of stage_
     mutable Buffer<Cf32, HipBackend> stage_;        // split layout staging of multi-launch plans
@@ -168,6 +168,9 @@ void set_chunk_limit_bytes(size_t bytes);
 // Units per chunk for `unit_bytes` per transform (image), and whether the
 // chunk's intermediates are kept cached, under the given limit.
 size_t chunk_units_for(uint64_t unit_bytes, size_t batch, size_t limit, bool* cached);
+// Whether a single-pass plan of `count` transforms of 2^log_n points runs the
+// latency geometry (fg_fft_n<L>_lat) on a device with `cu_count` CUs.
+bool use_latency_geometry(uint32_t log_n, uint64_t count, int cu_count);
 // Launch the tiled transpose out[b][c][r] = in[b][r][c] on `stream`.
 void transpose_c64(HipDevice& dev, const HipBackend::Module& mod, const void* in, void* out, uint32_t rows,
                    uint32_t cols, size_t batch, hipStream_t stream);

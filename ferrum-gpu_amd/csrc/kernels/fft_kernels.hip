@@ -54,6 +54,28 @@ FG_STOCKHAM(9, 4, 2)     // N=512:  32 threads
 FG_STOCKHAM(10, 4, 2)    // N=1024: 64 threads (one wave) per transform, 2 per workgroup
 FG_STOCKHAM(11, 4, 1)    // N=2048: 128 threads
 FG_STOCKHAM(12, 4, 1)    // N=4096: 256 threads
+// fg_fft_n<L>_lat[_split]: one transform per workgroup with fewer elements per
+// thread (kStockhamLatency in fft_plan.cpp), for batches too small to fill the
+// GPU; the split twin keeps split and interleaved results bit-identical.
+#define FG_STOCKHAM_LAT(LOGN, LOGE)                                                            \
+    extern "C" __global__ __launch_bounds__((1 << LOGN) >> LOGE) void                           \
+        fg_fft_n##LOGN##_lat(const float2* __restrict__ in, float2* __restrict__ out,           \
+                             const float2* __restrict__ tw, uint64_t batch, float scale,       \
+                             uint32_t flags) {                                                 \
+        fft_stockham_body<LOGN, LOGE, 1>(InterleavedIO{in, out}, tw, batch, scale, flags);     \
+    }                                                                                          \
+    extern "C" __global__ __launch_bounds__((1 << LOGN) >> LOGE) void                           \
+        fg_fft_n##LOGN##_lat_split(const float* __restrict__ in_re, const float* __restrict__ in_im, \
+                                   float* __restrict__ out_re, float* __restrict__ out_im,      \
+                                   const float2* __restrict__ tw, uint64_t batch, float scale,  \
+                                   uint32_t flags) {                                           \
+        fft_stockham_body<LOGN, LOGE, 1>(SplitIO{in_re, in_im, out_re, out_im}, tw, batch,     \
+                                         scale, flags);                                        \
+    }
+FG_STOCKHAM_LAT(8, 2)    // N=256:  64 threads (4 elements each)
+FG_STOCKHAM_LAT(10, 3)   // N=1024: 128 threads (8 elements each)
+FG_STOCKHAM_LAT(12, 3)   // N=4096: 512 threads (8 elements each)
+
 FG_STOCKHAM_SC(4, 4, 64)
 FG_STOCKHAM_SC(5, 4, 32)
 FG_STOCKHAM_SC(6, 4, 16)
@@ -140,7 +162,7 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
         fg_tile_l##LOGL##_g##G##_##TAG(const float2* __restrict__ in, float2* __restrict__ out,     \
                                        const float2* __restrict__ tw, const float2* __restrict__ big, \
                                        TileGeom g) {                                                  \
-        fft_tile_body<LOGL, (LOGL < 4 ? LOGL : 4), G, RW, true, LC, SC>(in, out, tw, big, g);        \
+        fft_tile_pass<LOGL, (LOGL < 4 ? LOGL : 4), G, RW, true, LC, SC>(in, out, tw, big, g);        \
     }
 #define FG_TILE(LOGL, G, RW, TAG)                  \
     FG_TILE_P(LOGL, G, RW, TAG, false, false)      \

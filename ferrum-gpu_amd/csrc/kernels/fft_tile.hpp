@@ -67,10 +67,19 @@ struct TileLayout {
         if constexpr (PADPOS) return lds_pos(pos) * G + c;
         else return pos * (G + 1) + c;
     }
+    // at(pos + D, c) - at(pos, c) for a step D that is a multiple of 16 (any D
+    // without position padding): lds_pos(p + 16u) = lds_pos(p) + 17u.
+    template <int D>
+    static constexpr int step() {
+        static_assert(!PADPOS || D % 16 == 0, "position-padded steps must be multiples of 16");
+        return PADPOS ? (D + D / 16) * G : D * (G + 1);
+    }
 };
 
 // Stockham stages on a [position][column] LDS tile: thread (c, q) holds
-// positions q + T*m of column c.
+// positions q + T*m of column c.  LDS addresses are a per-thread base plus
+// compile-time offsets (ds_read / ds_write immediates) wherever the layout
+// allows.
 template <int LOGL, int LOGE, int G, int S>
 struct TileStages {
     using Sh = StockhamShape<LOGL, LOGE>;
@@ -82,14 +91,34 @@ struct TileStages {
             constexpr int LOGR = (S < Sh::NFULL) ? LOGE : Sh::REM;
             constexpr int NB = Sh::E >> LOGR;
             constexpr int R = 1 << LOGR;
+            constexpr int L = 1 << (S * LOGE);
             __syncthreads();  // previous readers of the tile are done
 #pragma unroll
-            for (int i = 0; i < NB; ++i)
+            for (int i = 0; i < NB; ++i) {
+                if constexpr (Lay::PADPOS && L == 1 && R == 16) {
+                    // dst = 16*b + r, r < 16: lds_pos = 17*b + r
+                    float2* base = lds + Lay::at(16 * (q + Sh::T * i), c);
 #pragma unroll
-                for (int r = 0; r < R; ++r) lds[Lay::at(stockham_dst<LOGL, LOGE, S>(q, i, r), c)] = x[i + NB * r];
+                    for (int r = 0; r < R; ++r) base[r * G] = x[i + NB * r];
+                } else if constexpr (!Lay::PADPOS || L % 16 == 0) {
+                    // dst = dst(i, 0) + r*L
+                    float2* base = lds + Lay::at(stockham_dst<LOGL, LOGE, S>(q, i, 0), c);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) base[r * Lay::template step<L>()] = x[i + NB * r];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) lds[Lay::at(stockham_dst<LOGL, LOGE, S>(q, i, r), c)] = x[i + NB * r];
+                }
+            }
             __syncthreads();
+            if constexpr (!Lay::PADPOS || Sh::T % 16 == 0) {
+                const float2* base = lds + Lay::at(q, c);
 #pragma unroll
-            for (int m = 0; m < Sh::E; ++m) x[m] = lds[Lay::at(q + Sh::T * m, c)];
+                for (int m = 0; m < Sh::E; ++m) x[m] = base[m * Lay::template step<Sh::T>()];
+            } else {
+#pragma unroll
+                for (int m = 0; m < Sh::E; ++m) x[m] = lds[Lay::at(q + Sh::T * m, c)];
+            }
             TileStages<LOGL, LOGE, G, S + 1>::run(x, q, c, tw, lds);
         }
     }
@@ -100,14 +129,19 @@ struct TileStages {
 // first; otherwise columns are contiguous (ics == 1) and each thread loads its
 // own Stockham positions straight into VGPRs.  Output always has ocs == 1.
 // LOAD_CACHED / STORE_CACHED select the pass's cache policy (gload/gstore).
-template <int LOGL, int LOGE, int G, bool ROWWISE, bool TWREC, bool LOAD_CACHED, bool STORE_CACHED>
+// CONJ: the body reads the inverse's conjugation flags; forward passes
+// (flags == 0) run the CONJ = false body, which has no per-element selects.
+// Global addresses are a wave-uniform row base (scalar registers) plus a
+// 32-bit per-lane byte offset, so each access costs no 64-bit vector
+// arithmetic; a tile's offsets stay below 2^32 bytes (one transform or image
+// spans at most 128 MiB).
+template <int LOGL, int LOGE, int G, bool ROWWISE, bool TWREC, bool LOAD_CACHED, bool STORE_CACHED, bool CONJ>
 __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, float2* __restrict__ out,
                                               const float2* __restrict__ tw, const float2* __restrict__ big,
-                                              const TileGeom& g) {
+                                              const TileGeom& g, float2* __restrict__ lds) {
     using Sh = StockhamShape<LOGL, LOGE>;
     using Lay = TileLayout<LOGL, G>;
     constexpr int THREADS = G * Sh::T;
-    __shared__ float2 lds[Lay::ELEMS];
 
     const int tid = threadIdx.x;
     const int c = tid % G;
@@ -127,6 +161,8 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
     const uint32_t t2 = b / g.t1n;
     const uint64_t ib = t0 * g.is0 + t1 * g.is1 + (uint64_t)t2 * g.is2;
     const uint64_t ob = t0 * g.os0 + t1 * g.os1 + (uint64_t)t2 * g.os2;
+    const char* in_tile = reinterpret_cast<const char*>(in + ib);
+    char* out_tile = reinterpret_cast<char*>(out + ob);
 
     float2 x[Sh::E];
     if constexpr (ROWWISE) {
@@ -136,18 +172,30 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
             const int li = tid + THREADS * m;
             const int cc = li >> LOGL;
             const int n = li & (Sh::N - 1);
-            lds[Lay::at(n, cc)] = gload<LOAD_CACHED>(in + ib + (uint64_t)cc * g.ics + n);
+            const uint32_t off = (uint32_t)((cc * g.ics + n) * sizeof(float2));
+            lds[Lay::at(n, cc)] = gload<LOAD_CACHED>(reinterpret_cast<const float2*>(in_tile + off));
         }
         __syncthreads();
+        if constexpr (!Lay::PADPOS || Sh::T % 16 == 0) {
+            const float2* base = lds + Lay::at(q, c);
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = lds[Lay::at(q + Sh::T * m, c)];
+            for (int m = 0; m < Sh::E; ++m) x[m] = base[m * Lay::template step<Sh::T>()];
+        } else {
+#pragma unroll
+            for (int m = 0; m < Sh::E; ++m) x[m] = lds[Lay::at(q + Sh::T * m, c)];
+        }
     } else {
+        const uint32_t lane_off = (uint32_t)((c + (uint64_t)q * g.ies) * sizeof(float2));
+        const uint64_t row_step = (uint64_t)Sh::T * g.ies * sizeof(float2);
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = gload<LOAD_CACHED>(in + ib + c + (uint64_t)(q + Sh::T * m) * g.ies);
+        for (int m = 0; m < Sh::E; ++m)
+            x[m] = gload<LOAD_CACHED>(reinterpret_cast<const float2*>(in_tile + m * row_step + lane_off));
     }
-    if (g.flags & FG_PASS_CONJ_IN) {
+    if constexpr (CONJ) {
+        if (g.flags & FG_PASS_CONJ_IN) {
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = cconj(x[m]);
+            for (int m = 0; m < Sh::E; ++m) x[m] = cconj(x[m]);
+        }
     }
     TileStages<LOGL, LOGE, G, 0>::run(x, q, c, tw, lds);
 
@@ -155,14 +203,29 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
         const uint64_t r = (uint64_t)g.twc * c + (uint64_t)g.tw0 * t0 + (uint64_t)g.tw1 * t1;
         apply_pass_twiddle<Sh::E, Sh::T, TWREC>(x, big, r, q, g.log_m);
     }
-    const bool cs = (g.flags & FG_PASS_CONJ_SCALE_OUT) != 0;
+    const uint32_t lane_off = (uint32_t)((c + (uint64_t)q * g.oes) * sizeof(float2));
+    const uint64_t row_step = (uint64_t)Sh::T * g.oes * sizeof(float2);
+    const bool cs = CONJ && (g.flags & FG_PASS_CONJ_SCALE_OUT) != 0;
 #pragma unroll
     for (int m = 0; m < Sh::E; ++m) {
-        const int k = q + Sh::T * m;
         float2 v = x[m];
-        if (cs) v = cscale(cconj(v), g.scale);
-        gstore<STORE_CACHED>(out + ob + c + (uint64_t)k * g.oes, v);
+        if constexpr (CONJ) {
+            if (cs) v = cscale(cconj(v), g.scale);
+        }
+        gstore<STORE_CACHED>(reinterpret_cast<float2*>(out_tile + m * row_step + lane_off), v);
     }
+}
+
+// One pass: a forward body and one that applies the inverse's conjugations.
+template <int LOGL, int LOGE, int G, bool ROWWISE, bool TWREC, bool LOAD_CACHED, bool STORE_CACHED>
+__device__ __forceinline__ void fft_tile_pass(const float2* __restrict__ in, float2* __restrict__ out,
+                                              const float2* __restrict__ tw, const float2* __restrict__ big,
+                                              const TileGeom& g) {
+    __shared__ float2 lds[TileLayout<LOGL, G>::ELEMS];
+    if (g.flags)
+        fft_tile_body<LOGL, LOGE, G, ROWWISE, TWREC, LOAD_CACHED, STORE_CACHED, true>(in, out, tw, big, g, lds);
+    else
+        fft_tile_body<LOGL, LOGE, G, ROWWISE, TWREC, LOAD_CACHED, STORE_CACHED, false>(in, out, tw, big, g, lds);
 }
 
 }  // namespace fg

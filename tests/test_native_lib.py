@@ -71,6 +71,8 @@ def instantiated_kernels():
     names = {f"fg_fft_n{m.group(1)}" for m in re.finditer(r"^FG_STOCKHAM\((\d+),", src, flags=re.M)}
     names |= {f"{n}_split" for n in names}
     names |= {f"fg_fft_n{m.group(1)}_sc" for m in re.finditer(r"^FG_STOCKHAM_SC\((\d+),", src, flags=re.M)}
+    for m in re.finditer(r"^FG_STOCKHAM_LAT\((\d+),", src, flags=re.M):
+        names |= {f"fg_fft_n{m.group(1)}_lat", f"fg_fft_n{m.group(1)}_lat_split"}
     for m in re.finditer(r"^FG_TILE\((\d+), (\d+), (true|false), ([cr])\)", src, flags=re.M):
         base = f"fg_tile_l{m.group(1)}_g{m.group(2)}_{m.group(4)}"
         names |= {base + pol for pol in ("", "_sc", "_cc", "_cs")}  # cache policies (FG_TILE_P)
@@ -85,7 +87,10 @@ def planned_kernels():
         # unchunked: every pass streams; chunked: first _sc, middle _cc, last _cs
         return ("", "_sc" if i == 0 else ("_cs" if i == n - 1 else "_cc"))
 
+    from test_stockham_model import LATENCY_GEOM
+
     names = {f"fg_fft_n{l}" for l in range(2, 13)} | {f"fg_fft_n{l}_split" for l in range(2, 13)}
+    names |= {f"fg_fft_n{l}_lat{sfx}" for l in LATENCY_GEOM for sfx in ("", "_split")}
     for log_n in range(13, 25):
         passes = tile_geometry_1d(log_n, 1)
         for i, p in enumerate(passes):

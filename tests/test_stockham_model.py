@@ -21,6 +21,8 @@ from conftest import rel_l2, uniform_c64
 # kStockham in fft_plan.cpp / FG_STOCKHAM in fft_kernels.hip: (log_e, fpb)
 GEOM = {2: (2, 64), 3: (3, 64), 4: (4, 64), 5: (4, 32), 6: (4, 16), 7: (4, 8), 8: (4, 4),
         9: (4, 2), 10: (4, 2), 11: (4, 1), 12: (4, 1)}
+# kStockhamLatency / FG_STOCKHAM_LAT: single-pass plans too small to fill the GPU
+LATENCY_GEOM = {8: (2, 1), 10: (3, 1), 12: (3, 1)}
 
 
 def row_exponents(r):
@@ -119,6 +121,14 @@ def test_model_matches_oracle(log_n):
     assert rel_l2(model(x, log_n, log_e), oracle.fft_1d(x, log_n)) < 1e-5
 
 
+@pytest.mark.parametrize("log_n", sorted(LATENCY_GEOM))
+def test_model_matches_oracle_latency_geometry(log_n):
+    rng = np.random.default_rng(log_n + 50)
+    x = uniform_c64(rng, 3 << log_n)
+    log_e, _ = LATENCY_GEOM[log_n]
+    assert rel_l2(model(x, log_n, log_e), oracle.fft_1d(x, log_n)) < 1e-5
+
+
 @pytest.mark.parametrize("log_n,log_e", [(10, 3), (12, 3), (11, 2), (9, 5), (12, 6)])
 def test_model_other_radices(log_n, log_e):
     rng = np.random.default_rng(log_n * 7 + log_e)
@@ -129,7 +139,7 @@ def test_model_other_radices(log_n, log_e):
 def test_twiddle_rows_are_16_byte_aligned():
     # The kernel loads table rows as float4 pairs: every block offset and row
     # length must be even (8-byte entries -> 16-byte aligned rows).
-    for log_n, (log_e, _) in GEOM.items():
+    for log_n, (log_e, _) in list(GEOM.items()) + list(LATENCY_GEOM.items()):
         _, offs = stockham_table(log_n, log_e)
         assert all(o % 2 == 0 for o in offs), log_n
     assert all(len(row_exponents(r)) % 2 == 0 for r in (2, 4, 8, 16))
@@ -173,8 +183,30 @@ def test_staged_block_mapping_covers_each_element_once():
 
 
 def test_geometry_fits_hardware():
-    for log_n, (log_e, fpb) in GEOM.items():
+    for log_n, (log_e, fpb) in list(GEOM.items()) + list(LATENCY_GEOM.items()):
         threads = ((1 << log_n) >> log_e) * fpb
         assert 1 <= threads <= 1024
         lds = fpb * ((1 << log_n) + (1 << log_n) // 16) * 8
         assert lds <= 64 * 1024, (log_n, lds)
+
+
+def test_geometry_tables_match_the_sources():
+    # the mirrors above equal the host tables and the kernel instantiations
+    import os
+    import re
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    plan = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "fft_plan.cpp")).read()
+    hip = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
+
+    def table(name):
+        body = re.search(name + r"\[kMaxLogNSingle \+ 1\] = \{(.*?)\};", plan, flags=re.S).group(1)
+        body = re.sub(r"//[^\n]*", "", body)
+        return [tuple(int(v) for v in m) for m in re.findall(r"\{(\d+), (\d+)\}", body)]
+
+    assert {n: g for n, g in enumerate(table("kStockham")) if g != (0, 0)} == GEOM
+    assert {n: g for n, g in enumerate(table("kStockhamLatency")) if g != (0, 0)} == LATENCY_GEOM
+    inst = {int(a): (int(b), int(c)) for a, b, c in re.findall(r"^FG_STOCKHAM\((\d+), (\d+), (\d+)\)", hip, flags=re.M)}
+    assert inst == GEOM
+    lat = {int(a): (int(b), 1) for a, b in re.findall(r"^FG_STOCKHAM_LAT\((\d+), (\d+)\)", hip, flags=re.M)}
+    assert lat == LATENCY_GEOM
