@@ -31,10 +31,18 @@ struct fg_device {
     std::unique_ptr<HipDevice> dev;
     HipBackend::Module fft_module;
     std::mutex mu;  // guards the plan cache and the staging buffer of the host path
-    // key: (dims, log_n or log_cols, log_rows (0 for 1D), batch)
-    std::map<std::tuple<int, uint32_t, uint32_t, size_t>, std::unique_ptr<FftPlan>> plans;
+    // Host-path plans, key: (dims, log_n or log_cols, log_rows (0 for 1D), batch);
+    // the kCachedPlans most recently used are kept (a multi-pass plan holds up
+    // to a 128 MiB workspace, so the cache must not grow with every new batch).
+    struct CachedPlan {
+        std::unique_ptr<FftPlan> plan;
+        uint64_t last_use = 0;
+    };
+    std::map<std::tuple<int, uint32_t, uint32_t, size_t>, CachedPlan> plans;
+    uint64_t plan_clock = 0;
     Buffer<Cf32, HipBackend> staging;
     fg::Pointwise pointwise;  // elementwise kernels of fft_module
+    std::atomic<int> dependents{0};  // live plans and captured graphs made on this device
 };
 
 struct fg_module {
@@ -122,14 +130,28 @@ fg_device* default_device() {
     return dev;
 }
 
+constexpr size_t kCachedPlans = 8;
+
+// Caller holds d->mu, which also covers every use of the returned plan, so an
+// evicted plan is never in use.
 FftPlan& cached_plan(fg_device* d, int dims, uint32_t log_n, uint32_t log_rows, size_t batch) {
     auto key = std::make_tuple(dims, log_n, log_rows, batch);
+    const uint64_t now = ++d->plan_clock;
     auto it = d->plans.find(key);
-    if (it != d->plans.end()) return *it->second;
+    if (it != d->plans.end()) {
+        it->second.last_use = now;
+        return *it->second.plan;
+    }
     auto p = dims == 1 ? FftPlan::make_1d(*d->dev, d->fft_module, log_n, batch)
                        : FftPlan::make_2d(*d->dev, d->fft_module, log_rows, log_n, batch);
+    if (d->plans.size() >= kCachedPlans) {
+        auto oldest = d->plans.begin();
+        for (auto e = d->plans.begin(); e != d->plans.end(); ++e)
+            if (e->second.last_use < oldest->second.last_use) oldest = e;
+        d->plans.erase(oldest);
+    }
     FftPlan& ref = *p;
-    d->plans.emplace(key, std::move(p));
+    d->plans[key] = fg_device::CachedPlan{std::move(p), now};
     return ref;
 }
 
@@ -182,6 +204,9 @@ int fg_device_open(int ordinal, fg_device_t* out) {
 int fg_device_close(fg_device_t dev) {
     return guarded([&] {
         if (!dev) return;
+        if (dev->dependents.load() > 0)
+            fg::invalid("device still has " + std::to_string(dev->dependents.load()) +
+                        " plan(s) or graph(s); destroy them first");
         try {
             dev->dev->sync();
         } catch (...) {
@@ -415,6 +440,7 @@ int fg_fft_plan_1d(fg_device_t dev, uint32_t log_n, size_t batch, fg_fft_plan_t*
         std::unique_ptr<fg_fft_plan> p(new fg_fft_plan);
         p->dev = dev;
         p->plan = FftPlan::make_1d(*dev->dev, dev->fft_module, log_n, batch);
+        dev->dependents.fetch_add(1);
         *out = p.release();
     });
 }
@@ -427,15 +453,18 @@ int fg_fft_plan_2d(fg_device_t dev, uint32_t log_n, size_t batch, fg_fft_plan_t*
         std::unique_ptr<fg_fft_plan> p(new fg_fft_plan);
         p->dev = dev;
         p->plan = FftPlan::make_2d(*dev->dev, dev->fft_module, log_n, log_n, batch);
+        dev->dependents.fetch_add(1);
         *out = p.release();
     });
 }
 
 int fg_fft_plan_destroy(fg_fft_plan_t plan) {
     return guarded([&] {
-        if (plan && plan->graphs.load() > 0)
+        if (!plan) return;
+        if (plan->graphs.load() > 0)
             fg::invalid("plan still has " + std::to_string(plan->graphs.load()) +
                         " graph(s); destroy them first");
+        plan->dev->dependents.fetch_sub(1);
         delete plan;
     });
 }
@@ -519,6 +548,7 @@ int fg_graph_capture_end(fg_device_t dev, fg_stream_t capture_stream, fg_graph_t
         std::unique_ptr<fg_graph> g(new fg_graph);
         g->g = HipBackend::end_capture(dev->dev->handle(), (hipStream_t)capture_stream);
         g->dev = dev;
+        dev->dependents.fetch_add(1);
         *out = g.release();
     });
 }
@@ -541,7 +571,10 @@ int fg_graph_node_count(fg_graph_t graph, size_t* nodes) {
 int fg_graph_destroy(fg_graph_t graph) {
     return guarded([&] {
         if (!graph) return;
-        if (graph->plan) graph->plan->graphs.fetch_sub(1);
+        if (graph->plan)
+            graph->plan->graphs.fetch_sub(1);  // the plan holds the device
+        else
+            graph->dev->dependents.fetch_sub(1);
         delete graph;
     });
 }
@@ -656,6 +689,7 @@ int fg_fft_plan_2d_rect(fg_device_t dev, uint32_t log_rows, uint32_t log_cols, s
         std::unique_ptr<fg_fft_plan> p(new fg_fft_plan);
         p->dev = dev;
         p->plan = FftPlan::make_2d(*dev->dev, dev->fft_module, log_rows, log_cols, batch);
+        dev->dependents.fetch_add(1);
         *out = p.release();
     });
 }

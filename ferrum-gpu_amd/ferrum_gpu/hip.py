@@ -64,8 +64,10 @@ class Device:
                 "clock_khz": clk.value}
 
     def close(self) -> None:
+        """Release the device; refused (FerrumGpuError) while plans or graphs
+        made on it are alive."""
         if getattr(self, "_h", None) is not None:
-            _n.lib.fg_device_close(self._h)
+            _n.check(_n.lib.fg_device_close(self._h))
             self._h = None
 
     def __del__(self):  # pragma: no cover - interpreter teardown order

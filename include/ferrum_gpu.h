@@ -71,7 +71,9 @@ FG_API int fg_device_count(int *count);
  * crates/ferrum-gpu-py/src/lib.rs:400-408): select the GPU, create its default
  * stream and load the FFT code object into the device's module cache. */
 FG_API int fg_device_open(int ordinal, fg_device_t *out);
-/* Drop of Device: waits for the default stream, frees what the device owns. */
+/* Drop of Device: waits for the default stream, frees what the device owns.
+ * Refused (FG_ERR_INVALID_ARGUMENT) while plans or captured graphs made on the
+ * device are alive: destroy them first. */
 FG_API int fg_device_close(fg_device_t dev);
 /* Device::sync (crates/ferrum-gpu/src/device.rs:36-38, py lib.rs:410-416). */
 FG_API int fg_device_sync(fg_device_t dev);

@@ -85,3 +85,26 @@ def test_events_and_stream_copy(gpu_device):
     out = np.empty_like(src)
     b.copy_to_host(out)
     assert np.array_equal(out, src)
+
+
+def test_device_close_waits_for_its_plans_and_graphs(gpu_device):
+    # A device cannot be closed while plans or captured graphs made on it
+    # live (they refer to it); after they are destroyed it closes.
+    import ferrum_gpu
+    from ferrum_gpu._native import FerrumGpuError
+    from ferrum_gpu.hip import Capture, Device, DeviceBuffer
+
+    dev = Device(0)
+    plan = ferrum_gpu.fft.Plan1D(8, 4, dev)
+    buf = DeviceBuffer(dev, plan.nbytes)
+    with Capture(dev) as cap:
+        plan.execute(buf, buf, "forward", stream=cap.stream)
+    graph = cap.graph
+    with pytest.raises(FerrumGpuError, match="plan\\(s\\) or graph\\(s\\)"):
+        dev.close()
+    plan.destroy()
+    with pytest.raises(FerrumGpuError):
+        dev.close()          # the captured graph still refers to the device
+    graph.destroy()
+    buf.free()
+    dev.close()

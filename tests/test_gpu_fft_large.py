@@ -163,3 +163,18 @@ def test_config5_4096sq_b2(gpu_device):
     for k1, k2 in [(0, 0), (1, 4095), (2048, 7), (777, 3001)]:
         v = np.exp(-2j * np.pi * k1 * idx / n) @ img @ np.exp(-2j * np.pi * k2 * idx / n)
         assert abs(got[1, k1, k2] - v) <= 1e-4 * np.linalg.norm(img)
+
+
+def test_host_path_plan_cache_eviction(gpu_device):
+    # The host entry points keep the 8 most recently used plans per device:
+    # more distinct batches than that evict and re-create plans, every result
+    # stays correct (multi-pass plans, whose workspaces the bound protects).
+    import ferrum_gpu
+
+    rng = np.random.default_rng(77)
+    log_n = 14
+    batches = list(range(1, 12)) + [3, 1, 11]
+    for batch in batches:
+        x = uniform_c64(rng, batch << log_n)
+        y = ferrum_gpu.fft.fft_1d_c2c_pow2(x, log_n, device=gpu_device)
+        assert rel_l2(y, oracle.fft_1d(x, log_n)) <= TOL, batch
