@@ -20,7 +20,7 @@ from ferrum_gpu import _native as _n
 from ferrum_gpu.hip import Device, DeviceBuffer, Graph
 
 __all__ = ["fft_1d_c2c_pow2", "fft_2d_c2c_pow2", "fft2_c2c_pow2", "Plan1D", "Plan2D", "Graph", "transpose",
-           "MIN_LOG_N", "MAX_LOG_N", "MIN_LOG_N_2D", "MAX_LOG_N_2D"]
+           "set_chunk_bytes", "get_chunk_bytes", "MIN_LOG_N", "MAX_LOG_N", "MIN_LOG_N_2D", "MAX_LOG_N_2D"]
 
 MIN_LOG_N, MAX_LOG_N = 2, 24
 MIN_LOG_N_2D, MAX_LOG_N_2D = 4, 12

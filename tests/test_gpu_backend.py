@@ -108,3 +108,18 @@ def test_device_close_waits_for_its_plans_and_graphs(gpu_device):
     graph.destroy()
     buf.free()
     dev.close()
+
+
+def test_c_program_over_the_c_abi(gpu_device, capfd):
+    # examples/fft_c_abi.c drives the library from plain C (device, host and
+    # device-resident FFTs, the generator, plans, copies) and checks closed
+    # forms; its library build runs the same code in this process.
+    import os
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    lib = ctypes.CDLL(os.path.join(root, "ferrum-gpu_amd", "examples", "libfft_c_abi.so"))
+    lib.fft_c_abi_example.restype = ctypes.c_int
+    rc = lib.fft_c_abi_example()
+    out = capfd.readouterr().out
+    print(out)
+    assert rc == 0 and out.strip().endswith("OK"), out

@@ -243,3 +243,28 @@ def test_no_device_reports_cleanly():
         ferrum_gpu.hip.Device(0)
     with pytest.raises(ValueError, match=r"^ferrum-gpu fft error: "):
         ferrum_gpu.fft.fft_1d_c2c_pow2(np.zeros(16, np.complex64), 4)
+
+
+# ------------------------------------------------ the C ABI from plain C
+
+EXAMPLES = os.path.join(ROOT, "ferrum-gpu_amd", "examples")
+
+
+def test_header_is_plain_c(tmp_path):
+    # An FFI binding (bindgen, cgo, ctypes) reads the header as C.
+    src = tmp_path / "h.c"
+    src.write_text('#include "ferrum_gpu.h"\nint main(void) { return 0; }\n')
+    cmd = f"gcc -std=c99 -Wall -Wextra -pedantic -Werror -fsyntax-only -I{os.path.join(ROOT, 'include')} {src}"
+    assert os.system(cmd) == 0
+
+
+def test_c_example_is_built_against_the_library():
+    # make builds examples/fft_c_abi (executable) and libfft_c_abi.so (the same
+    # checks as fft_c_abi_example(), run in-process by the GPU tests).
+    exe = os.path.join(EXAMPLES, "fft_c_abi")
+    so = os.path.join(EXAMPLES, "libfft_c_abi.so")
+    assert os.path.exists(exe) and os.path.exists(so)
+    for f in (exe, so):
+        needed = os.popen(f"readelf -d {f}").read()
+        assert "libferrum_gpu.so" in needed, f
+    assert hasattr(ctypes.CDLL(so), "fft_c_abi_example")
