@@ -125,6 +125,66 @@ def cpu_model() -> str:
     return ""
 
 
+class ClockSampler:
+    """Samples the GPU's current shader clock from the kernel driver's sysfs
+    table (`pp_dpm_sclk`, the level marked `*`) every few ms while active,
+    the record the reference's bench keeps by locking clocks
+    (tools/bench-gpu-lock.sh).  Plain file reads; the first DRM card with the
+    table is taken (this build runs on one GPU).  Every failure leaves the
+    report empty rather than stopping the bench."""
+
+    def __init__(self, period_s: float = 0.002):
+        import glob
+
+        cards = sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
+        self.dir = os.path.dirname(cards[0]) if cards else None
+        self.period = period_s
+        self.samples: list[int] = []
+        self._stop = threading.Event()
+        self._thread = None
+
+    def _level(self, name: str):
+        try:
+            with open(os.path.join(self.dir, name)) as f:
+                for line in f:
+                    if line.rstrip().endswith("*"):
+                        return int(line.split(":")[1].strip().rstrip("*").strip().lower().rstrip("mhz"))
+        except (OSError, ValueError, IndexError):
+            return None
+        return None
+
+    def _run(self):
+        while not self._stop.is_set():
+            v = self._level("pp_dpm_sclk")
+            if v is not None:
+                self.samples.append(v)
+            self._stop.wait(self.period)
+
+    def __enter__(self):
+        if self.dir:
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self._thread:
+            self._thread.join()
+        return False
+
+    def report(self):
+        if not self.dir:
+            return None
+        import statistics
+
+        rep = {"source": self.dir + "/pp_dpm_{sclk,mclk}", "mclk_mhz": self._level("pp_dpm_mclk"),
+               "sclk_samples": len(self.samples)}
+        if self.samples:
+            rep["sclk_mhz_median"] = statistics.median(self.samples)
+            rep["sclk_mhz_max"] = max(self.samples)
+        return rep
+
+
 def in_threads(n_items: int, threads: int, part) -> None:
     """part(lo, hi) over [0, n_items) split across up to `threads` threads (the
     oracle's C calls drop the GIL)."""
@@ -510,6 +570,7 @@ def main() -> int:
     launches = len(wl.launch_names)
 
     per_kernel: dict[str, list[float]] = {}
+    clocks = ClockSampler()
     if not args.graph:
         for _ in range(args.warmup):
             wl.run(stream)
@@ -522,12 +583,13 @@ def main() -> int:
         start = Event(dev)
         evs = [[Event(dev) for _ in range(launches)] for _ in range(args.steps)]
         dev.sync()
-        t0 = time.perf_counter()
-        start.record(stream)
-        for k in range(args.steps):
-            wl.run(stream, evs[k])
-        dev.sync()
-        wall = time.perf_counter() - t0
+        with clocks:
+            t0 = time.perf_counter()
+            start.record(stream)
+            for k in range(args.steps):
+                wl.run(stream, evs[k])
+            dev.sync()
+            wall = time.perf_counter() - t0
         log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms")
         prev = start
         for k in range(args.steps):
@@ -548,13 +610,14 @@ def main() -> int:
         log(f"warmup {args.warmup} steps as graph replays done ({graph.node_count} nodes per graph)")
         start, end = Event(dev), Event(dev)
         dev.sync()
-        t0 = time.perf_counter()
-        start.record(stream)
-        for _ in range(args.steps // args.graph):
-            graph.launch(stream)
-        end.record(stream)
-        dev.sync()
-        wall = time.perf_counter() - t0
+        with clocks:
+            t0 = time.perf_counter()
+            start.record(stream)
+            for _ in range(args.steps // args.graph):
+                graph.launch(stream)
+            end.record(stream)
+            dev.sync()
+            wall = time.perf_counter() - t0
         per_launch = start.elapsed_ms(end) / (args.steps * launches)
         log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms as {args.steps // args.graph} graph replays")
         for key in wl.launch_keys:
@@ -637,6 +700,7 @@ def main() -> int:
         "host_path": host,
         ("max_abs_diff_vs_cpu" if wl.exact else "rel_l2_vs_cpu"): err,
         "device": info,
+        "gpu_clocks": clocks.report(),
     }
     if args.graph:
         result["launch_mode"] = f"HIP graph of {args.graph} steps per replay"
