@@ -1,0 +1,67 @@
+"""CPU checks of bench.py's contract that need no GPU: the one-GPU refusal,
+argument validation, the workload table and the sysfs clock parsing."""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BENCH = os.path.join(ROOT, "bench.py")
+
+
+def run_bench(*args):
+    return subprocess.run([sys.executable, BENCH, *args], capture_output=True, text=True, timeout=120)
+
+
+def test_more_than_one_gpu_is_refused_with_a_message():
+    r = run_bench("--gpus", "2")
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+@pytest.mark.parametrize("args", [["--steps", "0"], ["--warmup", "-1"], ["--graph", "3", "--steps", "10"]])
+def test_bad_arguments_are_refused(args):
+    r = run_bench(*args)
+    assert r.returncode == 2 and r.stdout == ""
+
+
+def test_workloads_cover_every_baseline_config():
+    import bench
+
+    for name in ("cfg1", "cfg2_256", "cfg2_4096", "cfg3", "cfg4", "cfg5"):
+        assert name in bench.FFT_WORKLOADS
+    dims, log_n, batch, seed, dist, steps, layout, _ = bench.FFT_WORKLOADS["cfg3"]
+    assert (dims, log_n, batch, seed, dist, layout) == (1, 10, 65536, 3, "normal", "interleaved")
+    assert bench.FFT_WORKLOADS["cfg4"][:5] == (1, 24, 4, 4, "normal")
+    assert bench.FFT_WORKLOADS["cfg5"][:5] == (2, 12, 2, 5, "uniform")
+    assert [d for d, _ in bench.FFT_WORKLOADS["cfg2_256"][5]] == ["forward", "inverse"]
+
+
+def test_clock_sampler_reads_the_marked_level(tmp_path):
+    import bench
+
+    (tmp_path / "pp_dpm_sclk").write_text("0: 500Mhz\n1: 1753Mhz *\n2: 2400Mhz\n")
+    (tmp_path / "pp_dpm_mclk").write_text("0: 2000Mhz *\n")
+    c = bench.ClockSampler(period_s=0.001)
+    c.dir = str(tmp_path)
+    with c:
+        import time
+
+        time.sleep(0.01)
+    rep = c.report()
+    assert rep["mclk_mhz"] == 2000
+    assert rep["sclk_samples"] >= 1 and rep["sclk_mhz_median"] == 1753 and rep["sclk_mhz_max"] == 1753
+
+
+def test_clock_sampler_without_sysfs_reports_nothing():
+    import bench
+
+    c = bench.ClockSampler()
+    c.dir = None
+    with c:
+        pass
+    assert c.report() is None
