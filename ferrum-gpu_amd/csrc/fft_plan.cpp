@@ -440,7 +440,6 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
     const bool inverse = dir == Direction::Inverse;
     const float scale = scale_for(dir, normalize);
     const void* big = big_.data();
-    hipStream_t st = stream ? stream : dev_->default_stream();
     const uint64_t unit = elems();
     size_t launch = 0;
     for (uint64_t u0 = 0; u0 < batch_; u0 += chunk_) {
@@ -466,7 +465,10 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
                 float sc = scale;
                 void* args[] = {&src, &dst, (void*)&tw, &count, &sc, &flags};
                 const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
-                HipBackend::launch(dev_->handle(), stream, s.fn, grid, s.block, 0, args);
+                if (events)
+                    HipBackend::launch_stamped(dev_->handle(), stream, s.fn, grid, s.block, 0, args, events[launch]);
+                else
+                    HipBackend::launch(dev_->handle(), stream, s.fn, grid, s.block, 0, args);
             } else {
                 TileGeom g = s.geom;
                 g.flags = flags;
@@ -474,10 +476,12 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
                 const uint64_t tiles = s.per_unit * units;
                 g.remap = (s.xcd_remap && tiles % 8 == 0) ? 1u : 0u;
                 void* args[] = {&src, &dst, (void*)&tw, (void*)&big, &g};
-                HipBackend::launch(dev_->handle(), stream, s.fn, Dim3((uint32_t)(s.per_unit * units)), s.block, 0,
-                                   args);
+                const Dim3 grid((uint32_t)(s.per_unit * units));
+                if (events)
+                    HipBackend::launch_stamped(dev_->handle(), stream, s.fn, grid, s.block, 0, args, events[launch]);
+                else
+                    HipBackend::launch(dev_->handle(), stream, s.fn, grid, s.block, 0, args);
             }
-            if (events) hip_check(hipEventRecord(events[launch], st), "hipEventRecord");
             ++launch;
         }
     }

@@ -5,6 +5,16 @@
 
 #include <string.h>
 
+// The launch extension of libamdhip64 that stamps start / stop events from
+// the kernel dispatch itself (declared in hip/hip_ext.h, whose C++ templates
+// need the HIP compiler; this file is plain g++).
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX, uint32_t globalWorkSizeY,
+                                               uint32_t globalWorkSizeZ, uint32_t localWorkSizeX,
+                                               uint32_t localWorkSizeY, uint32_t localWorkSizeZ,
+                                               size_t sharedMemBytes, hipStream_t hStream, void** kernelParams,
+                                               void** extra, hipEvent_t startEvent, hipEvent_t stopEvent,
+                                               uint32_t flags);
+
 namespace fg {
 
 void hip_check(hipError_t e, const char* what) {
@@ -147,6 +157,24 @@ void HipBackend::launch(const DeviceHandle& dev, Stream stream, KernelHandle k, 
     hip_check(hipModuleLaunchKernel(k, grid.x, grid.y, grid.z, block.x, block.y, block.z, shared_bytes,
                                     stream ? stream : dev->stream, args, nullptr),
               "hipModuleLaunchKernel");
+}
+
+void HipBackend::launch_stamped(const DeviceHandle& dev, Stream stream, KernelHandle k, Dim3 grid, Dim3 block,
+                                uint32_t shared_bytes, void** args, hipEvent_t stop) {
+    if (!k) invalid("launch of a null kernel");
+    if (grid.product() == 0 || block.product() == 0) invalid("launch with an empty grid or block");
+    if (block.product() > 1024) invalid("block of " + std::to_string(block.product()) + " threads exceeds 1024");
+    const uint64_t gx = (uint64_t)grid.x * block.x, gy = (uint64_t)grid.y * block.y, gz = (uint64_t)grid.z * block.z;
+    if (gx > 0xffffffffull || gy > 0xffffffffull || gz > 0xffffffffull) {
+        // Beyond the extension's 32-bit work sizes: a plain launch and a marker.
+        launch(dev, stream, k, grid, block, shared_bytes, args);
+        hip_check(hipEventRecord(stop, stream ? stream : dev->stream), "hipEventRecord");
+        return;
+    }
+    bind(dev);
+    hip_check(hipExtModuleLaunchKernel(k, (uint32_t)gx, (uint32_t)gy, (uint32_t)gz, block.x, block.y, block.z,
+                                       shared_bytes, stream ? stream : dev->stream, args, nullptr, nullptr, stop, 0),
+              "hipExtModuleLaunchKernel");
 }
 
 void HipBackend::sync_stream(const DeviceHandle& dev, Stream stream) {

@@ -77,6 +77,13 @@ struct HipBackend {
     static void launch(const DeviceHandle& dev, Stream stream, KernelHandle k, Dim3 grid, Dim3 block,
                        uint32_t shared_bytes, void** args);
 
+    // launch() whose completion stamps `stop` (as if it were recorded on the
+    // stream right after the kernel), from the dispatch itself rather than a
+    // separate marker packet between kernels: per-kernel timing that leaves
+    // back-to-back launches back to back.
+    static void launch_stamped(const DeviceHandle& dev, Stream stream, KernelHandle k, Dim3 grid, Dim3 block,
+                               uint32_t shared_bytes, void** args, hipEvent_t stop);
+
     // Backend::default_stream / sync_stream (backend.rs:73-76).
     static Stream default_stream(const DeviceHandle& dev) { return dev->stream; }
     static void sync_stream(const DeviceHandle& dev, Stream stream);

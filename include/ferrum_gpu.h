@@ -154,8 +154,9 @@ FG_API int fg_fft_exec(fg_fft_plan_t plan, const void *d_in, void *d_out, int di
  * i's duration is the time from the previous event on the stream (the
  * caller's start event, or events[i-1]) to events[i].  For per-kernel timing
  * in benchmarks: the reference's bench brackets its single launch with an
- * event pair (crates/ferrum-gpu-bench/src/lib.rs:163-198); recording one event
- * per launch keeps the marker overhead between back-to-back launches to one. */
+ * event pair (crates/ferrum-gpu-bench/src/lib.rs:163-198); here each event is
+ * stamped by its launch's dispatch (no marker packet between back-to-back
+ * launches), so the timed sequence runs as fg_fft_exec would. */
 FG_API int fg_fft_exec_events(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction,
                               int normalize, fg_stream_t stream, fg_event_t *events, int nevents);
 /* HIP graphs of plan executions.  No counterpart in the reference, whose host
