@@ -249,8 +249,19 @@ class FftWorkload:
         self.launch_keys = [f"{i % passes}:{k}" for _ in steps for i, k in enumerate(kernels)]
         self.bytes_per_launch = 16 * self.elems * units
 
-    def run(self, stream, events=None):
+    def bind_events(self, events):
+        """The per-step form run() takes of one step's launch events (built
+        before the timed loop: for interleaved plans, one EventList per
+        execute call)."""
+        from ferrum_gpu.hip import EventList
+
+        if self.layout == "split":
+            return list(events)
         L = len(self.kernels)
+        return [EventList(events[j * L:(j + 1) * L]) for j in range(len(self.steps))]
+
+    def run(self, stream, events=None):
+        """One step; ``events`` is None or what bind_events returned."""
         for j, (direction, normalize) in enumerate(self.steps):
             if self.layout == "split":
                 (ir, ii), (orr, oi) = self.parts[j], self.parts[j + 1]
@@ -260,8 +271,8 @@ class FftWorkload:
             elif events is None:
                 self.plan.execute(self.bufs[j], self.bufs[j + 1], direction, normalize, stream)
             else:
-                self.plan.execute_recording(self.bufs[j], self.bufs[j + 1], events[j * L:(j + 1) * L],
-                                            direction, normalize, stream)
+                self.plan.execute_recording(self.bufs[j], self.bufs[j + 1], events[j], direction, normalize,
+                                            stream)
 
     def output(self):
         np = self.np
@@ -391,6 +402,9 @@ class OpWorkload:
             ferrum_gpu.fft.transpose(d, i[0], o[0], self.side, self.side, 1, stream)
         if events is not None:
             events[0].record(stream)
+
+    def bind_events(self, events):
+        return list(events)
 
     def output(self):
         np = self.np
@@ -582,12 +596,13 @@ def main() -> int:
         # launch; a pair per launch measured ~6 us.
         start = Event(dev)
         evs = [[Event(dev) for _ in range(launches)] for _ in range(args.steps)]
+        bound = [wl.bind_events(e) for e in evs]
         dev.sync()
         with clocks:
             t0 = time.perf_counter()
             start.record(stream)
             for k in range(args.steps):
-                wl.run(stream, evs[k])
+                wl.run(stream, bound[k])
             dev.sync()
             wall = time.perf_counter() - t0
         log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms")

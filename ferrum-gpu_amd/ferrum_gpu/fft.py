@@ -17,7 +17,7 @@ import operator
 import numpy as np
 
 from ferrum_gpu import _native as _n
-from ferrum_gpu.hip import Device, DeviceBuffer, Graph
+from ferrum_gpu.hip import Device, DeviceBuffer, EventList, Graph
 
 __all__ = ["fft_1d_c2c_pow2", "fft_2d_c2c_pow2", "fft2_c2c_pow2", "Plan1D", "Plan2D", "Graph", "transpose",
            "set_chunk_bytes", "get_chunk_bytes", "MIN_LOG_N", "MAX_LOG_N", "MIN_LOG_N_2D", "MAX_LOG_N_2D"]
@@ -148,9 +148,13 @@ class _Plan:
                           stream: int = 0) -> None:
         """execute() that records events[i] right after launch i (len(events) ==
         launches), without synchronising; launch i ran between the previous event
-        recorded on the stream and events[i]."""
+        recorded on the stream and events[i].  ``events`` is a sequence of
+        Event or a prebuilt ``hip.EventList``."""
         d = _direction(direction)
-        arr = (ctypes.c_void_p * len(events))(*[e._e.value for e in events])
+        if isinstance(events, EventList):
+            arr = events.handles
+        else:
+            arr = (ctypes.c_void_p * len(events))(*[e._e.value for e in events])
         _n.check(_n.lib.fg_fft_exec_events(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),
                                            ctypes.c_void_p(stream or None), arr, len(events)))
 
