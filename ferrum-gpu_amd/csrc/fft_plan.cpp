@@ -114,7 +114,8 @@ std::vector<uint32_t> split_1d(uint32_t log_n) {
 }
 
 uint32_t tile_columns(uint32_t log_l) {
-    // Up to 1024 points: measured on gfx950 at 2^24 = 256^3, 32 columns of 256
+    // Passes that read HBM (a plan's first pass; every pass of an unchunked
+    // plan).  Up to 1024 points: measured on gfx950 at 2^24 = 256^3, 32 columns of 256
     // points (two 66 KB workgroups per CU) beat 64 (one 133 KB workgroup);
     // fewer than 16 columns (128-byte segments) loses HBM efficiency, so the
     // floor is 16.  2048 / 4096 points (2D columns only): 8 / 4 columns, the
@@ -125,6 +126,24 @@ uint32_t tile_columns(uint32_t log_l) {
     if (g > 64) g = 64;
     if (g < 16) g = 16;
     return g;
+}
+
+uint32_t cached_tile_columns(uint32_t log_l, bool rowwise) {
+    // Passes whose input is the previous pass's output, still cache-resident
+    // (chunked plans): the pieces of each 128-byte line meet in L2 / the
+    // Infinity Cache, so narrower tiles -- more resident workgroups per CU to
+    // overlap one tile's loads with another's arithmetic -- beat the wide
+    // ones HBM needs.  Measured on gfx950, us per 128 MiB chunk:
+    //  * column-wise, 8 columns in XCD-aware order from 128 points up: 256
+    //    points 47.3 -> 42.3 (32 columns), 512 rows 50.5 -> 47.8 and 1024
+    //    rows 58.2 -> 56.2 (16); at 64 points 8 columns lose (47.8 vs 40.2);
+    //  * row-wise (the 1D last pass, output streamed in G * 8-byte pieces):
+    //    16 rows at 128 / 256 points (128: 43.1 -> 39.4 from 64), 8 at 512
+    //    (48.4 -> 43.9 from 16), 16 at 1024 (8 lose: 60.6 vs 57.6); at 64
+    //    points 16 rows gain nothing over 64.
+    if (log_l < 7) return tile_columns(log_l);
+    if (rowwise) return log_l == 9 ? 8u : 16u;
+    return log_l > 10 ? 16384u >> log_l : 8u;
 }
 
 bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }
@@ -287,7 +306,9 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
     // four-step twiddle W_{S_{i-1}}^{r_i k_i}; in place in the workspace.
     for (size_t i = 1; i < P; ++i) {
         const uint32_t log_l = logs[i - 1];
-        const uint32_t g = tile_columns(log_l);
+        // Pass 1 reads the caller's input from HBM; later passes read the
+        // chunk's intermediate from the caches when the plan is chunked.
+        const uint32_t g = (i > 1 && p->cached_) ? cached_tile_columns(log_l, false) : tile_columns(log_l);
         if (S[i] < g) fail(FG_ERR_INTERNAL, "digit split leaves fewer columns than a tile");
         TileGeom t{};
         t.t0n = (uint32_t)(S[i] / g);
@@ -310,7 +331,7 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
     {
         const uint32_t log_l = logs[P - 1];
         const uint64_t L = 1ull << log_l, n1 = 1ull << logs[0];
-        const uint32_t g = tile_columns(log_l);
+        const uint32_t g = p->cached_ ? cached_tile_columns(log_l, true) : tile_columns(log_l);
         if (n1 < g) fail(FG_ERR_INTERNAL, "digit split leaves fewer rows than a tile");
         TileGeom t{};
         t.t0n = (uint32_t)(n1 / g);
@@ -349,7 +370,8 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     p->add_stockham(mod, log_cols, R, Buf::In, split ? Buf::Work : Buf::Out, p->policy(0, npass));
     if (!split) {
         // Column pass, in place: G adjacent columns of length R per tile.
-        const uint32_t g = (uint32_t)std::min<uint64_t>(tile_columns(log_rows), C);
+        const uint32_t g = (uint32_t)std::min<uint64_t>(
+            p->cached_ ? cached_tile_columns(log_rows, false) : tile_columns(log_rows), C);
         TileGeom t{};
         t.t0n = (uint32_t)(C / g);
         t.t1n = 1;

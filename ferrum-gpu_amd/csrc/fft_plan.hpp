@@ -155,8 +155,10 @@ std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e);
 std::vector<Cf32> big_twiddles();
 // Digit split (log2 sizes, slowest digit first) of a 1D length 2^log_n > 4096.
 std::vector<uint32_t> split_1d(uint32_t log_n);
-// Columns per tile for a pass of length 2^log_l.
+// Columns per tile for a pass of length 2^log_l that reads HBM.
 uint32_t tile_columns(uint32_t log_l);
+// Columns (row-wise: rows) per tile for a pass that reads cache-resident data.
+uint32_t cached_tile_columns(uint32_t log_l, bool rowwise);
 // Whether the column FFT of an image with 2^log_rows rows runs as two passes.
 bool split_2d_columns(uint32_t log_rows);
 // Largest chunk (bytes of one chunk's array) a multi-launch plan created from

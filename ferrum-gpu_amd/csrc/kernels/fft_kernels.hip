@@ -169,10 +169,14 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
     FG_TILE_P(LOGL, G, RW, TAG##_cs, true, false)  \
     FG_TILE_P(LOGL, G, RW, TAG##_sc, false, true)  \
     FG_TILE_P(LOGL, G, RW, TAG##_cc, true, true)
+// Narrow tiles (G < 16: 32- or 64-byte pieces of each line) only ever load
+// and store through the caches, in XCD-aware order: the _cc policy alone.
+#define FG_TILE_NARROW(LOGL, G, RW, TAG) FG_TILE_P(LOGL, G, RW, TAG##_cc, true, true)
 
-// Column passes: 1D digits of 128..1024 points (G = 64/32/16 by length), and
-// 2D column FFTs of 16..1024 points (or the 2048/4096 splits into 64 x 32 and
-// 64 x 64) over G = min(that width, image columns) adjacent columns.
+// Column passes reading HBM (the first 1D pass; every pass of an unchunked
+// plan): 1D digits of 64..1024 points (G = 64/32/16 by length), and 2D column
+// FFTs of 16..1024 points over G = min(that width, image columns) adjacent
+// columns.
 FG_TILE(4, 16, false, c)
 FG_TILE(4, 32, false, c)
 FG_TILE(4, 64, false, c)
@@ -189,16 +193,25 @@ FG_TILE(8, 16, false, c)
 FG_TILE(8, 32, false, c)
 FG_TILE(9, 16, false, c)
 FG_TILE(10, 16, false, c)
-// 2D column FFTs of 2048 / 4096 rows in one pass: 8 / 4 columns per tile
-// (1024 threads, 136 KB of LDS), XCD-aware tile order.
-FG_TILE(11, 8, false, c)
-FG_TILE(12, 4, false, c)
-// Row passes (last 1D digit: rows contiguous, transposed store).
+// Column passes over cache-resident data from 128 points up (1D middle
+// passes and 2D column FFTs of chunked plans): 8 columns per tile.  2048 /
+// 4096 rows (2D only, one pass): 8 / 4 columns (1024 threads, 136 KB of LDS).
+FG_TILE_NARROW(7, 8, false, c)
+FG_TILE_NARROW(8, 8, false, c)
+FG_TILE_NARROW(9, 8, false, c)
+FG_TILE_NARROW(10, 8, false, c)
+FG_TILE_NARROW(11, 8, false, c)
+FG_TILE_NARROW(12, 4, false, c)
+// Row passes (last 1D digit: rows contiguous, transposed store): the widths
+// for HBM-resident input, then those for cache-resident input.
 FG_TILE(6, 64, true, r)
 FG_TILE(7, 64, true, r)
 FG_TILE(8, 32, true, r)
 FG_TILE(9, 16, true, r)
 FG_TILE(10, 16, true, r)
+FG_TILE(7, 16, true, r)
+FG_TILE(8, 16, true, r)
+FG_TILE_NARROW(9, 8, true, r)
 
 // ------------------------------------------------------------- pointwise
 //

@@ -4,9 +4,10 @@ A multi-launch plan runs all of its passes over one chunk of whole
 transforms (images) before the next, keeping the chunk's intermediate array
 cached; the chunk limit is process-wide (ferrum_gpu.fft.set_chunk_bytes) and
 read when a plan is created.  Chunking changes only which transforms a launch
-covers and the cache hints of its accesses, never the arithmetic, so every
-chunking of a plan must give bit-identical output -- and the oracle's result
-within 1e-4.
+covers, the cache hints of its accesses and the tile widths of the passes
+that read the cached intermediate (how many columns a workgroup owns), never
+the arithmetic done on a column, so every chunking of a plan must give
+bit-identical output -- and the oracle's result within 1e-4.
 """
 
 from __future__ import annotations
@@ -16,6 +17,7 @@ import pytest
 
 import oracle
 from conftest import normal_c64, rel_l2, uniform_c64
+from test_multipass_model import plan_kernel_names
 
 pytestmark = pytest.mark.gpu
 
@@ -85,12 +87,10 @@ def test_every_chunking_gives_the_same_bits(gpu_device, chunk_limit, two_d, log_
             per = min(batch, limit // unit)
             assert d["cache_resident"] and d["units_per_chunk"] == per
             assert d["chunks"] == -(-batch // per)
-            # first pass streams in, last streams out (except a narrow 2D column
-            # pass, which stays cached), middle passes stay cached
-            narrow = two_d and log_n > 10
+            # first pass streams in, last streams out, middle passes stay
+            # cached; narrow tiles always cached (the model's names per pass)
             assert names[0].endswith("_sc")
-            assert names[d["passes"] - 1].endswith("_cc" if narrow else "_cs")
-            assert all(n.endswith("_cc") for n in names[1:d["passes"] - 1])
+            assert names[:d["passes"]] == plan_kernel_names(two_d, log_n, cached=True)
         assert d["launches"] == d["passes"] * d["chunks"] == len(names)
         outs[limit] = got
     for limit, got in outs.items():
@@ -150,3 +150,23 @@ def test_chunk_limit_applies_to_new_plans_only(gpu_device, chunk_limit):
     assert c.describe()["chunks"] == 1 and c.describe()["passes"] == 1
     for p in (a, b, c):
         p.destroy()
+
+
+@pytest.mark.parametrize("chunked", [True, False], ids=["chunked", "unchunked"])
+def test_plan_kernels_follow_the_tile_width_tables(gpu_device, chunk_limit, chunked):
+    # Passes that read HBM use the wide tiles, passes over a chunk's cached
+    # intermediate the cache-resident widths: the host's choice for every
+    # multi-launch plan equals the CPU model's (test_multipass_model), which
+    # is the geometry the CPU tests prove against the oracle.
+    import ferrum_gpu
+
+    chunk_limit(128 * MIB if chunked else 0)
+    for log_n in range(13, 25):
+        plan = ferrum_gpu.fft.Plan1D(log_n, 1, gpu_device)
+        assert plan.kernel_names() == plan_kernel_names(False, log_n, chunked), log_n
+        plan.destroy()
+    for lr in range(4, 13):
+        for lc in (4, 7, lr, 12):
+            plan = ferrum_gpu.fft.Plan2D(lr, 1, gpu_device, log_cols=lc)
+            assert plan.kernel_names() == plan_kernel_names(True, lr, chunked, lc), (lr, lc)
+            plan.destroy()

@@ -25,11 +25,21 @@ from conftest import rel_l2, uniform_c64
 
 
 def tile_columns(log_l):
-    """Columns per tile (tile_columns in fft_plan.cpp): 16..64 up to 1024 points,
-    8 / 4 (narrow tiles) for 2048 / 4096."""
+    """Columns per tile of a pass that reads HBM (tile_columns in fft_plan.cpp):
+    16..64 up to 1024 points, 8 / 4 (narrow tiles) for 2048 / 4096."""
     if log_l > 10:
         return 16384 >> log_l
     return max(16, min(64, 8192 >> log_l))
+
+
+def cached_tile_columns(log_l, rowwise):
+    """Columns (row-wise: rows) per tile of a pass that reads cache-resident data
+    (cached_tile_columns in fft_plan.cpp)."""
+    if log_l < 7:
+        return tile_columns(log_l)
+    if rowwise:
+        return 8 if log_l == 9 else 16
+    return 16384 >> log_l if log_l > 10 else 8
 
 
 def split_1d(log_n):
@@ -42,8 +52,9 @@ def split_1d(log_n):
     return [base + (1 if rest > 0 else 0), base + (1 if rest > 1 else 0), base]
 
 
-def tile_geometry_1d(log_n, batch):
-    """Per-pass geometry dicts (TileGeom), built as FftPlan::make_1d builds them."""
+def tile_geometry_1d(log_n, batch, cached=True):
+    """Per-pass geometry dicts (TileGeom), built as FftPlan::make_1d builds them;
+    ``cached``: the plan is chunked, so passes after the first read the caches."""
     logs = split_1d(log_n)
     P = len(logs)
     N = 1 << log_n
@@ -55,7 +66,7 @@ def tile_geometry_1d(log_n, batch):
     for i in range(1, P):
         L = sizes[i - 1]
         cols = S[i]                   # r_i ranges over [0, S_i): the faster digits
-        g = tile_columns(logs[i - 1])
+        g = cached_tile_columns(logs[i - 1], False) if (cached and i > 1) else tile_columns(logs[i - 1])
         assert cols >= g
         t0n = cols // g               # column groups
         t1n = N // (S[i - 1])         # values of the slower transformed digits k_1..k_{i-1}
@@ -67,7 +78,7 @@ def tile_geometry_1d(log_n, batch):
     # last pass: rows of length N_P, grouped by G' consecutive values of k_1
     L = sizes[-1]
     n1 = sizes[0]
-    gp = tile_columns(logs[-1])
+    gp = cached_tile_columns(logs[-1], True) if cached else tile_columns(logs[-1])
     assert n1 >= gp
     inner = N // (n1 * L)             # values of k_2..k_{P-1}
     # the row for (k_1, kmid) starts at k_1*S_1 + sum k_j S_j = k_1*S_1 + kmid*L
@@ -79,17 +90,44 @@ def tile_geometry_1d(log_n, batch):
     return passes
 
 
-def tile_geometry_2d(log_n, batch, log_cols=None):
+def tile_geometry_2d(log_n, batch, log_cols=None, cached=True):
     """Column FFT of each R x C image after the row pass, as FftPlan::make_2d builds it
     (R = 2^log_n rows, C = 2^log_cols columns, square by default): one tile pass over
-    min(tile_columns(R), C) adjacent columns of length R, in place."""
+    min(width, C) adjacent columns of length R, in place; the width is the
+    cache-resident one when the plan is chunked."""
     R = 1 << log_n
     C = R if log_cols is None else 1 << log_cols
-    g = min(tile_columns(log_n), C)
+    g = min(cached_tile_columns(log_n, False) if cached else tile_columns(log_n), C)
     return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
                  is0=g, is1=0, is2=R * C, ics=1, ies=C,
                  os0=g, os1=0, os2=R * C, ocs=1, oes=C,
                  twc=0, tw0=0, tw1=0, log_m=0)]
+
+
+def pass_policy(i, n, cached, g):
+    """Cache-policy suffix of pass i of n (FftPlan::policy / add_tile): narrow
+    tiles always _cc; unchunked plans stream; chunked: _sc, _cc..., _cs."""
+    if g < 16:
+        return "_cc"
+    if not cached:
+        return ""
+    return "_sc" if i == 0 else ("_cs" if i == n - 1 else "_cc")
+
+
+def plan_kernel_names(two_d, log_n, cached=True, log_cols=None):
+    """The kernel of every pass of a multi-launch plan (1D N > 4096, or 2D with
+    2^log_n rows and 2^log_cols columns), in launch order."""
+    def tile(p, pol):
+        return f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}{pol}"
+
+    if not two_d:
+        passes = tile_geometry_1d(log_n, 1, cached)
+        return [tile(p, pass_policy(i, len(passes), cached, p["g"])) for i, p in enumerate(passes)]
+    lc = log_n if log_cols is None else log_cols
+    passes = tile_geometry_2d(log_n, 1, lc, cached)
+    n = len(passes) + 1
+    return [f"fg_fft_n{lc}" + ("_sc" if cached else "")] + \
+        [tile(p, pass_policy(i + 1, n, cached, p["g"])) for i, p in enumerate(passes)]
 
 
 def xcd_remap(b, grid):
@@ -141,19 +179,21 @@ def run_geometry(buf_in, passes, batch, elems):
     return src
 
 
+@pytest.mark.parametrize("cached", [True, False], ids=["chunked", "unchunked"])
 @pytest.mark.parametrize("log_n", [13, 14, 15, 16, 17, 18, 20])
-def test_1d_multipass_matches_oracle(log_n):
+def test_1d_multipass_matches_oracle(log_n, cached):
     rng = np.random.default_rng(log_n)
     batch = 2
     x = uniform_c64(rng, batch << log_n)
-    got = run_geometry(x, tile_geometry_1d(log_n, batch), batch, 1 << log_n)
+    got = run_geometry(x, tile_geometry_1d(log_n, batch, cached), batch, 1 << log_n)
     assert rel_l2(got, oracle.fft_1d(x, log_n)) < 1e-5
 
 
-def test_1d_three_pass_small():
+@pytest.mark.parametrize("cached", [True, False], ids=["chunked", "unchunked"])
+def test_1d_three_pass_small(cached):
     # exercise the 3-pass geometry at a size numpy loops finish quickly
     log_n = 21
-    passes = tile_geometry_1d(log_n, 1)
+    passes = tile_geometry_1d(log_n, 1, cached)
     assert len(passes) == 3
     rng = np.random.default_rng(0)
     x = uniform_c64(rng, 1 << log_n)
@@ -161,14 +201,15 @@ def test_1d_three_pass_small():
     assert rel_l2(got, np.fft.fft(x.astype(np.complex128))) < 1e-5
 
 
-@pytest.mark.parametrize("log_n", [4, 5, 6, 8, 10, 11, 12])
-def test_2d_column_passes_match_oracle(log_n):
+@pytest.mark.parametrize("cached", [True, False], ids=["chunked", "unchunked"])
+@pytest.mark.parametrize("log_n", [4, 5, 6, 7, 8, 10, 11, 12])
+def test_2d_column_passes_match_oracle(log_n, cached):
     rng = np.random.default_rng(log_n + 100)
     n = 1 << log_n
     batch = 2 if log_n <= 10 else 1
     x = uniform_c64(rng, batch * n * n).reshape(batch, n, n)
     rows = np.fft.fft(x.astype(np.complex128), axis=2).reshape(-1)
-    got = run_geometry(rows, tile_geometry_2d(log_n, batch), batch, n * n).reshape(batch, n, n)
+    got = run_geometry(rows, tile_geometry_2d(log_n, batch, cached=cached), batch, n * n).reshape(batch, n, n)
     assert rel_l2(got, oracle.fft_2d(x, log_n)) < 1e-5
 
 
@@ -192,7 +233,8 @@ def test_xcd_remap_is_a_permutation_grouping_neighbours(grid):
         assert (b & 7) * per <= tiles[b] < ((b & 7) + 1) * per
 
 
-@pytest.mark.parametrize("log_l,g", [(12, 4), (11, 8), (10, 16), (8, 32), (6, 64)])
+@pytest.mark.parametrize("log_l,g", [(12, 4), (11, 8), (10, 16), (10, 8), (9, 8), (8, 32), (8, 16), (8, 8),
+                                     (7, 8), (6, 64), (6, 16)])
 def test_tile_lds_layout_is_injective_and_fits(log_l, g):
     n = 1 << log_l
     pos, c = np.meshgrid(np.arange(n), np.arange(g), indexing="ij")

@@ -73,39 +73,26 @@ def instantiated_kernels():
     names |= {f"fg_fft_n{m.group(1)}_sc" for m in re.finditer(r"^FG_STOCKHAM_SC\((\d+),", src, flags=re.M)}
     for m in re.finditer(r"^FG_STOCKHAM_LAT\((\d+),", src, flags=re.M):
         names |= {f"fg_fft_n{m.group(1)}_lat", f"fg_fft_n{m.group(1)}_lat_split"}
-    for m in re.finditer(r"^FG_TILE\((\d+), (\d+), (true|false), ([cr])\)", src, flags=re.M):
-        base = f"fg_tile_l{m.group(1)}_g{m.group(2)}_{m.group(4)}"
-        names |= {base + pol for pol in ("", "_sc", "_cc", "_cs")}  # cache policies (FG_TILE_P)
+    for m in re.finditer(r"^FG_TILE(_NARROW)?\((\d+), (\d+), (true|false), ([cr])\)", src, flags=re.M):
+        base = f"fg_tile_l{m.group(2)}_g{m.group(3)}_{m.group(5)}"
+        # cache policies (FG_TILE_P): all four, or _cc alone for narrow tiles
+        names |= {base + "_cc"} if m.group(1) else {base + pol for pol in ("", "_sc", "_cc", "_cs")}
     return names
 
 
 def planned_kernels():
     """Every kernel name FftPlan can request (mirrors fft_plan.cpp via the CPU models)."""
-    from test_multipass_model import tile_geometry_1d, tile_geometry_2d
-
-    def policies(i, n):
-        # unchunked: every pass streams; chunked: first _sc, middle _cc, last _cs
-        return ("", "_sc" if i == 0 else ("_cs" if i == n - 1 else "_cc"))
-
+    from test_multipass_model import plan_kernel_names
     from test_stockham_model import LATENCY_GEOM
 
     names = {f"fg_fft_n{l}" for l in range(2, 13)} | {f"fg_fft_n{l}_split" for l in range(2, 13)}
     names |= {f"fg_fft_n{l}_lat{sfx}" for l in LATENCY_GEOM for sfx in ("", "_split")}
-    for log_n in range(13, 25):
-        passes = tile_geometry_1d(log_n, 1)
-        for i, p in enumerate(passes):
-            # narrow tiles (g < 16) always load and store cached
-            for pol in (("_cc",) if p["g"] < 16 else policies(i, len(passes))):
-                names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}{pol}")
-    for lr in range(4, 13):
-        for lc in range(4, 13):
-            passes = tile_geometry_2d(lr, 1, lc)   # column passes; the row pass comes first
-            names |= {f"fg_fft_n{lc}", f"fg_fft_n{lc}_sc"}
-            for i, p in enumerate(passes):
-                # narrow tiles (g < 16) always load and store cached
-                pols = ("_cc",) if p["g"] < 16 else policies(i + 1, len(passes) + 1)
-                for pol in pols:
-                    names.add(f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}{pol}")
+    for cached in (False, True):
+        for log_n in range(13, 25):
+            names |= set(plan_kernel_names(False, log_n, cached))
+        for lr in range(4, 13):
+            for lc in range(4, 13):
+                names |= set(plan_kernel_names(True, lr, cached, lc))
     return names
 
 
