@@ -37,11 +37,14 @@ def _as_u32(log_n) -> int:
     return v
 
 
+_DIRECTIONS = {"forward": _n.FG_FORWARD, "inverse": _n.FG_INVERSE}
+
+
 def _direction(direction) -> int:
-    if direction == "forward":
-        return _n.FG_FORWARD
-    if direction == "inverse":
-        return _n.FG_INVERSE
+    try:
+        return _DIRECTIONS[direction]
+    except (KeyError, TypeError):
+        pass
     # Rust formats the offending string with {:?} (double-quoted), lib.rs:472-476.
     raise ValueError(f"direction must be 'forward' or 'inverse', got \"{direction}\"")
 
@@ -117,13 +120,21 @@ def fft_2d_c2c_pow2(arr, log_n, direction="forward", normalize=False, device=Non
     return out
 
 
-def _ptr(x) -> ctypes.c_void_p:
-    """A device address from a DeviceBuffer, a GPU torch tensor or an int."""
+def _ptr(x):
+    """A device address for a void* parameter from a DeviceBuffer (its own
+    c_void_p, which ctypes passes without converting), a GPU torch tensor or
+    an int."""
     if isinstance(x, DeviceBuffer):
-        return ctypes.c_void_p(x.ptr)
+        return x._p
     if hasattr(x, "data_ptr"):  # a torch tensor on the GPU
-        return ctypes.c_void_p(x.data_ptr())
-    return ctypes.c_void_p(int(x))
+        return x.data_ptr()
+    return int(x)
+
+
+# Bound once: the per-call cost of the device-resident entry points is host
+# time that launch-bound callers (small batches) pay on every call.
+_fft_exec = _n.lib.fg_fft_exec
+_fft_exec_events = _n.lib.fg_fft_exec_events
 
 
 class _Plan:
@@ -140,9 +151,10 @@ class _Plan:
 
     def execute(self, d_in, d_out, direction="forward", normalize=False, stream: int = 0) -> None:
         """Stream-ordered, asynchronous execution on device buffers (may alias)."""
-        d = _direction(direction)
-        _n.check(_n.lib.fg_fft_exec(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),
-                                    ctypes.c_void_p(stream or None)))
+        rc = _fft_exec(self._p, _ptr(d_in), _ptr(d_out), _direction(direction), 1 if normalize else 0,
+                       stream or None)
+        if rc:
+            _n.check(rc)
 
     def execute_recording(self, d_in, d_out, events, direction="forward", normalize=False,
                           stream: int = 0) -> None:
@@ -150,13 +162,14 @@ class _Plan:
         launches), without synchronising; launch i ran between the previous event
         recorded on the stream and events[i].  ``events`` is a sequence of
         Event or a prebuilt ``hip.EventList``."""
-        d = _direction(direction)
         if isinstance(events, EventList):
             arr = events.handles
         else:
             arr = (ctypes.c_void_p * len(events))(*[e._e.value for e in events])
-        _n.check(_n.lib.fg_fft_exec_events(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),
-                                           ctypes.c_void_p(stream or None), arr, len(events)))
+        rc = _fft_exec_events(self._p, _ptr(d_in), _ptr(d_out), _direction(direction), 1 if normalize else 0,
+                              stream or None, arr, len(arr))
+        if rc:
+            _n.check(rc)
 
     def execute_split(self, in_re, in_im, out_re, out_im, direction="forward", normalize=False,
                       stream: int = 0) -> None:
