@@ -124,6 +124,32 @@ struct TileStages {
     }
 };
 
+// This workgroup's tile: its (t0, t1) indices and input / output bases.
+struct TileCoords {
+    uint32_t t0, t1;
+    uint64_t ib, ob;
+};
+
+__device__ __forceinline__ TileCoords tile_coords(const TileGeom& g) {
+    uint32_t b = blockIdx.x;
+    if (g.remap) {
+        // XCD-aware order: workgroups are dealt round-robin over the 8 XCDs,
+        // so XCD x (blockIdx % 8) takes the contiguous tile range
+        // [x * grid/8, (x + 1) * grid/8).  Narrow tiles (4 or 8 columns, 32 or
+        // 64 bytes of a 128-byte line) then share each line fill of their
+        // XCD's L2 instead of each XCD fetching it (host: grid % 8 == 0).
+        b = (b & 7u) * (gridDim.x >> 3) + (b >> 3);
+    }
+    TileCoords tc;
+    tc.t0 = b % g.t0n;
+    b /= g.t0n;
+    tc.t1 = b % g.t1n;
+    const uint32_t t2 = b / g.t1n;
+    tc.ib = tc.t0 * g.is0 + tc.t1 * g.is1 + (uint64_t)t2 * g.is2;
+    tc.ob = tc.t0 * g.os0 + tc.t1 * g.os1 + (uint64_t)t2 * g.os2;
+    return tc;
+}
+
 // ROWWISE: input elements of a column are contiguous (ies == 1, rows of a
 // matrix), so loads run along elements and the tile is transposed into LDS
 // first; otherwise columns are contiguous (ics == 1) and each thread loads its
@@ -146,23 +172,10 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
     const int tid = threadIdx.x;
     const int c = tid % G;
     const int q = tid / G;
-    uint32_t b = blockIdx.x;
-    if (g.remap) {
-        // XCD-aware order: workgroups are dealt round-robin over the 8 XCDs,
-        // so XCD x (blockIdx % 8) takes the contiguous tile range
-        // [x * grid/8, (x + 1) * grid/8).  Narrow tiles (4 or 8 columns, 32 or
-        // 64 bytes of a 128-byte line) then share each line fill of their
-        // XCD's L2 instead of each XCD fetching it (host: grid % 8 == 0).
-        b = (b & 7u) * (gridDim.x >> 3) + (b >> 3);
-    }
-    const uint32_t t0 = b % g.t0n;
-    b /= g.t0n;
-    const uint32_t t1 = b % g.t1n;
-    const uint32_t t2 = b / g.t1n;
-    const uint64_t ib = t0 * g.is0 + t1 * g.is1 + (uint64_t)t2 * g.is2;
-    const uint64_t ob = t0 * g.os0 + t1 * g.os1 + (uint64_t)t2 * g.os2;
-    const char* in_tile = reinterpret_cast<const char*>(in + ib);
-    char* out_tile = reinterpret_cast<char*>(out + ob);
+    const TileCoords tc = tile_coords(g);
+    const uint32_t t0 = tc.t0, t1 = tc.t1;
+    const char* in_tile = reinterpret_cast<const char*>(in + tc.ib);
+    char* out_tile = reinterpret_cast<char*>(out + tc.ob);
 
     float2 x[Sh::E];
     if constexpr (ROWWISE) {

@@ -48,7 +48,9 @@ def test_1d_multipass_forward(gpu_device, log_n):
     assert rel_l2(got, oracle.fft_1d(x, log_n, threads=8)) <= TOL
 
 
-@pytest.mark.parametrize("log_n", [13, 16, 17, 20, 21, 24])
+# every last-pass / middle-pass tile shape of the chunked plans (64..1024-point
+# row passes, 8-column middle passes) runs the inverse's conjugations once
+@pytest.mark.parametrize("log_n", [13, 14, 16, 17, 18, 19, 20, 21, 22, 23, 24])
 @pytest.mark.parametrize("normalize", [False, True])
 def test_1d_multipass_inverse(gpu_device, log_n, normalize):
     rng = np.random.default_rng(400 + log_n)

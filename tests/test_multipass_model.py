@@ -247,7 +247,7 @@ def test_tile_lds_layout_is_injective_and_fits(log_l, g):
 def test_long_column_widths():
     # 2048 / 4096-point digits: 8 / 4 columns per tile, 1024 threads of 16 elements
     for log_n, g in ((11, 8), (12, 4)):
-        assert tile_columns(log_n) == g
+        assert tile_columns(log_n) == g == cached_tile_columns(log_n, False)
         assert g * (1 << log_n) // 16 == 1024
 
 
