@@ -4,6 +4,7 @@
 // thread-local message, the C-ABI shape of the reference's Result<_, Error> ->
 // PyValueError mapping (crates/ferrum-gpu-py/src/lib.rs:404-406, 497, 577).
 #include <hip/hip_runtime_api.h>
+#include <stdint.h>
 #include <string.h>
 
 #include <atomic>
@@ -176,6 +177,15 @@ void run_host(fg_device* d, int dims, uint32_t log_n, uint32_t log_rows, size_t 
     plan.exec(d->staging.data(), d->staging.data(), dir, normalize, nullptr);
     HipBackend::copy_async(h, out, d->staging.data(), total * sizeof(Cf32), hipMemcpyDeviceToHost, nullptr);
     d->dev->sync();
+}
+
+// Elements of `batch` images of 2^log_elems points, refusing a product that
+// does not fit in size_t (it would size the staging buffer below the plan).
+size_t host_2d_elems(uint32_t log_elems, size_t batch) {
+    if (batch > (SIZE_MAX >> log_elems) / sizeof(Cf32))
+        fg::invalid("batch " + std::to_string(batch) + " too large for images of 2^" + std::to_string(log_elems) +
+                    " points");
+    return (size_t(1) << log_elems) * batch;
 }
 
 }  // namespace
@@ -655,11 +665,11 @@ int fg_fft_2d_c2c_pow2_host(fg_device_t dev, const float* in, float* out, uint32
             fg::invalid("2D requires log_n in [" + std::to_string(fg::kMinLogN2D) + ", " +
                         std::to_string(fg::kMaxLogN2D) + "]; got " + std::to_string(log_n));
         if (batch == 0) fg::invalid("batch must be positive");
+        const size_t total = host_2d_elems(2 * log_n, batch);
         Direction dir = parse_dir(direction);
         need(in, "in");
         need(out, "out");
         fg_device* d = dev ? dev : default_device();
-        const size_t total = (size_t(1) << (2 * log_n)) * batch;
         run_host(d, 2, log_n, log_n, batch, total, in, out, dir, normalize != 0);
     });
 }
@@ -672,11 +682,11 @@ int fg_fft_2d_rect_host(fg_device_t dev, const float* in, float* out, uint32_t l
                 fg::invalid("2D requires log_n in [" + std::to_string(fg::kMinLogN2D) + ", " +
                             std::to_string(fg::kMaxLogN2D) + "]; got " + std::to_string(l));
         if (batch == 0) fg::invalid("batch must be positive");
+        const size_t total = host_2d_elems(log_rows + log_cols, batch);
         Direction dir = parse_dir(direction);
         need(in, "in");
         need(out, "out");
         fg_device* d = dev ? dev : default_device();
-        const size_t total = (size_t(1) << (log_rows + log_cols)) * batch;
         run_host(d, 2, log_cols, log_rows, batch, total, in, out, dir, normalize != 0);
     });
 }
@@ -751,6 +761,8 @@ int fg_stream_copy(fg_device_t dev, const void* d_in, void* d_out, size_t bytes,
         need(d_in, "d_in");
         need(d_out, "d_out");
         if (bytes % 16) fg::invalid("fg_stream_copy: bytes must be a multiple of 16");
+        if ((reinterpret_cast<uintptr_t>(d_in) | reinterpret_cast<uintptr_t>(d_out)) & 15)
+            fg::invalid("fg_stream_copy: d_in and d_out must be 16-byte aligned");
         static thread_local HipBackend::KernelHandle k = nullptr;
         static thread_local const void* k_mod = nullptr;
         if (!k || k_mod != dev->fft_module.get()) {

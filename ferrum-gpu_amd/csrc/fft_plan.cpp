@@ -459,6 +459,15 @@ float FftPlan::scale_for(Direction dir, bool normalize) const {
 void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
                    hipEvent_t* events) const {
     if (!in || !out) invalid("fft exec: null buffer");
+    if ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 7u)
+        invalid("fft exec: buffers must be 8-byte aligned (complex64)");
+    {
+        // In place or disjoint: a partial overlap would let one workgroup's
+        // stores reach elements another has not read yet.
+        const uintptr_t x = reinterpret_cast<uintptr_t>(in), y = reinterpret_cast<uintptr_t>(out);
+        const uint64_t nb = 8ull * elems() * batch_;
+        if (x != y && x < y + nb && y < x + nb) invalid("fft exec: d_in and d_out overlap without being equal");
+    }
     const bool inverse = dir == Direction::Inverse;
     const float scale = scale_for(dir, normalize);
     const void* big = big_.data();

@@ -150,7 +150,8 @@ class _Plan:
         return self.batch * self.elems * 8
 
     def execute(self, d_in, d_out, direction="forward", normalize=False, stream: int = 0) -> None:
-        """Stream-ordered, asynchronous execution on device buffers (may alias)."""
+        """Stream-ordered, asynchronous execution on device buffers: equal (in
+        place) or disjoint, 8-byte aligned."""
         rc = _fft_exec(self._p, _ptr(d_in), _ptr(d_out), _direction(direction), 1 if normalize else 0,
                        stream or None)
         if rc:

@@ -145,7 +145,8 @@ FG_API int fg_fft_plan_destroy(fg_fft_plan_t plan);
 /* Device-resident execution, stream-ordered and asynchronous: the kernel
  * launch of the host runner (py lib.rs:142-233, 325-358) with the inverse's
  * conjugation and 1/N (1/(N*N) for 2D) scaling done inside the kernels.
- * d_in and d_out each hold batch*N (2D: batch*N*N) complex64 and may be equal.
+ * d_in and d_out each hold batch*N (2D: batch*N*N) complex64, 8-byte aligned;
+ * they may be equal (in place) but must not otherwise overlap.
  * direction: FG_FORWARD or FG_INVERSE.  stream NULL = device default stream. */
 FG_API int fg_fft_exec(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction, int normalize,
                 fg_stream_t stream);
@@ -288,8 +289,9 @@ FG_API int fg_fill_uniform_c64(fg_device_t dev, void *d_out, size_t n, uint64_t 
 FG_API int fg_fill_normal_c64(fg_device_t dev, void *d_out, size_t n, uint64_t seed,
                               fg_stream_t stream);
 
-/* Streaming device copy of `bytes` (a multiple of 16) with the code object's
- * copy kernel: the HBM yardstick reported beside the FFT. */
+/* Streaming device copy of `bytes` (a multiple of 16; both pointers 16-byte
+ * aligned) with the code object's copy kernel: the HBM yardstick reported
+ * beside the FFT. */
 FG_API int fg_stream_copy(fg_device_t dev, const void *d_in, void *d_out, size_t bytes,
                    fg_stream_t stream);
 

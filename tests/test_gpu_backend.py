@@ -85,6 +85,13 @@ def test_events_and_stream_copy(gpu_device):
     out = np.empty_like(src)
     b.copy_to_host(out)
     assert np.array_equal(out, src)
+    # the copy kernel moves 16-byte vectors: misaligned pointers and odd sizes
+    # are refused on the host, nothing is launched
+    for p_in, p_out, n in ((a.ptr + 8, b.ptr, 1 << 20), (a.ptr, b.ptr + 4, 1 << 20), (a.ptr, b.ptr, 24)):
+        rc = N.lib.fg_stream_copy(gpu_device.handle, ctypes.c_void_p(p_in), ctypes.c_void_p(p_out), n,
+                                  ctypes.c_void_p(s))
+        assert rc == N.FG_ERR_INVALID_ARGUMENT, (p_in - a.ptr, p_out - b.ptr, n)
+        assert "16" in N.last_error()
 
 
 def test_device_close_waits_for_its_plans_and_graphs(gpu_device):

@@ -175,6 +175,29 @@ def test_in_place_and_deterministic(gpu_device):
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("log_n", [10, 16])
+def test_exec_refuses_partial_overlap_and_misalignment(gpu_device, log_n):
+    # checked on the host before any launch: in and out equal or disjoint,
+    # both 8-byte aligned (a single-pass and a multi-pass plan)
+    import ferrum_gpu
+    from ferrum_gpu import _native as N
+    from ferrum_gpu.hip import DeviceBuffer
+
+    plan = ferrum_gpu.fft.Plan1D(log_n, 4, gpu_device)
+    buf = DeviceBuffer(gpu_device, 2 * plan.nbytes)
+    for d_in, d_out, what in ((buf.ptr, buf.ptr + 8 * (1 << log_n), "overlap"),
+                              (buf.ptr + plan.nbytes - 8, buf.ptr, "overlap"),
+                              (buf.ptr + 4, buf.ptr + plan.nbytes + 8, "aligned"),
+                              (buf.ptr, buf.ptr + plan.nbytes + 4, "aligned")):
+        with pytest.raises(N.FerrumGpuError, match=what):
+            plan.execute(d_in, d_out)
+    # disjoint neighbours and in place are fine
+    plan.execute(buf.ptr, buf.ptr + plan.nbytes)
+    plan.execute(buf.ptr, buf.ptr)
+    gpu_device.sync()
+    plan.destroy()
+
+
 def test_persistent_device_and_one_shot_agree(gpu_device):
     rng = np.random.default_rng(10)
     x = uniform_c64(rng, 3 * 4096)

@@ -177,6 +177,11 @@ def test_c_abi_validation_without_device():
     assert rc == N.FG_ERR_INVALID_ARGUMENT and "direction" in N.last_error()
     rc = N.lib.fg_fft_2d_c2c_pow2_host(None, x.ctypes.data, y.ctypes.data, 2, 1, 1, 0)
     assert rc == N.FG_ERR_INVALID_ARGUMENT and "2D requires log_n in [4, 12]; got 2" in N.last_error()
+    # a batch whose element count overflows size_t is refused before any device work
+    rc = N.lib.fg_fft_2d_c2c_pow2_host(None, x.ctypes.data, y.ctypes.data, 12, 1 << 40, 1, 0)
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "too large for images of 2^24 points" in N.last_error()
+    rc = N.lib.fg_fft_2d_rect_host(None, x.ctypes.data, y.ctypes.data, 12, 11, 1 << 41, 1, 0)
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "too large for images of 2^23 points" in N.last_error()
     rc = N.lib.fg_fft_exec(None, None, None, 1, 0, None)
     assert rc == N.FG_ERR_INVALID_ARGUMENT and "plan is null" in N.last_error()
     rc = N.lib.fg_fft_plan_1d(None, 10, 1, ctypes.byref(ctypes.c_void_p()))
