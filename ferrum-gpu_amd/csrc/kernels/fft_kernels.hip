@@ -148,10 +148,11 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
 
 // ------------------------------------------------------- multi-pass tiles
 //
-// fg_tile_l<LOGL>_g<G>_<c|r>[_<policy>]: one pass over G columns of length
-// 2^LOGL per workgroup (G * 2^LOGL / 16 threads).  'c': columns contiguous in
-// memory (column passes); 'r': rows contiguous (the last 1D pass, which
-// transposes through LDS).  Policy (fft_common.hpp, gload/gstore): none =
+// fg_tile_l<LOGL>_g<G>_<c|r|h>[_<policy>]: one pass over G columns of length
+// 2^LOGL per workgroup (G * 2^LOGL / 16 threads; 'h': / 32).  'c': columns
+// contiguous in memory (column passes); 'r': rows contiguous (the last 1D
+// pass, which transposes through LDS); 'h': a column pass with 32 elements
+// per thread and the exchanges in halves (the first 1D pass).  Policy (fft_common.hpp, gload/gstore): none =
 // stream in and out; _sc = stream in, cached out (a chunk's first pass); _cc
 // (middle passes); _cs = cached in, stream out (last pass).  The host picks
 // the names in fft_plan.cpp (tile_name).
@@ -202,6 +203,25 @@ FG_TILE_NARROW(9, 8, false, c)
 FG_TILE_NARROW(10, 8, false, c)
 FG_TILE_NARROW(11, 8, false, c)
 FG_TILE_NARROW(12, 4, false, c)
+// First pass of a 1D multi-pass plan (input from HBM): the same column DFTs
+// and four-step twiddle with 32 elements per thread and the exchanges in
+// halves (fft_tile_halves_body): half the LDS of the tiles above, so twice
+// the workgroups per CU; at most 128 VGPRs (four waves per SIMD).  Policies:
+// none (unchunked) and _sc (a chunk's first pass).
+#define FG_TILE_HALVES_P(LOGL, G, TAG, LC, SC)                                                             \
+    extern "C" __global__ __launch_bounds__(G * HalvesShape<LOGL>::T) __attribute__((amdgpu_waves_per_eu(4))) \
+    void fg_tile_l##LOGL##_g##G##_h##TAG(const float2* __restrict__ in, float2* __restrict__ out,              \
+                                         const float2* __restrict__ tw, const float2* __restrict__ big,       \
+                                         TileGeom g) {                                                        \
+        fft_tile_halves_pass<LOGL, G, LC, SC>(in, out, tw, big, g);                                           \
+    }
+#define FG_TILE_HALVES(LOGL, G)                  \
+    FG_TILE_HALVES_P(LOGL, G, , false, false)    \
+    FG_TILE_HALVES_P(LOGL, G, _sc, false, true)
+FG_TILE_HALVES(7, 64)
+FG_TILE_HALVES(8, 32)
+FG_TILE_HALVES(9, 16)
+FG_TILE_HALVES(10, 16)
 // Row passes (last 1D digit: rows contiguous, transposed store): the widths
 // for HBM-resident input, then those for cache-resident input.
 FG_TILE(6, 64, true, r)

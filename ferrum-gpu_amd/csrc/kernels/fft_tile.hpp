@@ -229,6 +229,157 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
     }
 }
 
+// ---------------------------------------------------------------------------
+// Column pass with the Stockham exchanges in halves (the first pass of a 1D
+// multi-pass plan, which reads the caller's input from HBM).  T = L/32
+// threads per column hold 32 elements each (positions t + T*m) and run
+// NB = 32/R butterflies b = t + T*i of every stage of the radix list
+// (16, ..., 16, r).  Butterfly b of stage s writes to j*L_s*R + k + q*L_s
+// (j = b / L_s, k = b % L_s), below L/2 exactly when i < NB/2, so every
+// exchange runs in two rounds through an LDS tile of L/2 positions: round h
+// writes butterflies i in [h*NB/2, (h+1)*NB/2), then each thread reads its
+// elements m in [16h, 16h + 16).  Half the LDS of the 16-element tile: four
+// 33 KB workgroups per CU instead of two for 128 / 256 points (64 / 32
+// columns), two 68 KB ones instead of one for 1024 (16 columns), so more of a
+// CU's tiles are loading while others compute.  The last stage's outputs are
+// the thread's own positions t + T*m.
+template <int LOGL>
+struct HalvesShape {
+    static constexpr int N = 1 << LOGL, E = 32, T = N / E, HALF = N / 2;
+    static constexpr int NFULL = LOGL / 4, REM = LOGL % 4;
+    static constexpr int NSTAGES = NFULL + (REM ? 1 : 0);
+    static_assert(LOGL >= 7 && LOGL <= 10, "half exchanges: 128 .. 1024 points");
+};
+
+template <int LOGL, int S>
+struct HalvesStage {
+    static constexpr int LOGR = (S < HalvesShape<LOGL>::NFULL) ? 4 : HalvesShape<LOGL>::REM;
+    static constexpr int R = 1 << LOGR;
+    static constexpr int NB = HalvesShape<LOGL>::E / R;  // butterflies per thread
+    static constexpr int L = 1 << (4 * S);              // product of the earlier radices
+};
+
+// Stage S: y[i + NB*q] = output q of butterfly i (inputs x[i + NB*p]).  The
+// twiddles come from the table of the radix list (16, ..., 16, r), the one
+// the 16-element geometry uses.
+template <int LOGL, int S>
+__device__ __forceinline__ void halves_stage(const float2* x, float2* y, int t, const float2* __restrict__ tw) {
+    using H = HalvesShape<LOGL>;
+    using St = HalvesStage<LOGL, S>;
+#pragma unroll
+    for (int i = 0; i < St::NB; ++i) {
+        float2 u[St::R];
+#pragma unroll
+        for (int p = 0; p < St::R; ++p) u[p] = x[i + St::NB * p];
+        if constexpr (St::L > 1) {
+            const int k = (t + H::T * i) & (St::L - 1);
+            apply_stage_twiddles<St::R>(u, tw + stockham_tw_offset<LOGL, 4>(S) + k * tw_row_len(St::R));
+        }
+        Dft<St::R>::run(u);
+#pragma unroll
+        for (int q = 0; q < St::R; ++q) y[i + St::NB * q] = u[q];
+    }
+}
+
+// Exchange after stage S: x[m] = the element at position t + T*m.
+template <int LOGL, int S, int G>
+__device__ __forceinline__ void halves_exchange(const float2* y, float2* x, int t, int c, float2* __restrict__ lds) {
+    using H = HalvesShape<LOGL>;
+    using St = HalvesStage<LOGL, S>;
+    using Lay = TileLayout<LOGL - 1, G>;
+    static_assert(G >= 16, "wide tiles (pitch G + 1)");
+    // at(d + q*L, c) - at(d, c): output q of a butterfly is q*L positions further.
+    constexpr int QSTEP = Lay::template step<St::L>();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (S > 0 || h > 0) __syncthreads();  // the previous round's readers are done
+#pragma unroll
+        for (int ii = 0; ii < St::NB / 2; ++ii) {
+            const int i = h * (St::NB / 2) + ii;
+            const int b = t + H::T * i;
+            const int d0 = (b >> (4 * S)) * St::L * St::R + (b & (St::L - 1)) - H::HALF * h;
+            float2* wbase = lds + Lay::at(d0, c);
+#pragma unroll
+            for (int q = 0; q < St::R; ++q) wbase[q * QSTEP] = y[i + St::NB * q];
+        }
+        __syncthreads();
+        const float2* rbase = lds + Lay::at(t, c);
+#pragma unroll
+        for (int m = 0; m < H::E / 2; ++m) x[(H::E / 2) * h + m] = rbase[m * Lay::template step<H::T>()];
+    }
+}
+
+template <int LOGL, int S, int G>
+struct HalvesStages {
+    __device__ __forceinline__ static void run(float2* x, float2* y, int t, int c, const float2* __restrict__ tw,
+                                               float2* __restrict__ lds) {
+        halves_stage<LOGL, S>(x, y, t, tw);
+        if constexpr (S + 1 < HalvesShape<LOGL>::NSTAGES) {
+            halves_exchange<LOGL, S, G>(y, x, t, c, lds);
+            HalvesStages<LOGL, S + 1, G>::run(x, y, t, c, tw, lds);
+        }
+    }
+};
+
+template <int LOGL, int G, bool LOAD_CACHED, bool STORE_CACHED, bool CONJ>
+__device__ __forceinline__ void fft_tile_halves_body(const float2* __restrict__ in, float2* __restrict__ out,
+                                                     const float2* __restrict__ tw, const float2* __restrict__ big,
+                                                     const TileGeom& g, float2* __restrict__ lds) {
+    using H = HalvesShape<LOGL>;
+    const int tid = threadIdx.x;
+    const int c = tid % G;
+    const int t = tid / G;
+    const TileCoords tc = tile_coords(g);
+    const char* in_tile = reinterpret_cast<const char*>(in + tc.ib);
+    char* out_tile = reinterpret_cast<char*>(out + tc.ob);
+
+    float2 x[H::E], y[H::E];
+    {
+        const uint32_t lane_off = (uint32_t)((c + (uint64_t)t * g.ies) * sizeof(float2));
+        const uint64_t row_step = (uint64_t)H::T * g.ies * sizeof(float2);
+#pragma unroll
+        for (int m = 0; m < H::E; ++m)
+            x[m] = gload<LOAD_CACHED>(reinterpret_cast<const float2*>(in_tile + m * row_step + lane_off));
+    }
+    if constexpr (CONJ) {
+        if (g.flags & FG_PASS_CONJ_IN) {
+#pragma unroll
+            for (int m = 0; m < H::E; ++m) x[m] = cconj(x[m]);
+        }
+    }
+    HalvesStages<LOGL, 0, G>::run(x, y, t, c, tw, lds);
+    if (g.log_m != 0) {
+        // Four-step twiddle W^(r*(t + T*m)) by one 32-step recurrence (about
+        // 2e-6 relative at its end, 1e-4 is the gate); restarting it at m = 16,
+        // from two more table reads or from four squarings of the step,
+        // measured 1.7-2.4 us slower per 128 MiB pass.
+        const uint64_t r = (uint64_t)g.twc * c + (uint64_t)g.tw0 * tc.t0 + (uint64_t)g.tw1 * tc.t1;
+        apply_pass_twiddle<H::E, H::T, true>(y, big, r, t, g.log_m);
+    }
+    const uint32_t lane_off = (uint32_t)((c + (uint64_t)t * g.oes) * sizeof(float2));
+    const uint64_t row_step = (uint64_t)H::T * g.oes * sizeof(float2);
+    const bool cs = CONJ && (g.flags & FG_PASS_CONJ_SCALE_OUT) != 0;
+#pragma unroll
+    for (int m = 0; m < H::E; ++m) {
+        float2 v = y[m];
+        if constexpr (CONJ) {
+            if (cs) v = cscale(cconj(v), g.scale);
+        }
+        gstore<STORE_CACHED>(reinterpret_cast<float2*>(out_tile + m * row_step + lane_off), v);
+    }
+}
+
+template <int LOGL, int G, bool LOAD_CACHED, bool STORE_CACHED>
+__device__ __forceinline__ void fft_tile_halves_pass(const float2* __restrict__ in, float2* __restrict__ out,
+                                                     const float2* __restrict__ tw, const float2* __restrict__ big,
+                                                     const TileGeom& g) {
+    __shared__ float2 lds[TileLayout<LOGL - 1, G>::ELEMS];
+    if (g.flags)
+        fft_tile_halves_body<LOGL, G, LOAD_CACHED, STORE_CACHED, true>(in, out, tw, big, g, lds);
+    else
+        fft_tile_halves_body<LOGL, G, LOAD_CACHED, STORE_CACHED, false>(in, out, tw, big, g, lds);
+}
+
 // One pass: a forward body and one that applies the inverse's conjugations.
 template <int LOGL, int LOGE, int G, bool ROWWISE, bool TWREC, bool LOAD_CACHED, bool STORE_CACHED>
 __device__ __forceinline__ void fft_tile_pass(const float2* __restrict__ in, float2* __restrict__ out,

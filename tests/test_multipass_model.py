@@ -114,15 +114,24 @@ def pass_policy(i, n, cached, g):
     return "_sc" if i == 0 else ("_cs" if i == n - 1 else "_cc")
 
 
+def use_halves_tile(log_l, g, rowwise, reads_input):
+    """use_halves_tile in fft_plan.cpp: the column pass that reads the plan's
+    input runs the 32-element kernel with the exchanges in halves."""
+    return reads_input and not rowwise and 7 <= log_l <= 10 and g == tile_columns(log_l)
+
+
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None):
     """The kernel of every pass of a multi-launch plan (1D N > 4096, or 2D with
     2^log_n rows and 2^log_cols columns), in launch order."""
-    def tile(p, pol):
-        return f"fg_tile_l{p['log_l']}_g{p['g']}_{'r' if p['rowwise'] else 'c'}{pol}"
+    def tile(p, pol, reads_input=False):
+        kind = "h" if use_halves_tile(p["log_l"], p["g"], p["rowwise"], reads_input) else \
+            ("r" if p["rowwise"] else "c")
+        return f"fg_tile_l{p['log_l']}_g{p['g']}_{kind}{pol}"
 
     if not two_d:
         passes = tile_geometry_1d(log_n, 1, cached)
-        return [tile(p, pass_policy(i, len(passes), cached, p["g"])) for i, p in enumerate(passes)]
+        return [tile(p, pass_policy(i, len(passes), cached, p["g"]), reads_input=(i == 0))
+                for i, p in enumerate(passes)]
     lc = log_n if log_cols is None else log_cols
     passes = tile_geometry_2d(log_n, 1, lc, cached)
     n = len(passes) + 1

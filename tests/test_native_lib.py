@@ -77,6 +77,9 @@ def instantiated_kernels():
         base = f"fg_tile_l{m.group(2)}_g{m.group(3)}_{m.group(5)}"
         # cache policies (FG_TILE_P): all four, or _cc alone for narrow tiles
         names |= {base + "_cc"} if m.group(1) else {base + pol for pol in ("", "_sc", "_cc", "_cs")}
+    # first-pass tiles with the exchanges in halves: unchunked and _sc
+    for m in re.finditer(r"^FG_TILE_HALVES\((\d+), (\d+)\)", src, flags=re.M):
+        names |= {f"fg_tile_l{m.group(1)}_g{m.group(2)}_h{pol}" for pol in ("", "_sc")}
     return names
 
 
