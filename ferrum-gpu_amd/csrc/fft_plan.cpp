@@ -40,7 +40,17 @@ constexpr StockhamGeom kStockhamLatency[kMaxLogNSingle + 1] = {
     {2, 1}, {0, 0}, {3, 1}, {0, 0}, {3, 1},
 };
 
-std::string file_image;  // backing store when FERRUM_GPU_CODE_OBJECT is set
+// The code object named by FERRUM_GPU_CODE_OBJECT, read once per process (a
+// function-local static: thread-safe when several threads open devices);
+// empty if the file cannot be read.
+const std::string& file_image(const char* path) {
+    static const std::string image = [path] {
+        std::ifstream f(path, std::ios::binary);
+        if (!f) return std::string();
+        return std::string(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
+    }();
+    return image;
+}
 
 }  // namespace
 
@@ -50,13 +60,10 @@ KernelArtifact fft_code_object() {
     a.name = "ferrum-gpu-fft-kernels";
     a.target = "gfx950";
     if (const char* path = getenv("FERRUM_GPU_CODE_OBJECT")) {
-        if (file_image.empty()) {
-            std::ifstream f(path, std::ios::binary);
-            if (!f) invalid(std::string("FERRUM_GPU_CODE_OBJECT: cannot read ") + path);
-            file_image.assign(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
-        }
-        a.image = file_image.data();
-        a.size = file_image.size();
+        const std::string& image = file_image(path);
+        if (image.empty()) invalid(std::string("FERRUM_GPU_CODE_OBJECT: cannot read ") + path);
+        a.image = image.data();
+        a.size = image.size();
     } else {
         a.image = fg_fft_code_object_start;
         a.size = (size_t)(fg_fft_code_object_end - fg_fft_code_object_start);
@@ -148,9 +155,9 @@ uint32_t cached_tile_columns(uint32_t log_l, bool rowwise) {
 
 bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise, bool reads_input) {
     // Measured on gfx950 against the 16-element tiles at 512 MiB per plan (the
-    // first pass, us per 128 MiB chunk): 128 points 55.1 -> 50.5, 256: 56.9 ->
-    // 52.0, 512: 62.9 -> 59.3, 1024: 67.6 -> 60.3; whole plans 1-5 % faster
-    // for every 1D length 2^13 .. 2^24.
+    // first pass, us per 128 MiB chunk): 128 points 54.3 -> 50.6, 256: 57.0 ->
+    // 54.4 (config 4's pass: 52.8 -> 48.4), 512: 63.4 -> 59.4, 1024: 68.4 ->
+    // 61.0; whole plans 1-5 % faster for every 1D length 2^13 .. 2^24.
     return reads_input && !rowwise && log_l >= 7 && log_l <= 10 && g == tile_columns(log_l);
 }
 
