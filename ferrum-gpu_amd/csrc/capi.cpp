@@ -19,6 +19,7 @@
 #include "fft_plan.hpp"
 #include "ferrum_gpu.h"
 #include "hip_backend.hpp"
+#include "host_stage.hpp"
 
 using fg::Buffer;
 using fg::Cf32;
@@ -44,6 +45,7 @@ struct fg_device {
     Buffer<Cf32, HipBackend> staging;
     fg::Pointwise pointwise;  // elementwise kernels of fft_module
     std::atomic<int> dependents{0};  // live plans and captured graphs made on this device
+    std::unique_ptr<fg::HostStager> stager;  // pinned pieces of the host path (first large call)
 };
 
 struct fg_module {
@@ -162,6 +164,10 @@ Direction parse_dir(int direction) {
     fg::invalid("direction must be 1 (forward) or -1 (inverse), got " + std::to_string(direction));
 }
 
+// Host arrays from this size up go through HostStager's pinned pieces; below
+// it a plain pageable copy costs less than the staging's fixed overheads.
+constexpr size_t kStagedBytes = 2u << 20;
+
 // Host path shared by the 1D and 2D entry points: stage through one device
 // buffer (grown on demand, kept per device), run in place, copy back.
 void run_host(fg_device* d, int dims, uint32_t log_n, uint32_t log_rows, size_t batch, size_t total,
@@ -173,9 +179,19 @@ void run_host(fg_device* d, int dims, uint32_t log_n, uint32_t log_rows, size_t 
         d->staging = d->dev->alloc<Cf32>(total);
     }
     const auto& h = d->dev->handle();
-    HipBackend::copy_async(h, d->staging.data(), in, total * sizeof(Cf32), hipMemcpyHostToDevice, nullptr);
+    const size_t bytes = total * sizeof(Cf32);
+    if (bytes >= kStagedBytes) {
+        // Through pinned pieces and parallel host copies (host_stage.hpp).
+        if (!d->stager) d->stager.reset(new fg::HostStager(h));
+        const hipStream_t s = d->dev->default_stream();
+        d->stager->to_device(d->staging.data(), in, bytes, s);
+        plan.exec(d->staging.data(), d->staging.data(), dir, normalize, s);
+        d->stager->to_host(out, d->staging.data(), bytes, s);
+        return;
+    }
+    HipBackend::copy_async(h, d->staging.data(), in, bytes, hipMemcpyHostToDevice, nullptr);
     plan.exec(d->staging.data(), d->staging.data(), dir, normalize, nullptr);
-    HipBackend::copy_async(h, out, d->staging.data(), total * sizeof(Cf32), hipMemcpyDeviceToHost, nullptr);
+    HipBackend::copy_async(h, out, d->staging.data(), bytes, hipMemcpyDeviceToHost, nullptr);
     d->dev->sync();
 }
 
