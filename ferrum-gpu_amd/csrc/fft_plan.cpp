@@ -26,9 +26,12 @@ struct StockhamGeom {
     uint32_t log_e;  // log2 of elements per thread
     uint32_t fpb;    // transforms per workgroup
 };
+// N = 16 .. 128 hold 4 or 8 elements per thread: 16 (the larger sizes' choice)
+// measured 217 / 232 / 234 / 211 us per 512 MiB batch against 182 / 183 / 171
+// / 173 us for the entries below (N = 256 .. 4096 measured best at 16).
 constexpr StockhamGeom kStockham[kMaxLogNSingle + 1] = {
     {0, 0}, {0, 0},          // log_n 0, 1: unsupported
-    {2, 64}, {3, 64}, {4, 64}, {4, 32}, {4, 16}, {4, 8}, {4, 4}, {4, 2}, {4, 2}, {4, 1}, {4, 1},
+    {2, 64}, {3, 64}, {3, 32}, {3, 16}, {2, 4}, {3, 4}, {4, 4}, {4, 2}, {4, 2}, {4, 1}, {4, 1},
 };
 // Latency geometry (fg_fft_n<L>_lat, one transform per workgroup, fewer
 // elements per thread: more threads per transform, shorter serial chains),

@@ -45,10 +45,10 @@ using namespace fg;
 
 FG_STOCKHAM(2, 2, 64)    // N=4:    1 thread  / transform, 64 per wave
 FG_STOCKHAM(3, 3, 64)    // N=8:    1 thread  / transform
-FG_STOCKHAM(4, 4, 64)    // N=16:   1 thread  / transform
-FG_STOCKHAM(5, 4, 32)    // N=32:   2 threads / transform
-FG_STOCKHAM(6, 4, 16)    // N=64:   4 threads
-FG_STOCKHAM(7, 4, 8)     // N=128:  8 threads
+FG_STOCKHAM(4, 3, 32)    // N=16:   2 threads / transform
+FG_STOCKHAM(5, 3, 16)    // N=32:   4 threads / transform
+FG_STOCKHAM(6, 2, 4)     // N=64:   16 threads (4 elements each)
+FG_STOCKHAM(7, 3, 4)     // N=128:  16 threads (8 elements each)
 FG_STOCKHAM(8, 4, 4)     // N=256:  16 threads
 FG_STOCKHAM(9, 4, 2)     // N=512:  32 threads
 FG_STOCKHAM(10, 4, 2)    // N=1024: 64 threads (one wave) per transform, 2 per workgroup
@@ -76,10 +76,10 @@ FG_STOCKHAM_LAT(8, 2)    // N=256:  64 threads (4 elements each)
 FG_STOCKHAM_LAT(10, 3)   // N=1024: 128 threads (8 elements each)
 FG_STOCKHAM_LAT(12, 3)   // N=4096: 512 threads (8 elements each)
 
-FG_STOCKHAM_SC(4, 4, 64)
-FG_STOCKHAM_SC(5, 4, 32)
-FG_STOCKHAM_SC(6, 4, 16)
-FG_STOCKHAM_SC(7, 4, 8)
+FG_STOCKHAM_SC(4, 3, 32)
+FG_STOCKHAM_SC(5, 3, 16)
+FG_STOCKHAM_SC(6, 2, 4)
+FG_STOCKHAM_SC(7, 3, 4)
 FG_STOCKHAM_SC(8, 4, 4)
 FG_STOCKHAM_SC(9, 4, 2)
 FG_STOCKHAM_SC(10, 4, 2)

@@ -19,7 +19,7 @@ import oracle
 from conftest import rel_l2, uniform_c64
 
 # kStockham in fft_plan.cpp / FG_STOCKHAM in fft_kernels.hip: (log_e, fpb)
-GEOM = {2: (2, 64), 3: (3, 64), 4: (4, 64), 5: (4, 32), 6: (4, 16), 7: (4, 8), 8: (4, 4),
+GEOM = {2: (2, 64), 3: (3, 64), 4: (3, 32), 5: (3, 16), 6: (2, 4), 7: (3, 4), 8: (4, 4),
         9: (4, 2), 10: (4, 2), 11: (4, 1), 12: (4, 1)}
 # kStockhamLatency / FG_STOCKHAM_LAT: single-pass plans too small to fill the GPU
 LATENCY_GEOM = {8: (2, 1), 10: (3, 1), 12: (3, 1)}
