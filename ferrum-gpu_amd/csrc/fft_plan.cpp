@@ -386,6 +386,28 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     if (batch == 0) invalid("batch must be positive");
     std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::TwoD, log_cols, log_rows, batch));
     const uint64_t R = 1ull << log_rows, C = 1ull << log_cols, RC = R * C;
+    if (log_rows + log_cols <= FG_SMALL2D_MAX_LOG) {
+        // Images of up to 4096 points: the whole 2D FFT in one pass through
+        // LDS (kernels/fft_2d_small.hpp); nothing to chunk.
+        p->chunk_ = batch;
+        p->cached_ = false;
+        Step s;
+        s.small2d = true;
+        s.name = "fg_fft2d_l" + std::to_string(log_rows) + "_" + std::to_string(log_cols);
+        s.fn = HipBackend::get_kernel(mod, s.name.c_str());
+        s.fpb = FG_SMALL2D_FPI(log_rows, log_cols);
+        s.block = Dim3(FG_SMALL2D_BLOCK(log_rows, log_cols));
+        if ((batch + s.fpb - 1) / s.fpb > 0x7fffffffull) invalid("batch too large for one launch");
+        s.src = Buf::In;
+        s.dst = Buf::Out;
+        s.tw = p->stage_table(log_cols, FG_SMALL2D_LOGE);
+        s.tw_cols = p->stage_table(log_rows, FG_SMALL2D_LOGE);
+        s.per_unit = 1;
+        p->steps_.push_back(s);
+        p->main_kernel_ = s.name;
+        p->pw_ = Pointwise(mod);
+        return p;
+    }
     const bool split = split_2d_columns(log_rows);
     const size_t npass = split ? 3 : 2;
     p->choose_chunk();
@@ -515,7 +537,17 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
             void* src = bind(s.src);
             void* dst = bind(s.dst);
             const void* tw = s.tw;
-            if (!s.tile) {
+            if (s.small2d) {
+                uint64_t count = s.per_unit * units;
+                float sc = scale;
+                const void* twc = s.tw_cols;
+                void* args[] = {&src, &dst, (void*)&tw, (void*)&twc, &count, &sc, &flags};
+                const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
+                if (events)
+                    HipBackend::launch_stamped(dev_->handle(), stream, s.fn, grid, s.block, 0, args, events[launch]);
+                else
+                    HipBackend::launch(dev_->handle(), stream, s.fn, grid, s.block, 0, args);
+            } else if (!s.tile) {
                 uint64_t count = s.per_unit * units;
                 float sc = scale;
                 void* args[] = {&src, &dst, (void*)&tw, &count, &sc, &flags};

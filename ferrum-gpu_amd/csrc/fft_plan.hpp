@@ -94,6 +94,8 @@ private:
     enum class Buf { In, Out, Work };
     struct Step {
         bool tile = false;                      // tile pass (else single-pass Stockham)
+        bool small2d = false;                   // one-pass 2D of small images (fg_fft2d_*)
+        const void* tw_cols = nullptr;          // small2d: the column stage table
         std::string name;
         HipBackend::KernelHandle fn = nullptr;
         Dim3 block;

@@ -1,0 +1,116 @@
+// fft_2d_small.hpp -- the whole 2D FFT of images of R x C <= 4096 points in
+// one pass through HBM: a row pass and a column pass would each move every
+// byte once; here a workgroup loads FPI whole images into LDS, transforms
+// their rows and then their columns there, and stores them.
+//
+// Per image the LDS holds R rows of pitch P = C + C/16 + 1 (odd, so a column
+// read touches distinct banks):
+//   1. coalesced load of the workgroup's images (64 lanes x 8 contiguous bytes
+//      per instruction), element (r, c) at r*P + c;
+//   2. rows: thread (r, t), t < C/E, takes positions t + (C/E)*m of row r and
+//      runs the Stockham stages of length C (fft_stockham.hpp), exchanging in
+//      its own row's P slots (lds_pos layout: C + C/16 <= P); its outputs go
+//      back to r*P + k;
+//   3. columns: thread (c, t), t < R/E, takes rows t + (R/E)*m of column c;
+//      once every column is read, the image's memory holds the column
+//      exchanges (column c at c*(R + R/16), C*(R + R/16) <= R*P) for the
+//      Stockham stages of length R; the outputs go back to k*P + c;
+//   4. coalesced store.
+// A row's (a column's) threads are consecutive and lie in one wave, so their
+// exchanges need only wave-scope ordering; the phases are separated by
+// workgroup barriers.  Stage twiddles: the tables of the radix lists
+// (E, ..., E, r) for lengths C and R.  Inverse: conjugate on load, conjugate
+// and scale on store.
+#pragma once
+#include "fft_stockham.hpp"
+
+namespace fg {
+
+template <int LR, int LC, int LOGE, int FPI>
+struct Small2D {
+    static constexpr int R = 1 << LR, C = 1 << LC, N = R * C, E = 1 << LOGE;
+    static constexpr int TC = C / E;                 // threads per row
+    static constexpr int TR = R / E;                 // threads per column
+    static constexpr int TIMG = N / E;               // threads per image
+    static constexpr int BLOCK = FPI * TIMG;
+    static constexpr int P = C + C / 16 + 1;         // LDS row pitch
+    static constexpr int IMG = R * P;                // LDS elements per image
+    static_assert(LOGE <= LR && LOGE <= LC, "at least E points per row and column");
+    static_assert(C + C / 16 <= P && C * (R + R / 16) <= IMG, "exchange regions fit the image's LDS");
+    static_assert(TC <= 64 && TR <= 64 && 64 % TC == 0 && 64 % TR == 0, "a row's / column's threads lie in one wave");
+    static_assert(BLOCK <= 1024 && BLOCK % 64 == 0, "whole waves, at most 1024 threads");
+    static_assert(BLOCK == FG_SMALL2D_BLOCK(LR, LC) || LOGE != FG_SMALL2D_LOGE, "the host's launch geometry");
+};
+
+template <int LR, int LC, int LOGE, int FPI, class IO>
+__device__ __forceinline__ void fft2d_small_body(const IO io, const float2* __restrict__ tw_rows,
+                                                 const float2* __restrict__ tw_cols, uint64_t batch, float scale,
+                                                 uint32_t flags) {
+    using S = Small2D<LR, LC, LOGE, FPI>;
+    __shared__ float2 lds[FPI * S::IMG];
+    const int tid = threadIdx.x;
+    const int slot = tid / S::TIMG;
+    const int local = tid - slot * S::TIMG;
+    const uint64_t i0 = (uint64_t)blockIdx.x * FPI;
+    float2* img = lds + slot * S::IMG;
+    const bool cin = (flags & FG_PASS_CONJ_IN) != 0;
+    const bool cs = (flags & FG_PASS_CONJ_SCALE_OUT) != 0;
+
+    // 1. Load: element e of the block's FPI*N -> image e / N, (row, col) of e % N.
+#pragma unroll
+    for (int j = 0; j < S::E; ++j) {
+        const int e = tid + S::BLOCK * j;
+        const int is = e >> (LR + LC);
+        const int n = e & (S::N - 1);
+        float2 v = make_float2(0.f, 0.f);
+        if (i0 + is < batch) v = io.load(i0 * S::N + e);
+        if (cin) v = cconj(v);
+        lds[is * S::IMG + (n >> LC) * S::P + (n & (S::C - 1))] = v;
+    }
+    __syncthreads();
+
+    // 2. Rows.
+    {
+        const int r = local / S::TC;
+        const int t = local - r * S::TC;
+        float2* row = img + r * S::P;
+        float2 x[S::E];
+#pragma unroll
+        for (int m = 0; m < S::E; ++m) x[m] = row[t + S::TC * m];
+        StockhamStages<LC, LOGE, 0>::template run<true>(x, t, tw_rows, row);
+        wave_sync();  // the row's last exchange reads are done before the row is rewritten
+#pragma unroll
+        for (int m = 0; m < S::E; ++m) row[t + S::TC * m] = x[m];
+    }
+    __syncthreads();
+
+    // 3. Columns.
+    {
+        const int c = local / S::TR;
+        const int t = local - c * S::TR;
+        float2 x[S::E];
+#pragma unroll
+        for (int m = 0; m < S::E; ++m) x[m] = img[(t + S::TR * m) * S::P + c];
+        __syncthreads();  // every column read before the image's memory holds exchanges
+        StockhamStages<LR, LOGE, 0>::template run<true>(x, t, tw_cols, img + c * (S::R + S::R / 16));
+        __syncthreads();  // every exchange done before the plain layout is rewritten
+#pragma unroll
+        for (int m = 0; m < S::E; ++m) img[(t + S::TR * m) * S::P + c] = x[m];
+    }
+    __syncthreads();
+
+    // 4. Store.
+#pragma unroll
+    for (int j = 0; j < S::E; ++j) {
+        const int e = tid + S::BLOCK * j;
+        const int is = e >> (LR + LC);
+        const int n = e & (S::N - 1);
+        if (i0 + is < batch) {
+            float2 v = lds[is * S::IMG + (n >> LC) * S::P + (n & (S::C - 1))];
+            if (cs) v = cscale(cconj(v), scale);
+            io.store(i0 * S::N + e, v);
+        }
+    }
+}
+
+}  // namespace fg

@@ -146,6 +146,36 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
     if (i < n) c[i] = a[i] + b[i];
 }
 
+// ------------------------------------------------------------ small 2D
+//
+// fg_fft2d_l<LR>_<LC>: the whole 2D FFT of 2^LR x 2^LC images (<= 4096 points)
+// in one pass, FG_SMALL2D_FPI images per workgroup (fft_2d_small.hpp).
+#include "fft_2d_small.hpp"
+
+#define FG_FFT2D(LR, LC)                                                                            \
+    extern "C" __global__ __launch_bounds__(FG_SMALL2D_BLOCK(LR, LC)) void                           \
+        fg_fft2d_l##LR##_##LC(const float2* __restrict__ in, float2* __restrict__ out,              \
+                              const float2* __restrict__ tw_rows, const float2* __restrict__ tw_cols, \
+                              uint64_t batch, float scale, uint32_t flags) {                         \
+        fft2d_small_body<LR, LC, FG_SMALL2D_LOGE, FG_SMALL2D_FPI(LR, LC)>(InterleavedIO{in, out}, tw_rows, \
+                                                                          tw_cols, batch, scale, flags); \
+    }
+FG_FFT2D(4, 4)
+FG_FFT2D(4, 5)
+FG_FFT2D(4, 6)
+FG_FFT2D(4, 7)
+FG_FFT2D(4, 8)
+FG_FFT2D(5, 4)
+FG_FFT2D(5, 5)
+FG_FFT2D(5, 6)
+FG_FFT2D(5, 7)
+FG_FFT2D(6, 4)
+FG_FFT2D(6, 5)
+FG_FFT2D(6, 6)
+FG_FFT2D(7, 4)
+FG_FFT2D(7, 5)
+FG_FFT2D(8, 4)
+
 // ------------------------------------------------------- multi-pass tiles
 //
 // fg_tile_l<LOGL>_g<G>_<c|r|h>[_<policy>]: one pass over G columns of length

@@ -28,6 +28,15 @@ typedef struct TileGeom {
     uint32_t remap;         /* 1: XCD-aware tile order (grid a multiple of 8; fft_tile.hpp) */
 } TileGeom;
 
+/* One-pass 2D FFT of images of 2^lr x 2^lc <= 4096 points (fft_2d_small.hpp):
+ * 2^FG_SMALL2D_LOGE elements per thread, FG_SMALL2D_FPI(lr, lc) images per
+ * workgroup (256 threads, or one image when it needs more). */
+#define FG_SMALL2D_MAX_LOG 12
+#define FG_SMALL2D_LOGE 3
+#define FG_SMALL2D_FPI(lr, lc) \
+    ((((1 << ((lr) + (lc))) >> FG_SMALL2D_LOGE) >= 256) ? 1 : (256 / ((1 << ((lr) + (lc))) >> FG_SMALL2D_LOGE)))
+#define FG_SMALL2D_BLOCK(lr, lc) (FG_SMALL2D_FPI(lr, lc) * ((1 << ((lr) + (lc))) >> FG_SMALL2D_LOGE))
+
 #ifdef __cplusplus
 }  // namespace fg
 #endif

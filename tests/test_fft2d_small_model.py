@@ -1,0 +1,108 @@
+"""CPU model of the one-pass 2D FFT of small images (fft2d_small_body,
+ferrum-gpu_amd/csrc/kernels/fft_2d_small.hpp), checked against the oracle
+before any launch.
+
+Per image the workgroup's LDS holds R rows of pitch P = C + C/16 + 1.  The
+model replays the kernel's index bookkeeping: the coalesced load and store
+cover the workgroup's FPI images exactly once, each row's Stockham exchanges
+stay in its own P slots and each column's in its own R + R/16 slots of the
+image, all inside the image, and the data flow (rows, then columns, each by
+the Stockham model of tests/test_stockham_model.py, which checks the
+exchanges' own indices) gives the 2D DFT.  The host's launch geometry
+(FG_SMALL2D_* in kernels/tile_geom.h) is mirrored here and checked against
+the sources.
+"""
+
+from __future__ import annotations
+
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_l2, uniform_c64
+from test_stockham_model import model as stockham_model
+
+LOGE = 3
+MAX_LOG = 12
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def fpi(lr, lc):
+    """FG_SMALL2D_FPI: images per workgroup (256 threads, or one image)."""
+    t = (1 << (lr + lc)) >> LOGE
+    return 1 if t >= 256 else 256 // t
+
+
+def shapes():
+    return [(lr, lc) for lr in range(4, 9) for lc in range(4, 9) if lr + lc <= MAX_LOG]
+
+
+def small2d_model(images, lr, lc):
+    """images: (FPI, R, C) complex; returns the kernel's output, checking indices."""
+    R, C = 1 << lr, 1 << lc
+    N, E = R * C, 1 << LOGE
+    F = images.shape[0]
+    P = C + C // 16 + 1
+    IMG = R * P
+    block = F * (N // E)
+    # 1. load: e = tid + BLOCK*j -> LDS is*IMG + r*P + c
+    lds = np.full(F * IMG, np.nan + 0j)
+    e = (np.arange(block)[:, None] + block * np.arange(E)[None, :]).reshape(-1)
+    assert np.array_equal(np.sort(e), np.arange(F * N))
+    img_of, n = e >> (lr + lc), e & (N - 1)
+    idx = img_of * IMG + (n >> lc) * P + (n & (C - 1))
+    assert idx.max() < lds.size and len(np.unique(idx)) == idx.size
+    lds[idx] = images.reshape(-1)[e]
+    out = np.empty((F, R, C), np.complex128)
+    for s in range(F):
+        img = lds[s * IMG:(s + 1) * IMG]
+        # 2. rows: row r's exchanges in [r*P, r*P + C + C/16)
+        assert C + C // 16 <= P and (R - 1) * P + C + C // 16 <= IMG
+        rows = np.stack([img[r * P:r * P + C] for r in range(R)])
+        rows = stockham_model(rows.reshape(-1), lc, LOGE).reshape(R, C)
+        for r in range(R):
+            img[r * P:r * P + C] = rows[r]
+        # 3. columns: column c read at k*P + c; its exchanges in [c*(R + R/16), (c+1)*(R + R/16))
+        cols = np.stack([img[np.arange(R) * P + c] for c in range(C)])
+        assert C * (R + R // 16) <= IMG
+        cols = stockham_model(cols.reshape(-1), lr, LOGE).reshape(C, R)
+        for c in range(C):
+            img[np.arange(R) * P + c] = cols[c]
+        out[s] = np.stack([img[r * P:r * P + C] for r in range(R)])
+    return out
+
+
+@pytest.mark.parametrize("lr,lc", shapes())
+def test_small2d_model_matches_oracle(lr, lc):
+    R, C = 1 << lr, 1 << lc
+    F = min(fpi(lr, lc), 3)
+    x = uniform_c64(np.random.default_rng(lr * 16 + lc), F * R * C).reshape(F, R, C)
+    got = small2d_model(x, lr, lc)
+    want = np.fft.fft2(x.astype(np.complex128))
+    if lr == lc:
+        assert rel_l2(got, oracle.fft_2d(x, lr)) < 1e-5
+    assert rel_l2(got, want) < 1e-5
+
+
+@pytest.mark.parametrize("lr,lc", shapes())
+def test_small2d_geometry_fits(lr, lc):
+    R, C = 1 << lr, 1 << lc
+    N, E = R * C, 1 << LOGE
+    block = fpi(lr, lc) * N // E
+    assert block <= 1024 and block % 64 == 0
+    tc, tr = C // E, R // E
+    assert tc <= 64 and tr <= 64 and 64 % tc == 0 and 64 % tr == 0   # rows / columns within a wave
+    lds = fpi(lr, lc) * R * (C + C // 16 + 1) * 8
+    assert lds <= 64 * 1024
+
+
+def test_small2d_mirror_matches_the_sources():
+    geom = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "tile_geom.h")).read()
+    assert re.search(r"#define FG_SMALL2D_LOGE (\d+)", geom).group(1) == str(LOGE)
+    assert re.search(r"#define FG_SMALL2D_MAX_LOG (\d+)", geom).group(1) == str(MAX_LOG)
+    hip = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
+    inst = {(int(a), int(b)) for a, b in re.findall(r"^FG_FFT2D\((\d+), (\d+)\)", hip, flags=re.M)}
+    assert inst == set(shapes())

@@ -77,6 +77,8 @@ def instantiated_kernels():
         base = f"fg_tile_l{m.group(2)}_g{m.group(3)}_{m.group(5)}"
         # cache policies (FG_TILE_P): all four, or _cc alone for narrow tiles
         names |= {base + "_cc"} if m.group(1) else {base + pol for pol in ("", "_sc", "_cc", "_cs")}
+    # one-pass 2D FFTs of small images
+    names |= {f"fg_fft2d_l{a}_{b}" for a, b in re.findall(r"^FG_FFT2D\((\d+), (\d+)\)", src, flags=re.M)}
     # first-pass tiles with the exchanges in halves: unchunked and _sc
     for m in re.finditer(r"^FG_TILE_HALVES\((\d+), (\d+)\)", src, flags=re.M):
         names |= {f"fg_tile_l{m.group(1)}_g{m.group(2)}_h{pol}" for pol in ("", "_sc")}
