@@ -8,7 +8,7 @@ on): batched 1D forward C2C complex64 FFT, N = 1024, batch = 65536 (512 MiB in,
 cfg2_4096, cfg4, cfg5) and the operations beside the path (cfg3_split: config 3
 in the split layout; cmul, cmul_split, deinterleave, interleave: the pointwise
 kernels over config 3's 2^26 elements; transpose: an 8192 x 8192 complex64
-matrix) for the numbers quoted in DESIGN.md.
+matrix).
 
 A "step" is one pass of the workload over its batch (for cfg2: the forward and
 the normalised inverse transform).  W untimed warmup steps, then K timed steps

@@ -227,7 +227,7 @@ FG_API int fg_fft_1d_c2c_pow2_host(fg_device_t dev, const float *in, float *out,
 FG_API int fg_fft_2d_c2c_pow2_host(fg_device_t dev, const float *in, float *out, uint32_t log_n,
                             size_t batch, int direction, int normalize);
 
-/* Non-square 2D (SURVEY's "general 2D", beyond Plan2D's square images,
+/* Non-square 2D (general power-of-two images, beyond Plan2D's square ones,
  * crates/ferrum-gpu-fft/src/plan.rs:98-135): `batch` row-major images of
  * 2^log_rows x 2^log_cols, each log in [4, 12]; normalize scales the inverse
  * by 1/(rows*cols). */

@@ -64,7 +64,7 @@ def test_radix_tables_match_fp64_roots():
             exp = np.concatenate(exp)
             assert tw.size == exp.size
             assert np.max(np.abs(tw - exp)) < 4e-7
-    assert oracle.twiddles_radix4(10).size == 4 * (1024 - 1) // 3  # 1364
+    assert oracle.twiddles_radix4(10).size == 4 * (1024 - 1) // 3  # 1364: 4·m entries per stage, m = 1, 4, ..., 256
     assert oracle.twiddles_radix8(12).size == 4680
 
 
