@@ -58,6 +58,42 @@ def test_rect_2d_inverse_roundtrip(gpu_device, lr, lc):
     assert rel_l2(back, x) <= TOL
 
 
+SMALL_2D = [(lr, lc) for lr in range(4, 9) for lc in range(4, 9) if lr + lc <= 12]
+
+
+@pytest.mark.parametrize("lr,lc", SMALL_2D)
+def test_one_pass_small_2d_every_shape(gpu_device, lr, lc):
+    """The one-kernel plans (images of up to 4096 points): forward and
+    normalised inverse, a batch that leaves the last workgroup partly empty,
+    out of place and in place."""
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer
+
+    n = 1 << (lr + lc)
+    per_group = max(1, 256 * 8 // n)          # images per workgroup
+    batch = 2 * per_group + 1
+    rng = np.random.default_rng(900 + 16 * lr + lc)
+    x = uniform_c64(rng, batch * n).reshape(batch, 1 << lr, 1 << lc)
+    print(f"[case] one-pass 2d {1 << lr}x{1 << lc} batch={batch}", flush=True)
+    plan = ferrum_gpu.fft.Plan2D(lr, batch, gpu_device, log_cols=lc)
+    assert plan.kernel_names() == [f"fg_fft2d_l{lr}_{lc}"]
+    a, b = DeviceBuffer(gpu_device, plan.nbytes), DeviceBuffer(gpu_device, plan.nbytes)
+    a.copy_from_host(x)
+    plan.execute(a, b, "forward")
+    gpu_device.sync()
+    fwd = np.empty_like(x)
+    b.copy_to_host(fwd)
+    assert rel_l2(fwd, oracle_2d_rect(x, lr, lc)) <= TOL
+    assert rel_l2(fwd, np.fft.fft2(x.astype(np.complex128))) <= TOL
+    plan.execute(b, b, "inverse", True)       # in place
+    gpu_device.sync()
+    inv = np.empty_like(x)
+    b.copy_to_host(inv)
+    assert rel_l2(inv, oracle_2d_rect(fwd, lr, lc, "inverse", True)) <= TOL
+    assert rel_l2(inv, x) <= TOL
+    plan.destroy()
+
+
 def test_square_api_equals_rect_api(gpu_device):
     import ferrum_gpu
 
