@@ -387,7 +387,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     std::unique_ptr<FftPlan> p(new FftPlan(dev, Kind::TwoD, log_cols, log_rows, batch));
     const uint64_t R = 1ull << log_rows, C = 1ull << log_cols, RC = R * C;
     if (log_rows + log_cols <= FG_SMALL2D_MAX_LOG) {
-        // Images of up to 4096 points: the whole 2D FFT in one pass through
+        // Images of up to 16384 points: the whole 2D FFT in one pass through
         // LDS (kernels/fft_2d_small.hpp); nothing to chunk.
         p->chunk_ = batch;
         p->cached_ = false;
@@ -400,8 +400,8 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         if ((batch + s.fpb - 1) / s.fpb > 0x7fffffffull) invalid("batch too large for one launch");
         s.src = Buf::In;
         s.dst = Buf::Out;
-        s.tw = p->stage_table(log_cols, FG_SMALL2D_LOGE);
-        s.tw_cols = p->stage_table(log_rows, FG_SMALL2D_LOGE);
+        s.tw = p->stage_table(log_cols, FG_SMALL2D_LOGE(log_rows, log_cols));
+        s.tw_cols = p->stage_table(log_rows, FG_SMALL2D_LOGE(log_rows, log_cols));
         s.per_unit = 1;
         p->steps_.push_back(s);
         p->main_kernel_ = s.name;

@@ -1,10 +1,11 @@
-// fft_2d_small.hpp -- the whole 2D FFT of images of R x C <= 4096 points in
+// fft_2d_small.hpp -- the whole 2D FFT of images of R x C <= 16384 points in
 // one pass through HBM: a row pass and a column pass would each move every
-// byte once; here a workgroup loads FPI whole images into LDS, transforms
-// their rows and then their columns there, and stores them.
+// byte once; here a workgroup loads FPI whole images into LDS (at most 147 KB
+// for one 16384-point image), transforms their rows and then their columns
+// there, and stores them.  E = 8 elements per thread, 16 for 16384 points.
 //
-// Per image the LDS holds R rows of pitch P = C + C/16 + 1 (odd, so a column
-// read touches distinct banks):
+// Per image the LDS holds R rows of pitch P = C + C/16 + 1 (odd, so that the
+// rows of one column start in different banks):
 //   1. coalesced load of the workgroup's images (64 lanes x 8 contiguous bytes
 //      per instruction), element (r, c) at r*P + c;
 //   2. rows: thread (r, t), t < C/E, takes positions t + (C/E)*m of row r and
@@ -39,7 +40,8 @@ struct Small2D {
     static_assert(C + C / 16 <= P && C * (R + R / 16) <= IMG, "exchange regions fit the image's LDS");
     static_assert(TC <= 64 && TR <= 64 && 64 % TC == 0 && 64 % TR == 0, "a row's / column's threads lie in one wave");
     static_assert(BLOCK <= 1024 && BLOCK % 64 == 0, "whole waves, at most 1024 threads");
-    static_assert(BLOCK == FG_SMALL2D_BLOCK(LR, LC) || LOGE != FG_SMALL2D_LOGE, "the host's launch geometry");
+    static_assert(LOGE == FG_SMALL2D_LOGE(LR, LC) && BLOCK == FG_SMALL2D_BLOCK(LR, LC), "the host's launch geometry");
+    static_assert(FPI * IMG * 8 <= 160 * 1024, "the workgroup's images fit the LDS");
 };
 
 template <int LR, int LC, int LOGE, int FPI, class IO>

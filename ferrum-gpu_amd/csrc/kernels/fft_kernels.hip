@@ -148,7 +148,7 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
 
 // ------------------------------------------------------------ small 2D
 //
-// fg_fft2d_l<LR>_<LC>: the whole 2D FFT of 2^LR x 2^LC images (<= 4096 points)
+// fg_fft2d_l<LR>_<LC>: the whole 2D FFT of 2^LR x 2^LC images (<= 16384 points)
 // in one pass, FG_SMALL2D_FPI images per workgroup (fft_2d_small.hpp).
 #include "fft_2d_small.hpp"
 
@@ -157,7 +157,7 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
         fg_fft2d_l##LR##_##LC(const float2* __restrict__ in, float2* __restrict__ out,              \
                               const float2* __restrict__ tw_rows, const float2* __restrict__ tw_cols, \
                               uint64_t batch, float scale, uint32_t flags) {                         \
-        fft2d_small_body<LR, LC, FG_SMALL2D_LOGE, FG_SMALL2D_FPI(LR, LC)>(InterleavedIO{in, out}, tw_rows, \
+        fft2d_small_body<LR, LC, FG_SMALL2D_LOGE(LR, LC), FG_SMALL2D_FPI(LR, LC)>(InterleavedIO{in, out}, tw_rows, \
                                                                           tw_cols, batch, scale, flags); \
     }
 FG_FFT2D(4, 4)
@@ -165,16 +165,29 @@ FG_FFT2D(4, 5)
 FG_FFT2D(4, 6)
 FG_FFT2D(4, 7)
 FG_FFT2D(4, 8)
+FG_FFT2D(4, 9)
+FG_FFT2D(4, 10)
 FG_FFT2D(5, 4)
 FG_FFT2D(5, 5)
 FG_FFT2D(5, 6)
 FG_FFT2D(5, 7)
+FG_FFT2D(5, 8)
+FG_FFT2D(5, 9)
 FG_FFT2D(6, 4)
 FG_FFT2D(6, 5)
 FG_FFT2D(6, 6)
+FG_FFT2D(6, 7)
+FG_FFT2D(6, 8)
 FG_FFT2D(7, 4)
 FG_FFT2D(7, 5)
+FG_FFT2D(7, 6)
+FG_FFT2D(7, 7)
 FG_FFT2D(8, 4)
+FG_FFT2D(8, 5)
+FG_FFT2D(8, 6)
+FG_FFT2D(9, 4)
+FG_FFT2D(9, 5)
+FG_FFT2D(10, 4)
 
 // ------------------------------------------------------- multi-pass tiles
 //

@@ -28,14 +28,15 @@ typedef struct TileGeom {
     uint32_t remap;         /* 1: XCD-aware tile order (grid a multiple of 8; fft_tile.hpp) */
 } TileGeom;
 
-/* One-pass 2D FFT of images of 2^lr x 2^lc <= 4096 points (fft_2d_small.hpp):
- * 2^FG_SMALL2D_LOGE elements per thread, FG_SMALL2D_FPI(lr, lc) images per
- * workgroup (256 threads, or one image when it needs more). */
-#define FG_SMALL2D_MAX_LOG 12
-#define FG_SMALL2D_LOGE 3
-#define FG_SMALL2D_FPI(lr, lc) \
-    ((((1 << ((lr) + (lc))) >> FG_SMALL2D_LOGE) >= 256) ? 1 : (256 / ((1 << ((lr) + (lc))) >> FG_SMALL2D_LOGE)))
-#define FG_SMALL2D_BLOCK(lr, lc) (FG_SMALL2D_FPI(lr, lc) * ((1 << ((lr) + (lc))) >> FG_SMALL2D_LOGE))
+/* One-pass 2D FFT of images of 2^lr x 2^lc <= 16384 points (fft_2d_small.hpp):
+ * 2^FG_SMALL2D_LOGE(lr, lc) elements per thread (8, or 16 for 16384 points,
+ * so that an image needs at most 1024 threads), FG_SMALL2D_FPI(lr, lc) images
+ * per workgroup (256 threads, or one image when it needs more). */
+#define FG_SMALL2D_MAX_LOG 14
+#define FG_SMALL2D_LOGE(lr, lc) (((lr) + (lc)) >= 14 ? 4 : 3)
+#define FG_SMALL2D_TPI(lr, lc) ((1 << ((lr) + (lc))) >> FG_SMALL2D_LOGE(lr, lc))
+#define FG_SMALL2D_FPI(lr, lc) (FG_SMALL2D_TPI(lr, lc) >= 256 ? 1 : 256 / FG_SMALL2D_TPI(lr, lc))
+#define FG_SMALL2D_BLOCK(lr, lc) (FG_SMALL2D_FPI(lr, lc) * FG_SMALL2D_TPI(lr, lc))
 
 #ifdef __cplusplus
 }  // namespace fg

@@ -25,24 +25,29 @@ import oracle
 from conftest import rel_l2, uniform_c64
 from test_stockham_model import model as stockham_model
 
-LOGE = 3
-MAX_LOG = 12
+MAX_LOG = 14
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def loge(lr, lc):
+    """FG_SMALL2D_LOGE: 8 elements per thread, 16 for 16384-point images."""
+    return 4 if lr + lc >= 14 else 3
 
 
 def fpi(lr, lc):
     """FG_SMALL2D_FPI: images per workgroup (256 threads, or one image)."""
-    t = (1 << (lr + lc)) >> LOGE
+    t = (1 << (lr + lc)) >> loge(lr, lc)
     return 1 if t >= 256 else 256 // t
 
 
 def shapes():
-    return [(lr, lc) for lr in range(4, 9) for lc in range(4, 9) if lr + lc <= MAX_LOG]
+    return [(lr, lc) for lr in range(4, 11) for lc in range(4, 11) if lr + lc <= MAX_LOG]
 
 
 def small2d_model(images, lr, lc):
     """images: (FPI, R, C) complex; returns the kernel's output, checking indices."""
     R, C = 1 << lr, 1 << lc
+    LOGE = loge(lr, lc)
     N, E = R * C, 1 << LOGE
     F = images.shape[0]
     P = C + C // 16 + 1
@@ -90,18 +95,19 @@ def test_small2d_model_matches_oracle(lr, lc):
 @pytest.mark.parametrize("lr,lc", shapes())
 def test_small2d_geometry_fits(lr, lc):
     R, C = 1 << lr, 1 << lc
-    N, E = R * C, 1 << LOGE
+    N, E = R * C, 1 << loge(lr, lc)
     block = fpi(lr, lc) * N // E
     assert block <= 1024 and block % 64 == 0
     tc, tr = C // E, R // E
     assert tc <= 64 and tr <= 64 and 64 % tc == 0 and 64 % tr == 0   # rows / columns within a wave
     lds = fpi(lr, lc) * R * (C + C // 16 + 1) * 8
-    assert lds <= 64 * 1024
+    assert lds <= 160 * 1024
 
 
 def test_small2d_mirror_matches_the_sources():
     geom = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "tile_geom.h")).read()
-    assert re.search(r"#define FG_SMALL2D_LOGE (\d+)", geom).group(1) == str(LOGE)
+    m = re.search(r"#define FG_SMALL2D_LOGE\(lr, lc\) \(\(\(lr\) \+ \(lc\)\) >= (\d+) \? (\d+) : (\d+)\)", geom)
+    assert m and m.groups() == ("14", "4", "3")
     assert re.search(r"#define FG_SMALL2D_MAX_LOG (\d+)", geom).group(1) == str(MAX_LOG)
     hip = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
     inst = {(int(a), int(b)) for a, b in re.findall(r"^FG_FFT2D\((\d+), (\d+)\)", hip, flags=re.M)}

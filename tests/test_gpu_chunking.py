@@ -59,7 +59,7 @@ CASES = [
     (False, 13, 37),
     (False, 16, 64),
     (False, 20, 3),
-    (True, 7, 40),
+    (True, 8, 40),
     (True, 10, 9),
     (True, 11, 3),
 ]

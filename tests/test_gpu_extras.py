@@ -58,19 +58,19 @@ def test_rect_2d_inverse_roundtrip(gpu_device, lr, lc):
     assert rel_l2(back, x) <= TOL
 
 
-SMALL_2D = [(lr, lc) for lr in range(4, 9) for lc in range(4, 9) if lr + lc <= 12]
+SMALL_2D = [(lr, lc) for lr in range(4, 11) for lc in range(4, 11) if lr + lc <= 14]
 
 
 @pytest.mark.parametrize("lr,lc", SMALL_2D)
 def test_one_pass_small_2d_every_shape(gpu_device, lr, lc):
-    """The one-kernel plans (images of up to 4096 points): forward and
+    """The one-kernel plans (images of up to 16384 points): forward and
     normalised inverse, a batch that leaves the last workgroup partly empty,
     out of place and in place."""
     import ferrum_gpu
     from ferrum_gpu.hip import DeviceBuffer
 
     n = 1 << (lr + lc)
-    per_group = max(1, 256 * 8 // n)          # images per workgroup
+    per_group = max(1, 256 * (16 if lr + lc >= 14 else 8) // n)   # images per workgroup
     batch = 2 * per_group + 1
     rng = np.random.default_rng(900 + 16 * lr + lc)
     x = uniform_c64(rng, batch * n).reshape(batch, 1 << lr, 1 << lc)

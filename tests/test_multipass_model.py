@@ -133,8 +133,8 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None):
         return [tile(p, pass_policy(i, len(passes), cached, p["g"]), reads_input=(i == 0))
                 for i, p in enumerate(passes)]
     lc = log_n if log_cols is None else log_cols
-    if log_n + lc <= 12:
-        # images of up to 4096 points: one pass (fg_fft2d_*, test_fft2d_small_model)
+    if log_n + lc <= 14:
+        # images of up to 16384 points: one pass (fg_fft2d_*, test_fft2d_small_model)
         return [f"fg_fft2d_l{log_n}_{lc}"]
     passes = tile_geometry_2d(log_n, 1, lc, cached)
     n = len(passes) + 1
