@@ -5,7 +5,8 @@ Default workload (the one the north-star target is quoted
 on): batched 1D forward C2C complex64 FFT, N = 1024, batch = 65536 (512 MiB in,
 512 MiB out), re/im iid N(0,1) from seed 3, device-resident buffers.
 `--workload` selects the other BASELINE configurations (cfg1, cfg2_256,
-cfg2_4096, cfg4, cfg5) and the operations beside the path (cfg3_split: config 3
+cfg2_4096, cfg4, cfg5), 2D images on the one-pass path (2d_64, 2d_128: 512 MiB
+batches of 64x64 / 128x128 images) and the operations beside the path (cfg3_split: config 3
 in the split layout; cmul, cmul_split, deinterleave, interleave: the pointwise
 kernels over config 3's 2^26 elements; transpose: an 8192 x 8192 complex64
 matrix).
@@ -58,6 +59,10 @@ FFT_WORKLOADS = {
              "1D forward C2C FFT N=2^24 batch=4 complex64, re/im iid N(0,1) seed 4"),
     "cfg5": (2, 12, 2, 5, "uniform", [("forward", False)], "interleaved",
              "2D forward C2C FFT 4096x4096 batch=2 complex64, re/im iid U[-1,1) seed 5"),
+    "2d_64": (2, 6, 16384, 6, "uniform", [("forward", False)], "interleaved",
+              "2D forward C2C FFT 64x64 batch=16384 complex64 (one-pass path), re/im iid U[-1,1) seed 6"),
+    "2d_128": (2, 7, 4096, 7, "uniform", [("forward", False)], "interleaved",
+               "2D forward C2C FFT 128x128 batch=4096 complex64 (one-pass path), re/im iid U[-1,1) seed 7"),
     "cfg3_split": (1, 10, 65536, 3, "normal", [("forward", False)], "split",
                    "1D forward C2C FFT N=1024 batch=65536, split layout (re, im f32 arrays), "
                    "re/im iid N(0,1) seed 3"),
