@@ -36,8 +36,10 @@ struct StockhamShape {
     static_assert(LOGE <= LOGN, "more elements per thread than points");
 };
 
-// Padded LDS slot of logical position p.
-__device__ __forceinline__ int lds_pos(int p) { return p + (p >> 4); }
+// Padded LDS slot of logical position p: one pad slot per 2^SH positions
+// (16 unless a caller's bank pattern wants another spacing).
+template <int SH = 4>
+__device__ __forceinline__ int lds_pos(int p) { return p + (p >> SH); }
 
 // Stage twiddle table, built by the host for this radix list (stage 0 has no
 // block).  The block of stage s (radix R, L = product of earlier radices,
@@ -137,49 +139,53 @@ __device__ __forceinline__ int stockham_dst(int t, int i, int q) {
 }
 
 // LDS addresses as a per-thread base plus compile-time offsets, using
-// lds_pos(a + 16c) = lds_pos(a) + 17c: the gather of position t + T*m and the
-// scatter of output q of butterfly i then need no per-element index
-// arithmetic (ds_read/ds_write take the offset as an immediate).
-template <int LOGN, int LOGE>
+// lds_pos(a + K*c) = lds_pos(a) + (K+1)*c for K = 2^SH: the gather of position
+// t + T*m and the scatter of output q of butterfly i then need no per-element
+// index arithmetic (ds_read/ds_write take the offset as an immediate).
+template <int LOGN, int LOGE, int SH = 4>
 __device__ __forceinline__ void lds_gather(float2* x, const float2* __restrict__ lds, int t) {
     using Sh = StockhamShape<LOGN, LOGE>;
-    if constexpr (Sh::T % 16 == 0) {
-        const float2* base = lds + lds_pos(t);
+    constexpr int K = 1 << SH;
+    if constexpr (Sh::T % K == 0) {
+        const float2* base = lds + lds_pos<SH>(t);
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = base[m * (Sh::T + Sh::T / 16)];
+        for (int m = 0; m < Sh::E; ++m) x[m] = base[m * (Sh::T + Sh::T / K)];
     } else {
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = lds[lds_pos(t + Sh::T * m)];
+        for (int m = 0; m < Sh::E; ++m) x[m] = lds[lds_pos<SH>(t + Sh::T * m)];
     }
 }
 
-template <int LOGN, int LOGE, int S>
+template <int LOGN, int LOGE, int S, int SH = 4>
 __device__ __forceinline__ void lds_scatter(const float2* x, float2* __restrict__ lds, int t) {
     using Sh = StockhamShape<LOGN, LOGE>;
     constexpr int LOGR = (S < Sh::NFULL) ? LOGE : Sh::REM;
     constexpr int NB = Sh::E >> LOGR;
     constexpr int R = 1 << LOGR;
     constexpr int L = 1 << (S * LOGE);
+    constexpr int K = 1 << SH;
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-        if constexpr (L == 1 && R == 16) {
-            // dst = 16*b + q, q < 16  ->  lds_pos = 17*b + q
-            float2* base = lds + 17 * (t + Sh::T * i);
+        if constexpr (L == 1 && R == K) {
+            // dst = K*b + q, q < K  ->  lds_pos = (K+1)*b + q
+            float2* base = lds + (K + 1) * (t + Sh::T * i);
 #pragma unroll
             for (int q = 0; q < R; ++q) base[q] = x[i + NB * q];
-        } else if constexpr (L % 16 == 0) {
-            // dst = (j*L*R + k) + q*L with L a multiple of 16
-            float2* base = lds + lds_pos(stockham_dst<LOGN, LOGE, S>(t, i, 0));
+        } else if constexpr (L % K == 0) {
+            // dst = (j*L*R + k) + q*L with L a multiple of K
+            float2* base = lds + lds_pos<SH>(stockham_dst<LOGN, LOGE, S>(t, i, 0));
 #pragma unroll
-            for (int q = 0; q < R; ++q) base[q * (L + L / 16)] = x[i + NB * q];
+            for (int q = 0; q < R; ++q) base[q * (L + L / K)] = x[i + NB * q];
         } else {
 #pragma unroll
-            for (int q = 0; q < R; ++q) lds[lds_pos(stockham_dst<LOGN, LOGE, S>(t, i, q))] = x[i + NB * q];
+            for (int q = 0; q < R; ++q) lds[lds_pos<SH>(stockham_dst<LOGN, LOGE, S>(t, i, q))] = x[i + NB * q];
         }
     }
 }
 
-template <int LOGN, int LOGE, int S>
+// SH: the exchanges' padding (lds_pos<SH>); the exchange buffer holds
+// N + N/2^SH positions.
+template <int LOGN, int LOGE, int S, int SH = 4>
 struct StockhamStages {
     using Sh = StockhamShape<LOGN, LOGE>;
     // Runs stage S (already gathered in x) and every later stage.
@@ -188,13 +194,13 @@ struct StockhamStages {
                                                float2* __restrict__ lds) {
         stockham_stage_regs<LOGN, LOGE, S>(x, t, tw);
         if constexpr (S + 1 < Sh::NSTAGES) {
-            lds_scatter<LOGN, LOGE, S>(x, lds, t);
+            lds_scatter<LOGN, LOGE, S, SH>(x, lds, t);
             if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
-            lds_gather<LOGN, LOGE>(x, lds, t);
+            lds_gather<LOGN, LOGE, SH>(x, lds, t);
             if constexpr (S + 2 < Sh::NSTAGES) {
                 if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
             }
-            StockhamStages<LOGN, LOGE, S + 1>::template run<ONE_WAVE>(x, t, tw, lds);
+            StockhamStages<LOGN, LOGE, S + 1, SH>::template run<ONE_WAVE>(x, t, tw, lds);
         }
     }
 };
@@ -236,11 +242,11 @@ __device__ __forceinline__ void fft_stockham_body(const IO io, const float2* __r
             const int fs = e >> LOGN;
             float2 v = make_float2(0.f, 0.f);
             if (f0 + fs < batch) v = io.load(f0 * Sh::N + e);
-            lds_all[fs][lds_pos(e & (Sh::N - 1))] = v;
+            lds_all[fs][lds_pos<>(e & (Sh::N - 1))] = v;
         }
         if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
 #pragma unroll
-        for (int m = 0; m < Sh::E; ++m) x[m] = lds_all[slot][lds_pos(t + Sh::T * m)];
+        for (int m = 0; m < Sh::E; ++m) x[m] = lds_all[slot][lds_pos<>(t + Sh::T * m)];
         if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
     } else if (valid) {
 #pragma unroll
@@ -260,14 +266,14 @@ __device__ __forceinline__ void fft_stockham_body(const IO io, const float2* __r
         for (int m = 0; m < Sh::E; ++m) {
             float2 v = x[m];
             if (cs) v = cscale(cconj(v), scale);
-            lds_all[slot][lds_pos(t + Sh::T * m)] = v;
+            lds_all[slot][lds_pos<>(t + Sh::T * m)] = v;
         }
         if constexpr (ONE_WAVE) wave_sync(); else __syncthreads();
 #pragma unroll
         for (int j = 0; j < Sh::E; ++j) {
             const int e = tid + BLOCK * j;
             const int fs = e >> LOGN;
-            if (f0 + fs < batch) io.store(f0 * Sh::N + e, lds_all[fs][lds_pos(e & (Sh::N - 1))]);
+            if (f0 + fs < batch) io.store(f0 * Sh::N + e, lds_all[fs][lds_pos<>(e & (Sh::N - 1))]);
         }
     } else if (valid) {
 #pragma unroll

@@ -64,7 +64,7 @@ struct TileLayout {
     static constexpr int N = 1 << LOGL;
     static constexpr int ELEMS = PADPOS ? (N + N / 16) * G : N * (G + 1);
     __device__ __forceinline__ static int at(int pos, int c) {
-        if constexpr (PADPOS) return lds_pos(pos) * G + c;
+        if constexpr (PADPOS) return lds_pos<>(pos) * G + c;
         else return pos * (G + 1) + c;
     }
     // at(pos + D, c) - at(pos, c) for a step D that is a multiple of 16 (any D

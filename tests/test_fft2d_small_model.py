@@ -2,15 +2,17 @@
 ferrum-gpu_amd/csrc/kernels/fft_2d_small.hpp), checked against the oracle
 before any launch.
 
-Per image the workgroup's LDS holds R rows of pitch P = C + C/16 + 1.  The
-model replays the kernel's index bookkeeping: the coalesced load and store
-cover the workgroup's FPI images exactly once, each row's Stockham exchanges
-stay in its own P slots and each column's in its own R + R/16 slots of the
-image, all inside the image, and the data flow (rows, then columns, each by
-the Stockham model of tests/test_stockham_model.py, which checks the
-exchanges' own indices) gives the 2D DFT.  The host's launch geometry
-(FG_SMALL2D_* in kernels/tile_geom.h) is mirrored here and checked against
-the sources.
+Per image the workgroup's LDS holds R rows of pitch P; the column exchanges
+use regions of CP slots (both from the shape's Small2DLayout, read from the
+header).  The model replays the kernel's index bookkeeping: the coalesced load
+and store cover the workgroup's FPI images exactly once, both lane orders
+give every (line, thread) pair once and keep a line's threads in one wave,
+each row's Stockham exchanges stay in its own P slots and each column's in its
+own CP slots of the image, all inside the image, and the data flow (rows, then
+columns, each by the Stockham model of tests/test_stockham_model.py, which
+checks the exchanges' own indices) gives the 2D DFT.  The host's launch
+geometry (FG_SMALL2D_* in kernels/tile_geom.h) is mirrored here and checked
+against the sources.
 """
 
 from __future__ import annotations
@@ -27,6 +29,38 @@ from test_stockham_model import model as stockham_model
 
 MAX_LOG = 14
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def layouts():
+    """small2d_layout's table: (lr, lc) -> (dp, dc, shr, shc, row_tm, col_tm)."""
+    src = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_2d_small.hpp")).read()
+    pat = r"case (\d+) \* 16 \+ (\d+): return \{(\d+), (\d+), (\d+), (\d+), (true|false), (true|false)\};"
+    tab = {}
+    for m in re.finditer(pat, src):
+        g = m.groups()
+        tab[(int(g[0]), int(g[1]))] = tuple(int(v) for v in g[2:6]) + (g[6] == "true", g[7] == "true")
+    assert "default: return {1, 0, 4, 4, false, false};" in src
+    return tab
+
+
+LAYOUTS = layouts()
+
+
+def layout(lr, lc):
+    dp, dc, shr, shc, row_tm, col_tm = LAYOUTS.get((lr, lc), (1, 0, 4, 4, False, False))
+    R, C = 1 << lr, 1 << lc
+    return dict(P=C + (C >> shr) + dp, CP=R + (R >> shc) + dc, shr=shr, shc=shc, row_tm=row_tm, col_tm=col_tm)
+
+
+def lanes(timg, threads_per_line, thread_major):
+    """The kernel's (line, thread) of each local thread id."""
+    local = np.arange(timg)
+    k = min(64, timg)
+    part, l = local // k, local % k
+    per = k // threads_per_line
+    if thread_major:
+        return part * per + l % per, l // per
+    return part * per + l // threads_per_line, l % threads_per_line
 
 
 def loge(lr, lc):
@@ -50,7 +84,8 @@ def small2d_model(images, lr, lc):
     LOGE = loge(lr, lc)
     N, E = R * C, 1 << LOGE
     F = images.shape[0]
-    P = C + C // 16 + 1
+    lay = layout(lr, lc)
+    P, CP = lay["P"], lay["CP"]
     IMG = R * P
     block = F * (N // E)
     # 1. load: e = tid + BLOCK*j -> LDS is*IMG + r*P + c
@@ -64,16 +99,16 @@ def small2d_model(images, lr, lc):
     out = np.empty((F, R, C), np.complex128)
     for s in range(F):
         img = lds[s * IMG:(s + 1) * IMG]
-        # 2. rows: row r's exchanges in [r*P, r*P + C + C/16)
-        assert C + C // 16 <= P and (R - 1) * P + C + C // 16 <= IMG
+        # 2. rows: row r's exchanges in [r*P, r*P + C + C/2^shr)
+        assert C + (C >> lay["shr"]) <= P and (R - 1) * P + C + (C >> lay["shr"]) <= IMG
         rows = np.stack([img[r * P:r * P + C] for r in range(R)])
-        rows = stockham_model(rows.reshape(-1), lc, LOGE).reshape(R, C)
+        rows = stockham_model(rows.reshape(-1), lc, LOGE, lay["shr"]).reshape(R, C)
         for r in range(R):
             img[r * P:r * P + C] = rows[r]
-        # 3. columns: column c read at k*P + c; its exchanges in [c*(R + R/16), (c+1)*(R + R/16))
+        # 3. columns: column c read at k*P + c; its exchanges in [c*CP, c*CP + R + R/2^shc)
         cols = np.stack([img[np.arange(R) * P + c] for c in range(C)])
-        assert C * (R + R // 16) <= IMG
-        cols = stockham_model(cols.reshape(-1), lr, LOGE).reshape(C, R)
+        assert R + (R >> lay["shc"]) <= CP and C * CP <= IMG
+        cols = stockham_model(cols.reshape(-1), lr, LOGE, lay["shc"]).reshape(C, R)
         for c in range(C):
             img[np.arange(R) * P + c] = cols[c]
         out[s] = np.stack([img[r * P:r * P + C] for r in range(R)])
@@ -100,8 +135,17 @@ def test_small2d_geometry_fits(lr, lc):
     assert block <= 1024 and block % 64 == 0
     tc, tr = C // E, R // E
     assert tc <= 64 and tr <= 64 and 64 % tc == 0 and 64 % tr == 0   # rows / columns within a wave
-    lds = fpi(lr, lc) * R * (C + C // 16 + 1) * 8
+    lay = layout(lr, lc)
+    lds = fpi(lr, lc) * R * lay["P"] * 8
     assert lds <= 160 * 1024
+    timg = N // E
+    for tpl, tm, lines in ((tc, lay["row_tm"], R), (tr, lay["col_tm"], C)):
+        line, t = lanes(timg, tpl, tm)
+        assert np.array_equal(np.sort(line * tpl + t), np.arange(timg))   # every (line, thread) once
+        assert line.max() == lines - 1
+        wave = np.arange(timg) // 64
+        for ln in range(lines):                                         # a line's threads in one wave
+            assert len(set(wave[line == ln])) == 1
 
 
 def test_small2d_mirror_matches_the_sources():

@@ -62,11 +62,12 @@ def stage_twiddles(tw, off, k, r):
     return np.stack(cols, axis=1)
 
 
-def lds_pos(p):
-    return p + (p >> 4)
+def lds_pos(p, sh=4):
+    return p + (p >> sh)
 
 
-def model(x, log_n, log_e):
+def model(x, log_n, log_e, sh=4):
+    """sh: the exchanges' padding, one slot per 2**sh positions (lds_pos<SH>)."""
     n, e = 1 << log_n, 1 << log_e
     t_per = n // e
     nfull, rem = divmod(log_n, log_e)
@@ -75,7 +76,7 @@ def model(x, log_n, log_e):
     lanes = x.reshape(-1, n)
     t = np.arange(t_per)
     regs = lanes[:, t[:, None] + t_per * np.arange(e)[None, :]]   # regs[b, t, m] = x[t + T m]
-    lds_elems = n + n // 16
+    lds_elems = n + (n >> sh)
     for s, logr in enumerate(logrs):
         r = 1 << logr
         nb = e // r
@@ -99,9 +100,9 @@ def model(x, log_n, log_e):
         assert np.array_equal(np.sort(dst_pos.reshape(-1)), np.arange(n))
         if s + 1 < len(logrs):
             lds = np.zeros((lanes.shape[0], lds_elems), np.complex128)
-            assert lds_pos(dst_pos).max() < lds_elems
-            lds[:, lds_pos(dst_pos)] = new
-            gather = lds_pos(t[:, None] + t_per * np.arange(e)[None, :])
+            assert lds_pos(dst_pos, sh).max() < lds_elems
+            lds[:, lds_pos(dst_pos, sh)] = new
+            gather = lds_pos(t[:, None] + t_per * np.arange(e)[None, :], sh)
             assert gather.max() < lds_elems
             regs = lds[:, gather]
         else:
