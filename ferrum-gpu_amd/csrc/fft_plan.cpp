@@ -405,6 +405,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         s.per_unit = 1;
         p->steps_.push_back(s);
         p->main_kernel_ = s.name;
+        p->split_fn_ = HipBackend::get_kernel(mod, (s.name + "_split").c_str());
         p->pw_ = Pointwise(mod);
         return p;
     }
@@ -593,8 +594,14 @@ void FftPlan::exec_split(const void* in_re, const void* in_im, void* out_re, voi
         float sc = scale_for(dir, normalize);
         const void* tw = s.tw;
         uint64_t count = s.per_unit * batch_;
-        void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, &count, &sc, &flags};
         const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
+        if (s.small2d) {
+            const void* twc = s.tw_cols;
+            void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, (void*)&twc, &count, &sc, &flags};
+            HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
+            return;
+        }
+        void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, &count, &sc, &flags};
         HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
         return;
     }

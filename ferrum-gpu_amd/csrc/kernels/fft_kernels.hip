@@ -148,7 +148,7 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
 
 // ------------------------------------------------------------ small 2D
 //
-// fg_fft2d_l<LR>_<LC>: the whole 2D FFT of 2^LR x 2^LC images (<= 16384 points)
+// fg_fft2d_l<LR>_<LC>[_split]: the whole 2D FFT of 2^LR x 2^LC images (<= 16384 points)
 // in one pass, FG_SMALL2D_FPI images per workgroup (fft_2d_small.hpp).
 #include "fft_2d_small.hpp"
 
@@ -159,6 +159,15 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
                               uint64_t batch, float scale, uint32_t flags) {                         \
         fft2d_small_body<LR, LC, FG_SMALL2D_LOGE(LR, LC), FG_SMALL2D_FPI(LR, LC)>(InterleavedIO{in, out}, tw_rows, \
                                                                           tw_cols, batch, scale, flags); \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(FG_SMALL2D_BLOCK(LR, LC)) void                           \
+        fg_fft2d_l##LR##_##LC##_split(const float* __restrict__ in_re, const float* __restrict__ in_im, \
+                                      float* __restrict__ out_re, float* __restrict__ out_im,        \
+                                      const float2* __restrict__ tw_rows,                             \
+                                      const float2* __restrict__ tw_cols, uint64_t batch, float scale, \
+                                      uint32_t flags) {                                               \
+        fft2d_small_body<LR, LC, FG_SMALL2D_LOGE(LR, LC), FG_SMALL2D_FPI(LR, LC)>(                    \
+            SplitIO{in_re, in_im, out_re, out_im}, tw_rows, tw_cols, batch, scale, flags);            \
     }
 FG_FFT2D(4, 4)
 FG_FFT2D(4, 5)

@@ -248,8 +248,9 @@ FG_API int fg_transpose_c64(fg_device_t dev, const void *d_in, void *d_out, uint
  * crates/ferrum-gpu-fft-kernels/src/kernels_body.rs:509-626, 986-1130,
  * 1463-1610, for every plan).  Same results as fg_fft_exec on the interleaved
  * data.  d_out_re / d_out_im may equal d_in_re / d_in_im; no other overlap.
- * Single-pass plans (1D, N <= 4096) run one launch; other plans stage through
- * an interleaved buffer the plan allocates at its first split call.
+ * Single-pass plans (1D, N <= 4096; 2D images of up to 16384 points) run one
+ * launch; other plans stage through an interleaved buffer the plan allocates
+ * at its first split call.
  * Stream-ordered, asynchronous. */
 FG_API int fg_fft_exec_split(fg_fft_plan_t plan, const void *d_in_re, const void *d_in_im,
                              void *d_out_re, void *d_out_im, int direction, int normalize,

@@ -91,7 +91,7 @@ def test_split_1d_equals_interleaved(gpu_device, log_n):
     assert rel_l2(split_i, x) <= TOL
 
 
-@pytest.mark.parametrize("lr,lc", [(8, 8), (12, 12), (5, 9), (11, 4)])
+@pytest.mark.parametrize("lr,lc", [(8, 8), (12, 12), (5, 9), (11, 4), (4, 4), (6, 6), (7, 7), (10, 4), (4, 8)])
 def test_split_2d_equals_interleaved(gpu_device, lr, lc):
     import ferrum_gpu
 
@@ -116,6 +116,20 @@ def test_split_in_place(gpu_device, log_n):
     plan.execute_split(re, im, re, im)
     got = (d.get(re, x.size, np.float32) + 1j * d.get(im, x.size, np.float32)).astype(np.complex64)
     assert rel_l2(got, oracle.fft_1d(x, log_n, threads=8)) <= TOL
+
+
+def test_split_2d_one_pass_in_place(gpu_device):
+    import ferrum_gpu
+
+    batch = 5
+    x = uniform_c64(np.random.default_rng(77), batch << 12)
+    plan = ferrum_gpu.fft.Plan2D(6, batch, gpu_device)
+    assert plan.kernel_names() == ["fg_fft2d_l6_6"]
+    d = Dev(gpu_device)
+    re, im = d.put(np.ascontiguousarray(x.real)), d.put(np.ascontiguousarray(x.imag))
+    plan.execute_split(re, im, re, im, "inverse", True)
+    got = (d.get(re, x.size, np.float32) + 1j * d.get(im, x.size, np.float32)).astype(np.complex64)
+    assert rel_l2(got, oracle.fft_2d(x, 6, "inverse", True)) <= TOL
 
 
 def test_split_rejects_crossed_parts(gpu_device):

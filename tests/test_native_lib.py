@@ -78,7 +78,8 @@ def instantiated_kernels():
         # cache policies (FG_TILE_P): all four, or _cc alone for narrow tiles
         names |= {base + "_cc"} if m.group(1) else {base + pol for pol in ("", "_sc", "_cc", "_cs")}
     # one-pass 2D FFTs of small images
-    names |= {f"fg_fft2d_l{a}_{b}" for a, b in re.findall(r"^FG_FFT2D\((\d+), (\d+)\)", src, flags=re.M)}
+    for a, b in re.findall(r"^FG_FFT2D\((\d+), (\d+)\)", src, flags=re.M):
+        names |= {f"fg_fft2d_l{a}_{b}", f"fg_fft2d_l{a}_{b}_split"}
     # first-pass tiles with the exchanges in halves: unchunked and _sc
     for m in re.finditer(r"^FG_TILE_HALVES\((\d+), (\d+)\)", src, flags=re.M):
         names |= {f"fg_tile_l{m.group(1)}_g{m.group(2)}_h{pol}" for pol in ("", "_sc")}
@@ -98,6 +99,8 @@ def planned_kernels():
         for lr in range(4, 13):
             for lc in range(4, 13):
                 names |= set(plan_kernel_names(True, lr, cached, lc))
+                if lr + lc <= 14:   # one-pass images: exec_split's twin
+                    names.add(f"fg_fft2d_l{lr}_{lc}_split")
     return names
 
 
