@@ -33,7 +33,7 @@ namespace fg {
 // (thread-major).  Chosen per shape so that the 16 lanes that share an LDS
 // cycle of a 64-bit access hit distinct banks in every phase (a CPU model of
 // 32 four-byte banks, which reproduces the conflict rates rocprof measured on
-// the first layout, the default below).
+// the first layout, the default below; tests/test_fft2d_small_banks.py).
 struct Small2DLayout {
     int dp, dc, shr, shc;
     bool row_tm, col_tm;
