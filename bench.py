@@ -12,8 +12,10 @@ kernels over config 3's 2^26 elements; transpose: an 8192 x 8192 complex64
 matrix).
 
 A "step" is one pass of the workload over its batch (for cfg2: the forward and
-the normalised inverse transform).  W untimed warmup steps, then K timed steps
-between two device synchronisations.  Every kernel launch of the timed steps
+the normalised inverse transform).  A clock ramp (--ramp-ms of plain copy
+kernels, not workload steps), W untimed warmup steps, then K timed steps
+between two device synchronisations; `steady_state` compares the first and
+last quarter of the timed launches, so a run still on a rising clock shows.  Every kernel launch of the timed steps
 is followed by a HIP event recorded on the stream it runs on (plus one event
 before the first), which gives each kernel's duration for the roofline.  With
 --graph G the steps are recorded G at a time into a HIP graph and the timed
@@ -546,6 +548,44 @@ def cpu_baseline(np, wl, gpu_out, budget_s: float):
     return base, multi_d, err
 
 
+def clock_ramp(N, dev, wl, stream, ramp_ms: float):
+    """Plain copy kernels over the workload's own buffers for ramp_ms of wall
+    time, before the warmup steps: the shader clock idles low and needs tens of
+    milliseconds of work to rise, which a short warmup does not give.  Not a
+    step of the workload and not timed; reported in the JSON line."""
+    if ramp_ms <= 0:
+        return None
+    src, dst, nbytes = wl.copy_bufs
+    nbytes = min(nbytes, 256 << 20)
+    t0 = time.perf_counter()
+    copies = 0
+    while (time.perf_counter() - t0) * 1e3 < ramp_ms:
+        for _ in range(8):
+            N.check(N.lib.fg_stream_copy(dev.handle, src._p, dst._p, nbytes, stream))
+        copies += 8
+        dev.sync()
+    return {"kernel": "fg_copy_f4", "copies": copies, "bytes_per_copy": nbytes,
+            "ms": round((time.perf_counter() - t0) * 1e3, 1),
+            "note": "untimed plain-copy launches before the warmup steps (clock ramp), not workload steps"}
+
+
+def steady_state(np, per_kernel, dominant_key: str, graph: bool):
+    """Whether the timed launches ran at a steady clock: the median duration of
+    the dominant kernel's first quarter of timed launches against its last
+    quarter (a ratio well above 1 means the first timed steps still ran on a
+    rising clock)."""
+    v = per_kernel[dominant_key]
+    if graph or len(v) < 8:
+        return {"launches": len(v), "note": "too few per-launch timings to compare quarters" if not graph
+                else "graph replays are timed as a whole"}
+    q = len(v) // 4
+    first, last = float(np.median(v[:q])), float(np.median(v[-q:]))
+    ratio = first / last if last > 0 else None
+    return {"launches": len(v), "first_quarter_median_ms": round(first, 5),
+            "last_quarter_median_ms": round(last, 5), "ratio": None if ratio is None else round(ratio, 4),
+            "pre_ramp": bool(ratio is not None and ratio > 1.02)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -558,6 +598,9 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of single-thread CPU timing")
     ap.add_argument("--no-host-path", action="store_true",
                     help="skip timing the host-array entry points (PCIe-inclusive)")
+    ap.add_argument("--ramp-ms", type=float, default=40.0,
+                    help="before the warmup steps, run the plain copy kernel for this long (wall ms) so "
+                         "that the shader clock leaves its idle level; reported as clock_ramp, 0 = off")
     ap.add_argument("--graph", type=int, default=0, metavar="G",
                     help="record G steps into one HIP graph and time replays of it (for launch-bound "
                          "workloads); --steps must be a multiple of G.  0: one host launch per kernel")
@@ -590,6 +633,9 @@ def main() -> int:
 
     per_kernel: dict[str, list[float]] = {}
     clocks = ClockSampler()
+    ramp = clock_ramp(N, dev, wl, stream, args.ramp_ms)
+    if ramp:
+        log(f"clock ramp: {ramp['copies']} copy launches in {ramp['ms']} ms")
     if not args.graph:
         for _ in range(args.warmup):
             wl.run(stream)
@@ -643,6 +689,8 @@ def main() -> int:
         for key in wl.launch_keys:
             per_kernel.setdefault(key, []).extend([per_launch] * args.steps)
         graph.destroy()
+    steady = steady_state(np, per_kernel, dominant_key=max(per_kernel, key=lambda k: sum(per_kernel[k])),
+                          graph=bool(args.graph))
     kernel_ms = {key: float(np.mean(v)) for key, v in per_kernel.items()}
     kernel_med = {key: float(np.median(v)) for key, v in per_kernel.items()}
     dominant = max(kernel_ms, key=lambda key: kernel_ms[key] * len(per_kernel[key]))
@@ -721,6 +769,8 @@ def main() -> int:
         ("max_abs_diff_vs_cpu" if wl.exact else "rel_l2_vs_cpu"): err,
         "device": info,
         "gpu_clocks": clocks.report(),
+        "clock_ramp": ramp,
+        "steady_state": steady,
     }
     if args.graph:
         result["launch_mode"] = f"HIP graph of {args.graph} steps per replay"

@@ -62,6 +62,9 @@ struct fg_kernel {
 struct fg_event {
     hipEvent_t ev = nullptr;
     int ordinal = 0;
+    // The device's default stream, where a NULL stream records (as NULL means
+    // that stream for launches and copies); the handle keeps it alive.
+    HipBackend::DeviceHandle dev;
 };
 
 struct fg_fft_plan {
@@ -420,6 +423,7 @@ int fg_event_create(fg_device_t dev, fg_event_t* out) {
         HipBackend::bind(dev->dev->handle());
         std::unique_ptr<fg_event> e(new fg_event);
         e->ordinal = dev->dev->handle()->ordinal;
+        e->dev = dev->dev->handle();
         fg::hip_check(hipEventCreate(&e->ev), "hipEventCreate");
         *out = e.release();
     });
@@ -438,7 +442,8 @@ int fg_event_record(fg_event_t ev, fg_stream_t stream) {
     return guarded([&] {
         need(ev, "event");
         fg::hip_check(hipSetDevice(ev->ordinal), "hipSetDevice");
-        fg::hip_check(hipEventRecord(ev->ev, (hipStream_t)stream), "hipEventRecord");
+        const hipStream_t s = stream ? (hipStream_t)stream : HipBackend::default_stream(ev->dev);
+        fg::hip_check(hipEventRecord(ev->ev, s), "hipEventRecord");
     });
 }
 
@@ -724,7 +729,7 @@ int fg_transpose_c64(fg_device_t dev, const void* d_in, void* d_out, uint32_t ro
                      fg_stream_t stream) {
     return guarded([&] {
         need(dev, "device");
-        fg::transpose_c64(*dev->dev, dev->fft_module, d_in, d_out, rows, cols, batch, (hipStream_t)stream);
+        dev->pointwise.transpose_c64(dev->dev->handle(), d_in, d_out, rows, cols, batch, (hipStream_t)stream);
     });
 }
 
@@ -776,25 +781,7 @@ int fg_stream_copy(fg_device_t dev, const void* d_in, void* d_out, size_t bytes,
         need(dev, "device");
         need(d_in, "d_in");
         need(d_out, "d_out");
-        if (bytes % 16) fg::invalid("fg_stream_copy: bytes must be a multiple of 16");
-        if ((reinterpret_cast<uintptr_t>(d_in) | reinterpret_cast<uintptr_t>(d_out)) & 15)
-            fg::invalid("fg_stream_copy: d_in and d_out must be 16-byte aligned");
-        static thread_local HipBackend::KernelHandle k = nullptr;
-        static thread_local const void* k_mod = nullptr;
-        if (!k || k_mod != dev->fft_module.get()) {
-            k = HipBackend::get_kernel(dev->fft_module, "fg_copy_f4");
-            k_mod = dev->fft_module.get();
-        }
-        uint64_t n4 = bytes / 16;
-        const uint32_t block = 64;
-        uint64_t blocks = (n4 + block - 1) / block;
-        if (blocks > 0x7fffffffull) blocks = 0x7fffffffull;  // the kernel strides beyond this
-        if (blocks == 0) return;
-        const void* src = d_in;
-        void* dst = d_out;
-        void* args[] = {(void*)&src, &dst, &n4};
-        HipBackend::launch(dev->dev->handle(), (hipStream_t)stream, k, fg::Dim3((uint32_t)blocks),
-                           fg::Dim3(block), 0, args);
+        dev->pointwise.stream_copy(dev->dev->handle(), d_in, d_out, bytes, (hipStream_t)stream);
     });
 }
 

@@ -468,27 +468,6 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     return p;
 }
 
-void transpose_c64(HipDevice& dev, const HipBackend::Module& mod, const void* in, void* out, uint32_t rows,
-                   uint32_t cols, size_t batch, hipStream_t stream) {
-    if (!in || !out) invalid("transpose: null buffer");
-    if (in == out) invalid("transpose: in and out must not alias");
-    if (rows == 0 || cols == 0 || batch == 0) invalid("transpose: rows, cols and batch must be positive");
-    const uint32_t tc = (cols + 63) / 64, tr = (rows + 63) / 64;
-    const uint64_t tiles = (uint64_t)tc * tr * batch;
-    if (tiles > 0x7fffffffull) invalid("transpose: too many tiles for one launch");
-    static thread_local const void* cached_mod = nullptr;
-    static thread_local HipBackend::KernelHandle k = nullptr;
-    if (!k || cached_mod != mod.get()) {
-        k = HipBackend::get_kernel(mod, "fg_transpose_c64");
-        cached_mod = mod.get();
-    }
-    const void* src = in;
-    void* dst = out;
-    uint32_t r = rows, c = cols, a = tc, b = tr;
-    void* args[] = {(void*)&src, &dst, &r, &c, &a, &b};
-    HipBackend::launch(dev.handle(), stream, k, Dim3((uint32_t)tiles), Dim3(256), 0, args);
-}
-
 std::vector<std::string> FftPlan::kernel_names() const {
     std::vector<std::string> v;
     for (size_t c = 0; c < chunks(); ++c)
@@ -607,7 +586,18 @@ void FftPlan::exec_split(const void* in_re, const void* in_im, void* out_re, voi
     }
     {
         std::lock_guard<std::mutex> lock(stage_mu_);
-        if (!stage_.data()) stage_ = dev_->alloc<Cf32>(n);
+        if (!stage_.data()) {
+            // The allocation is hipMalloc + hipMemsetAsync + a stream sync
+            // (alloc_zeros is synchronous by contract, backend.rs:30-33), none of
+            // which a stream capture can record: refuse before touching HIP.
+            hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+            hip_check(hipStreamIsCapturing(stream ? stream : dev_->default_stream(), &status),
+                      "hipStreamIsCapturing");
+            if (status != hipStreamCaptureStatusNone)
+                invalid("fft exec_split: the first split-layout execution of a multi-launch plan allocates its "
+                        "staging buffer, which a stream capture cannot record; run it once before capturing");
+            stage_ = dev_->alloc<Cf32>(n);
+        }
     }
     pw_.interleave(dev_->handle(), in_re, in_im, stage_.data(), n, stream);
     exec(stage_.data(), stage_.data(), dir, normalize, stream);

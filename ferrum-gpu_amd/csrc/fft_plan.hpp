@@ -179,8 +179,5 @@ size_t chunk_units_for(uint64_t unit_bytes, size_t batch, size_t limit, bool* ca
 // Whether a single-pass plan of `count` transforms of 2^log_n points runs the
 // latency geometry (fg_fft_n<L>_lat) on a device with `cu_count` CUs.
 bool use_latency_geometry(uint32_t log_n, uint64_t count, int cu_count);
-// Launch the tiled transpose out[b][c][r] = in[b][r][c] on `stream`.
-void transpose_c64(HipDevice& dev, const HipBackend::Module& mod, const void* in, void* out, uint32_t rows,
-                   uint32_t cols, size_t batch, hipStream_t stream);
 
 }  // namespace fg

@@ -49,6 +49,8 @@ Pointwise::Pointwise(const HipBackend::Module& mod) {
         interleave_[v] = HipBackend::get_kernel(mod, ("fg_interleave_c64" + w).c_str());
     }
     fill_ = HipBackend::get_kernel(mod, "fg_fill_c64");
+    transpose_ = HipBackend::get_kernel(mod, "fg_transpose_c64");
+    copy_ = HipBackend::get_kernel(mod, "fg_copy_f4");
 }
 
 void Pointwise::cmul_c64(const HipBackend::DeviceHandle& dev, const void* a, const void* b, void* out, uint64_t n,
@@ -115,6 +117,33 @@ void Pointwise::fill_c64(const HipBackend::DeviceHandle& dev, void* out, uint64_
     uint32_t nrm = normal ? 1u : 0u;
     void* args[] = {&out, &n, &seed, &nrm};
     launch(dev, stream, fill_, n, 1, args);
+}
+
+void Pointwise::transpose_c64(const HipBackend::DeviceHandle& dev, const void* in, void* out, uint32_t rows,
+                              uint32_t cols, uint64_t batch, hipStream_t stream) const {
+    if (!in || !out) invalid("transpose: null buffer");
+    if (rows == 0 || cols == 0 || batch == 0) invalid("transpose: rows, cols and batch must be positive");
+    const uint64_t nb = 8ull * rows * cols * batch;
+    if (overlap(in, nb, out, nb)) invalid("transpose: in and out must not overlap");
+    const uint32_t tc = (cols + 63) / 64, tr = (rows + 63) / 64;
+    const uint64_t tiles = (uint64_t)tc * tr * batch;
+    if (tiles > 0x7fffffffull) invalid("transpose: too many tiles for one launch");
+    void* args[] = {(void*)&in, &out, &rows, &cols, (void*)&tc, (void*)&tr};
+    HipBackend::launch(dev, stream, transpose_, Dim3((uint32_t)tiles), Dim3(256), 0, args);
+}
+
+void Pointwise::stream_copy(const HipBackend::DeviceHandle& dev, const void* in, void* out, uint64_t bytes,
+                            hipStream_t stream) const {
+    need_ptrs("stream_copy", {in, out});
+    if (bytes % 16) invalid("fg_stream_copy: bytes must be a multiple of 16");
+    if (!aligned16({in, out})) invalid("fg_stream_copy: d_in and d_out must be 16-byte aligned");
+    uint64_t n4 = bytes / 16;
+    const uint32_t block = 64;
+    uint64_t blocks = (n4 + block - 1) / block;
+    if (blocks > 0x7fffffffull) blocks = 0x7fffffffull;  // the kernel strides beyond this
+    if (blocks == 0) return;
+    void* args[] = {(void*)&in, &out, &n4};
+    HipBackend::launch(dev, stream, copy_, Dim3((uint32_t)blocks), Dim3(block), 0, args);
 }
 
 }  // namespace fg

@@ -41,34 +41,53 @@ _DIRECTIONS = {"forward": _n.FG_FORWARD, "inverse": _n.FG_INVERSE}
 
 
 def _direction(direction) -> int:
+    # `direction: &str` (lib.rs:451, 533): PyO3 0.23 refuses anything but a
+    # str with a TypeError before the function body runs.
+    if not isinstance(direction, str):
+        raise TypeError(f"argument 'direction': '{type(direction).__name__}' object cannot be converted to "
+                        "'PyString'")
     try:
         return _DIRECTIONS[direction]
-    except (KeyError, TypeError):
+    except KeyError:
         pass
     # Rust formats the offending string with {:?} (double-quoted), lib.rs:472-476.
     raise ValueError(f"direction must be 'forward' or 'inverse', got \"{direction}\"")
+
+
+def _normalize(normalize) -> int:
+    # `normalize: bool` (lib.rs:452, 534): PyO3 0.23 extracts Python bool and
+    # numpy.bool_ only; anything else (0, 1, "yes", None) is a TypeError.
+    if isinstance(normalize, (bool, np.bool_)):
+        return 1 if normalize else 0
+    raise TypeError(f"argument 'normalize': '{type(normalize).__name__}' object cannot be converted to 'PyBool'")
 
 
 def _device_handle(device):
     if device is None:
         return None
     if not isinstance(device, Device):
-        raise TypeError(f"argument 'device': expected ferrum_gpu.hip.Device, got {type(device).__name__}")
+        # `device: Option<PyRef<Device>>` (lib.rs:453, 535).
+        raise TypeError(f"argument 'device': '{type(device).__name__}' object cannot be converted to 'Device'")
     return device.handle
 
 
 def _complex64_array(arr, ndims: tuple[int, ...]) -> np.ndarray:
-    # PyReadonlyArray{1,2}<Complex32> + as_slice(): a complex64 ndarray of the
-    # right rank, C-contiguous (lib.rs:449, 461, 531, 560).
+    # PyReadonlyArray{1,2}<Complex32> extraction: a complex64 ndarray of the
+    # right rank (lib.rs:449, 531).  Contiguity is checked later, where the
+    # body calls as_slice() (_contiguous).
     if not isinstance(arr, np.ndarray):
         raise TypeError(f"argument 'arr': '{type(arr).__name__}' object cannot be converted to 'PyArray'")
     if arr.dtype != np.complex64:
         raise TypeError(f"argument 'arr': type mismatch: from={arr.dtype}, to=complex64")
     if arr.ndim not in ndims:
         raise TypeError(f"argument 'arr': dimensionality mismatch: from={arr.ndim}, to={ndims[0]}")
-    if not arr.flags.c_contiguous:
-        raise TypeError("The given array is not contiguous")
     return arr
+
+
+def _contiguous(a: np.ndarray) -> None:
+    # arr.as_slice()? (lib.rs:461, 560): numpy's NotContiguousError, a TypeError.
+    if not a.flags.c_contiguous:
+        raise TypeError("The given array is not contiguous")
 
 
 def fft_1d_c2c_pow2(arr, log_n, direction="forward", normalize=False, device=None):
@@ -78,19 +97,26 @@ def fft_1d_c2c_pow2(arr, log_n, direction="forward", normalize=False, device=Non
     "forward" (default) or "inverse"; ``normalize`` scales the inverse by 1/N;
     ``device`` is an optional persistent :class:`ferrum_gpu.hip.Device`.
     Returns a new ``complex64`` array of the same length.
+
+    Checks run in the reference's order: argument extraction (TypeError) for
+    every argument first, then the body's checks (lib.rs:455-477).
     """
     a = _complex64_array(arr, (1,))
     log_n = _as_u32(log_n)
+    if not isinstance(direction, str):
+        _direction(direction)
+    norm = _normalize(normalize)
+    h = _device_handle(device)
     if not (MIN_LOG_N <= log_n <= MAX_LOG_N):
         raise ValueError(f"log_n must be in [{MIN_LOG_N}, {MAX_LOG_N}], got {log_n}")
     n = 1 << log_n
+    _contiguous(a)
     total = a.size
     if total == 0 or total % n != 0:
         raise ValueError(f"arr len {total} must be a positive multiple of N = {n}")
     d = _direction(direction)
-    h = _device_handle(device)
     out = np.empty_like(a)
-    rc = _n.lib.fg_fft_1d_c2c_pow2_host(h, a.ctypes.data, out.ctypes.data, total, log_n, d, int(bool(normalize)))
+    rc = _n.lib.fg_fft_1d_c2c_pow2_host(h, a.ctypes.data, out.ctypes.data, total, log_n, d, norm)
     if rc != _n.FG_OK:
         raise ValueError(f"ferrum-gpu fft error: {_n.last_error()}")
     return out
@@ -101,9 +127,15 @@ def fft_2d_c2c_pow2(arr, log_n, direction="forward", normalize=False, device=Non
 
     Arguments mirror crates/ferrum-gpu-py/src/lib.rs:506-526; ``normalize``
     scales the inverse by 1/(N*N).  Returns a new array of the same shape.
+    Checks run in the reference's order (argument extraction, then
+    lib.rs:537-560).
     """
     a = _complex64_array(arr, (2, 3))
     log_n = _as_u32(log_n)
+    if not isinstance(direction, str):
+        _direction(direction)
+    norm = _normalize(normalize)
+    h = _device_handle(device)
     if not (MIN_LOG_N_2D <= log_n <= MAX_LOG_N_2D):
         raise ValueError(f"2D requires log_n in [{MIN_LOG_N_2D}, {MAX_LOG_N_2D}]; got {log_n}")
     n = 1 << log_n
@@ -111,10 +143,10 @@ def fft_2d_c2c_pow2(arr, log_n, direction="forward", normalize=False, device=Non
     if dims[-2:] != [n, n] or (a.ndim == 3 and dims[0] == 0):
         raise ValueError(f"arr shape {dims} != ({n}, {n})")
     d = _direction(direction)
-    h = _device_handle(device)
+    _contiguous(a)
     batch = 1 if a.ndim == 2 else dims[0]
     out = np.empty_like(a)
-    rc = _n.lib.fg_fft_2d_c2c_pow2_host(h, a.ctypes.data, out.ctypes.data, log_n, batch, d, int(bool(normalize)))
+    rc = _n.lib.fg_fft_2d_c2c_pow2_host(h, a.ctypes.data, out.ctypes.data, log_n, batch, d, norm)
     if rc != _n.FG_OK:
         raise ValueError(f"ferrum-gpu fft 2d error: {_n.last_error()}")
     return out
@@ -131,6 +163,23 @@ def _ptr(x):
     return int(x)
 
 
+def _ptr_sized(x, need: int, what: str):
+    """_ptr(x), refusing a DeviceBuffer or tensor smaller than ``need`` bytes:
+    the kernels would read and write past its end.  A raw address cannot be
+    checked; the caller vouches for it."""
+    if isinstance(x, DeviceBuffer):
+        if x.nbytes < need:
+            raise ValueError(f"{what}: buffer of {x.nbytes} bytes, the plan reads or writes {need}")
+        return x._p
+    if hasattr(x, "data_ptr"):
+        have = x.numel() * x.element_size()
+        if have < need or not x.is_contiguous():
+            raise ValueError(f"{what}: tensor of {have} bytes (contiguous: {x.is_contiguous()}), the plan "
+                             f"reads or writes {need} contiguous bytes")
+        return x.data_ptr()
+    return int(x)
+
+
 # Bound once: the per-call cost of the device-resident entry points is host
 # time that launch-bound callers (small batches) pay on every call.
 _fft_exec = _n.lib.fg_fft_exec
@@ -143,6 +192,7 @@ class _Plan:
         self._p = handle
         self.elems = elems
         self.batch = batch
+        self._nbytes = batch * elems * 8
 
     @property
     def nbytes(self) -> int:
@@ -152,8 +202,9 @@ class _Plan:
     def execute(self, d_in, d_out, direction="forward", normalize=False, stream: int = 0) -> None:
         """Stream-ordered, asynchronous execution on device buffers: equal (in
         place) or disjoint, 8-byte aligned."""
-        rc = _fft_exec(self._p, _ptr(d_in), _ptr(d_out), _direction(direction), 1 if normalize else 0,
-                       stream or None)
+        nb = self._nbytes
+        rc = _fft_exec(self._p, _ptr_sized(d_in, nb, "d_in"), _ptr_sized(d_out, nb, "d_out"), _direction(direction),
+                       1 if normalize else 0, stream or None)
         if rc:
             _n.check(rc)
 
@@ -167,8 +218,9 @@ class _Plan:
             arr = events.handles
         else:
             arr = (ctypes.c_void_p * len(events))(*[e._e.value for e in events])
-        rc = _fft_exec_events(self._p, _ptr(d_in), _ptr(d_out), _direction(direction), 1 if normalize else 0,
-                              stream or None, arr, len(arr))
+        nb = self._nbytes
+        rc = _fft_exec_events(self._p, _ptr_sized(d_in, nb, "d_in"), _ptr_sized(d_out, nb, "d_out"),
+                              _direction(direction), 1 if normalize else 0, stream or None, arr, len(arr))
         if rc:
             _n.check(rc)
 
@@ -178,8 +230,10 @@ class _Plan:
         float32 device arrays of ``batch * elems`` each (the reference's *_split
         kernels).  out_re/out_im may be in_re/in_im; stream-ordered."""
         d = _direction(direction)
-        _n.check(_n.lib.fg_fft_exec_split(self._p, _ptr(in_re), _ptr(in_im), _ptr(out_re), _ptr(out_im), d,
-                                          int(bool(normalize)), ctypes.c_void_p(stream or None)))
+        half = self._nbytes // 2
+        ptrs = [_ptr_sized(b, half, name) for b, name in
+                ((in_re, "in_re"), (in_im, "in_im"), (out_re, "out_re"), (out_im, "out_im"))]
+        _n.check(_n.lib.fg_fft_exec_split(self._p, *ptrs, d, int(bool(normalize)), ctypes.c_void_p(stream or None)))
 
     def capture_graph(self, d_in, d_out, direction="forward", normalize=False, reps: int = 1) -> "Graph":
         """A HIP graph of ``reps`` back-to-back ``execute(d_in, d_out, ...)``
@@ -189,8 +243,9 @@ class _Plan:
         destroyed while the graph exists)."""
         d = _direction(direction)
         g = ctypes.c_void_p()
-        _n.check(_n.lib.fg_fft_graph_create(self._p, _ptr(d_in), _ptr(d_out), d, int(bool(normalize)),
-                                            int(reps), ctypes.byref(g)))
+        nb = self._nbytes
+        _n.check(_n.lib.fg_fft_graph_create(self._p, _ptr_sized(d_in, nb, "d_in"), _ptr_sized(d_out, nb, "d_out"), d,
+                                            int(bool(normalize)), int(reps), ctypes.byref(g)))
         return Graph(self.device, g, keep=(self,))
 
     def kernel_names(self) -> list[str]:
@@ -260,6 +315,8 @@ def fft2_c2c_pow2(arr, direction="forward", normalize=False, device=None):
     ``(..., 2**a, 2**b)`` (4 <= a, b <= 12), rows and columns of any
     power-of-two lengths; ``normalize`` scales the inverse by 1/(rows*cols)."""
     a = _complex64_array(arr, (2, 3, 4))
+    norm = _normalize(normalize)
+    h = _device_handle(device)
     rows, cols = a.shape[-2], a.shape[-1]
     lr, lc = rows.bit_length() - 1, cols.bit_length() - 1
     if rows != 1 << lr or cols != 1 << lc or not (MIN_LOG_N_2D <= lr <= MAX_LOG_N_2D) \
@@ -270,9 +327,9 @@ def fft2_c2c_pow2(arr, direction="forward", normalize=False, device=None):
     if batch == 0:
         raise ValueError(f"arr shape {list(a.shape)} holds no image")
     d = _direction(direction)
+    _contiguous(a)
     out = np.empty_like(a)
-    rc = _n.lib.fg_fft_2d_rect_host(_device_handle(device), a.ctypes.data, out.ctypes.data, lr, lc, batch, d,
-                                    int(bool(normalize)))
+    rc = _n.lib.fg_fft_2d_rect_host(h, a.ctypes.data, out.ctypes.data, lr, lc, batch, d, norm)
     if rc != _n.FG_OK:
         raise ValueError(f"ferrum-gpu fft 2d error: {_n.last_error()}")
     return out
@@ -281,8 +338,10 @@ def fft2_c2c_pow2(arr, direction="forward", normalize=False, device=None):
 def transpose(device: Device, d_in, d_out, rows: int, cols: int, batch: int = 1, stream: int = 0) -> None:
     """out[b][c][r] = in[b][r][c] for ``batch`` rows x cols complex64 matrices on
     the device (stream-ordered; in and out must not alias)."""
-    _n.check(_n.lib.fg_transpose_c64(device.handle, _ptr(d_in), _ptr(d_out), int(rows), int(cols), int(batch),
-                                     ctypes.c_void_p(stream or None)))
+    rows, cols, batch = int(rows), int(cols), int(batch)
+    nb = 8 * rows * cols * batch
+    _n.check(_n.lib.fg_transpose_c64(device.handle, _ptr_sized(d_in, nb, "d_in"), _ptr_sized(d_out, nb, "d_out"),
+                                     rows, cols, batch, ctypes.c_void_p(stream or None)))
 
 
 def set_chunk_bytes(nbytes: int) -> None:

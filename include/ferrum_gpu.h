@@ -126,6 +126,8 @@ FG_API int fg_stream_destroy(fg_device_t dev, fg_stream_t stream);
 FG_API int fg_stream_sync(fg_device_t dev, fg_stream_t stream);
 FG_API int fg_event_create(fg_device_t dev, fg_event_t *out);
 FG_API int fg_event_destroy(fg_event_t ev);
+/* Records the event on `stream`; NULL = the default stream of the device the
+ * event was created on (the stream fg_fft_exec and the copies use for NULL). */
 FG_API int fg_event_record(fg_event_t ev, fg_stream_t stream);
 FG_API int fg_event_sync(fg_event_t ev);
 FG_API int fg_event_elapsed_ms(fg_event_t start, fg_event_t end, float *ms);
@@ -147,7 +149,11 @@ FG_API int fg_fft_plan_destroy(fg_fft_plan_t plan);
  * conjugation and 1/N (1/(N*N) for 2D) scaling done inside the kernels.
  * d_in and d_out each hold batch*N (2D: batch*N*N) complex64, 8-byte aligned;
  * they may be equal (in place) but must not otherwise overlap.
- * direction: FG_FORWARD or FG_INVERSE.  stream NULL = device default stream. */
+ * direction: FG_FORWARD or FG_INVERSE.  stream NULL = device default stream.
+ * A multi-launch plan (1D N > 4096, 2D images above 16384 points) keeps one
+ * workspace (and one split-layout staging buffer): executions of one plan
+ * must be ordered, one stream at a time; run concurrent work on separate
+ * plans. */
 FG_API int fg_fft_exec(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction, int normalize,
                 fg_stream_t stream);
 /* fg_fft_exec that also records events[i] on the stream right after launch i
@@ -183,7 +189,8 @@ FG_API int fg_graph_launch(fg_graph_t graph, fg_stream_t stream);
  * calling thread (fg_fft_exec, the elementwise kernels, fg_transpose_c64, ...)
  * are recorded instead of run, and fg_graph_capture_end turns them into one
  * graph and destroys the stream.  Make calls that allocate (the first
- * fg_fft_exec_split of a multi-launch plan) once before capturing.  The caller
+ * fg_fft_exec_split of a multi-launch plan, which refuses to run on a
+ * capturing stream) once before capturing.  The caller
  * keeps every plan and buffer the recorded calls use alive while the graph is
  * launched.  fg_graph_capture_end must be called once per begin, also after
  * a failed call. */
@@ -250,7 +257,9 @@ FG_API int fg_transpose_c64(fg_device_t dev, const void *d_in, void *d_out, uint
  * data.  d_out_re / d_out_im may equal d_in_re / d_in_im; no other overlap.
  * Single-pass plans (1D, N <= 4096; 2D images of up to 16384 points) run one
  * launch; other plans stage through an interleaved buffer the plan allocates
- * at its first split call.
+ * at its first split call (synchronously: that first call is refused with
+ * FG_ERR_INVALID_ARGUMENT, before any allocation, when `stream` is being
+ * captured).
  * Stream-ordered, asynchronous. */
 FG_API int fg_fft_exec_split(fg_fft_plan_t plan, const void *d_in_re, const void *d_in_im,
                              void *d_out_re, void *d_out_im, int direction, int normalize,

@@ -173,6 +173,91 @@ def test_fft_2d_argument_errors():
         f(np.zeros((16, 16), np.complex64), 4, direction="back")
 
 
+def test_argument_types_match_pyo3_extraction():
+    # `direction: &str` and `normalize: bool` (crates/ferrum-gpu-py/src/lib.rs:451-452,
+    # 533-534): PyO3 0.23 raises TypeError for any other type, before the
+    # function body's ValueErrors.
+    x = np.zeros(1024, np.complex64)
+    img = np.zeros((16, 16), np.complex64)
+    for f, a, ln in ((ferrum_gpu.fft.fft_1d_c2c_pow2, x, 10), (ferrum_gpu.fft.fft_2d_c2c_pow2, img, 4)):
+        with pytest.raises(TypeError, match=r"^argument 'direction': 'int' object cannot be converted to 'PyString'$"):
+            f(a, ln, direction=5)
+        with pytest.raises(TypeError, match=r"^argument 'direction': 'NoneType' object cannot be converted"):
+            f(a, ln, None)
+        with pytest.raises(TypeError, match=r"^argument 'normalize': 'str' object cannot be converted to 'PyBool'$"):
+            f(a, ln, "inverse", "yes")
+        with pytest.raises(TypeError, match=r"^argument 'normalize': 'int' object cannot be converted to 'PyBool'$"):
+            f(a, ln, "inverse", 1)
+        with pytest.raises(TypeError, match=r"^argument 'device': 'str' object cannot be converted to 'Device'$"):
+            f(a, ln, device="gpu0")
+        # extraction comes first: a bad normalize wins over an out-of-range log_n
+        with pytest.raises(TypeError, match="normalize"):
+            f(a, 40, "forward", 0)
+        # numpy.bool_ passes extraction (the log_n ValueError is what stops the call)
+        with pytest.raises(ValueError, match="log_n"):
+            f(a, 40, "forward", np.bool_(True))
+        with pytest.raises(ValueError, match="log_n"):
+            f(a, 40, "forward", False)
+    # the body's order: the log_n range check runs before as_slice()'s contiguity check
+    with pytest.raises(ValueError, match="log_n"):
+        ferrum_gpu.fft.fft_1d_c2c_pow2(np.zeros(2048, np.complex64)[::2], 30)
+    with pytest.raises(ValueError, match="direction"):
+        ferrum_gpu.fft.fft_2d_c2c_pow2(np.zeros((16, 32), np.complex64)[:, ::2], 4, "back")
+
+
+def _fake_buffer(nbytes, addr=1 << 20):
+    # A DeviceBuffer that owns nothing (no device call): only the size and
+    # address the Python layer checks.
+    b = object.__new__(ferrum_gpu.hip.DeviceBuffer)
+    b.nbytes = nbytes
+    b._p = ctypes.c_void_p(addr)
+    b.device = None
+    return b
+
+
+def test_small_buffers_are_refused_before_any_launch():
+    # A plan object with no native plan behind it: every refusal below must
+    # come from the size check, before the C ABI is called.
+    plan = object.__new__(ferrum_gpu.fft._Plan)
+    plan._p = ctypes.c_void_p(None)
+    plan.elems, plan.batch, plan._nbytes = 1024, 4, 4 * 1024 * 8
+    ok, small = _fake_buffer(plan.nbytes), _fake_buffer(plan.nbytes - 8)
+    with pytest.raises(ValueError, match=r"^d_in: buffer of 32760 bytes, the plan reads or writes 32768$"):
+        plan.execute(small, ok)
+    with pytest.raises(ValueError, match=r"^d_out: buffer of 32760 bytes"):
+        plan.execute(ok, small)
+    with pytest.raises(ValueError, match="d_out"):
+        plan.execute_recording(ok, small, [])
+    with pytest.raises(ValueError, match="d_in"):
+        plan.capture_graph(small, ok)
+    half_ok, half_small = _fake_buffer(plan.nbytes // 2), _fake_buffer(plan.nbytes // 2 - 4)
+    with pytest.raises(ValueError, match=r"^out_im: buffer of 16380 bytes, the plan reads or writes 16384$"):
+        plan.execute_split(half_ok, half_ok, half_ok, half_small)
+    # right-sized buffers reach the C ABI, which refuses the null plan
+    with pytest.raises(N.FerrumGpuError, match="plan is null"):
+        plan.execute(ok, ok)
+    with pytest.raises(N.FerrumGpuError, match="plan is null"):
+        plan.execute_split(half_ok, half_ok, half_ok, half_ok)
+    n = 100
+
+    class NoDevice:  # a device handle the size checks never reach
+        handle = None
+
+    dev = NoDevice()
+    with pytest.raises(ValueError, match="^out: buffer of 792 bytes"):
+        ferrum_gpu.pointwise.cmul(dev, _fake_buffer(800), _fake_buffer(800), _fake_buffer(792), n)
+    with pytest.raises(ValueError, match="^im: buffer of 396 bytes"):
+        ferrum_gpu.pointwise.deinterleave(dev, _fake_buffer(800), _fake_buffer(400), _fake_buffer(396), n)
+    with pytest.raises(ValueError, match="^re: buffer"):
+        ferrum_gpu.pointwise.interleave(dev, _fake_buffer(396), _fake_buffer(400), _fake_buffer(800), n)
+    with pytest.raises(ValueError, match="^b_im: buffer"):
+        ferrum_gpu.pointwise.cmul_split(dev, *[_fake_buffer(400)] * 3, _fake_buffer(4), *[_fake_buffer(400)] * 2, n)
+    with pytest.raises(ValueError, match="^out: buffer of 799 bytes"):
+        ferrum_gpu.synthetic.normal(dev, _fake_buffer(799), n, 1)
+    with pytest.raises(ValueError, match="^d_out: buffer"):
+        ferrum_gpu.fft.transpose(dev, _fake_buffer(8 * 64 * 32), _fake_buffer(8 * 64 * 31), 64, 32)
+
+
 def test_c_abi_validation_without_device():
     # The host entry points validate before they need a device.
     x = np.zeros(64, np.complex64)
