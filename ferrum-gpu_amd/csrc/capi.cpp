@@ -20,6 +20,7 @@
 #include "ferrum_gpu.h"
 #include "hip_backend.hpp"
 #include "host_stage.hpp"
+#include "scratch.hpp"
 
 using fg::Buffer;
 using fg::Cf32;
@@ -114,6 +115,10 @@ fg_device* open_device(int ordinal) {
     d->dev.reset(new HipDevice(h));
     d->fft_module = d->dev->load_or_cache(fg::fft_code_object());
     d->pointwise = fg::Pointwise(d->fft_module);
+    // The allocation-free entry point's scratch area: its address on this
+    // device, resolved once with the device current (scratch.hip).
+    HipBackend::bind(h);
+    fg::scratch_init(h->ordinal);
     return d.release();
 }
 
@@ -516,6 +521,18 @@ int fg_fft_exec_split(fg_fft_plan_t plan, const void* d_in_re, const void* d_in_
         need(plan, "plan");
         plan->plan->exec_split(d_in_re, d_in_im, d_out_re, d_out_im, parse_dir(direction), normalize != 0,
                                (hipStream_t)stream);
+    });
+}
+
+int fg_fft_exec_split_noalloc(fg_fft_plan_t plan, const void* d_in_re, const void* d_in_im, void* d_out_re,
+                              void* d_out_im, int direction, int normalize, fg_stream_t stream) {
+    return guarded([&] {
+        need(plan, "plan");
+        const Direction dir = parse_dir(direction);
+        std::string why;
+        void* scratch = fg::scratch_device_ptr(plan->dev->dev->handle()->ordinal, &why);
+        plan->plan->exec_split_into(d_in_re, d_in_im, d_out_re, d_out_im, dir, normalize != 0, (hipStream_t)stream,
+                                    scratch, fg::kScratchBytes, why);
     });
 }
 

@@ -554,10 +554,9 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
     }
 }
 
-void FftPlan::exec_split(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
-                         bool normalize, hipStream_t stream) const {
+void FftPlan::check_split(const void* in_re, const void* in_im, const void* out_re, const void* out_im) const {
     if (!in_re || !in_im || !out_re || !out_im) invalid("fft exec_split: null buffer");
-    const uint64_t n = (uint64_t)elems() * batch_, nb = 4 * n;
+    const uint64_t nb = 4ull * elems() * batch_;
     auto overlap = [nb](const void* a, const void* b) {
         const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
         return x < y + nb && y < x + nb;
@@ -567,21 +566,39 @@ void FftPlan::exec_split(const void* in_re, const void* in_im, void* out_re, voi
     if (overlap(out_re, out_im) || overlap(out_re, in_im) || overlap(out_im, in_re) ||
         (out_re != in_re && overlap(out_re, in_re)) || (out_im != in_im && overlap(out_im, in_im)))
         invalid("fft exec_split: overlapping buffers (only out_re == in_re and out_im == in_im may alias)");
-    if (split_fn_) {
-        const Step& s = steps_[0];  // the split twin has the same geometry and table
-        uint32_t flags = dir == Direction::Inverse ? (FG_PASS_CONJ_IN | FG_PASS_CONJ_SCALE_OUT) : 0u;
-        float sc = scale_for(dir, normalize);
-        const void* tw = s.tw;
-        uint64_t count = s.per_unit * batch_;
-        const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
-        if (s.small2d) {
-            const void* twc = s.tw_cols;
-            void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, (void*)&twc, &count, &sc, &flags};
-            HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
-            return;
-        }
-        void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, &count, &sc, &flags};
+}
+
+void FftPlan::split_one_launch(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
+                               bool normalize, hipStream_t stream) const {
+    const Step& s = steps_[0];  // the split twin has the same geometry and table
+    uint32_t flags = dir == Direction::Inverse ? (FG_PASS_CONJ_IN | FG_PASS_CONJ_SCALE_OUT) : 0u;
+    float sc = scale_for(dir, normalize);
+    const void* tw = s.tw;
+    uint64_t count = s.per_unit * batch_;
+    const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
+    if (s.small2d) {
+        const void* twc = s.tw_cols;
+        void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, (void*)&twc, &count, &sc, &flags};
         HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
+        return;
+    }
+    void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, &count, &sc, &flags};
+    HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
+}
+
+void FftPlan::split_staged(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
+                           bool normalize, hipStream_t stream, Cf32* stage) const {
+    const uint64_t n = (uint64_t)elems() * batch_;
+    pw_.interleave(dev_->handle(), in_re, in_im, stage, n, stream);
+    exec(stage, stage, dir, normalize, stream);
+    pw_.deinterleave(dev_->handle(), stage, out_re, out_im, n, stream);
+}
+
+void FftPlan::exec_split(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
+                         bool normalize, hipStream_t stream) const {
+    check_split(in_re, in_im, out_re, out_im);
+    if (split_fn_) {
+        split_one_launch(in_re, in_im, out_re, out_im, dir, normalize, stream);
         return;
     }
     {
@@ -596,12 +613,28 @@ void FftPlan::exec_split(const void* in_re, const void* in_im, void* out_re, voi
             if (status != hipStreamCaptureStatusNone)
                 invalid("fft exec_split: the first split-layout execution of a multi-launch plan allocates its "
                         "staging buffer, which a stream capture cannot record; run it once before capturing");
-            stage_ = dev_->alloc<Cf32>(n);
+            stage_ = dev_->alloc<Cf32>((uint64_t)elems() * batch_);
         }
     }
-    pw_.interleave(dev_->handle(), in_re, in_im, stage_.data(), n, stream);
-    exec(stage_.data(), stage_.data(), dir, normalize, stream);
-    pw_.deinterleave(dev_->handle(), stage_.data(), out_re, out_im, n, stream);
+    split_staged(in_re, in_im, out_re, out_im, dir, normalize, stream, stage_.data());
+}
+
+void FftPlan::exec_split_into(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
+                              bool normalize, hipStream_t stream, void* staging, size_t staging_bytes,
+                              const std::string& no_staging) const {
+    check_split(in_re, in_im, out_re, out_im);
+    if (split_fn_) {
+        split_one_launch(in_re, in_im, out_re, out_im, dir, normalize, stream);
+        return;
+    }
+    const uint64_t need = 8ull * elems() * batch_;
+    if (need > staging_bytes)
+        invalid("fft exec_split_noalloc: the plan stages " + std::to_string(need) + " bytes (" +
+                std::to_string(batch_) + " x " + std::to_string(elems()) + " complex64), beyond the " +
+                std::to_string(staging_bytes) + "-byte device scratch area");
+    if (!staging) fail(FG_ERR_INTERNAL, "fft exec_split_noalloc: " + no_staging);
+    if (reinterpret_cast<uintptr_t>(staging) & 15u) fail(FG_ERR_INTERNAL, "fft exec_split_noalloc: scratch misaligned");
+    split_staged(in_re, in_im, out_re, out_im, dir, normalize, stream, static_cast<Cf32*>(staging));
 }
 
 }  // namespace fg

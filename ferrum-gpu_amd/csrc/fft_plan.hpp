@@ -66,6 +66,14 @@ public:
     // deinterleave.  out_re/out_im may be in_re/in_im (in place).
     void exec_split(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
                     bool normalize, hipStream_t stream) const;
+    // exec_split staging through `staging` (staging_bytes long, 16-byte
+    // aligned device memory the caller owns) instead of the plan's own
+    // buffer: allocates nothing.  Single-pass plans use no staging; a plan
+    // whose batch needs more than staging_bytes is refused, and a null
+    // `staging` fails with `no_staging` as the reason.
+    void exec_split_into(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
+                         bool normalize, hipStream_t stream, void* staging, size_t staging_bytes,
+                         const std::string& no_staging) const;
     // Launches exec_split makes: 1 for single-pass plans, launches() + 2 otherwise.
     int split_launches() const { return split_fn_ ? 1 : launches() + 2; }
 
@@ -113,6 +121,13 @@ private:
         : dev_(&dev), kind_(kind), log_n_(log_n), log_rows_(log_rows), batch_(batch), chunk_(batch) {}
 
     float scale_for(Direction dir, bool normalize) const;
+    // The split-layout paths: argument checks, the one launch of single-pass
+    // plans, and interleave -> exec in place -> deinterleave through `stage`.
+    void check_split(const void* in_re, const void* in_im, const void* out_re, const void* out_im) const;
+    void split_one_launch(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
+                          bool normalize, hipStream_t stream) const;
+    void split_staged(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
+                      bool normalize, hipStream_t stream, Cf32* stage) const;
     // Stage table for a length-2^log_l Stockham transform with 2^log_e elements
     // per thread (uploaded once per plan).
     const void* stage_table(uint32_t log_l, uint32_t log_e);

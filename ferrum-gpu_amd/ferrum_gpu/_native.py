@@ -116,6 +116,7 @@ _sig("fg_fft_plan_2d_rect", _vp, _u32, _u32, _sz, _P(_vp))
 _sig("fg_fft_2d_rect_host", _vp, _vp, _vp, _u32, _u32, _sz, _i, _i)
 _sig("fg_transpose_c64", _vp, _vp, _vp, _u32, _u32, _sz, _vp)
 _sig("fg_fft_exec_split", _vp, _vp, _vp, _vp, _vp, _i, _i, _vp)
+_sig("fg_fft_exec_split_noalloc", _vp, _vp, _vp, _vp, _vp, _i, _i, _vp)
 _sig("fg_cmul_c64", _vp, _vp, _vp, _vp, _sz, _vp)
 _sig("fg_cmul_split", _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp)
 _sig("fg_deinterleave_c64", _vp, _vp, _vp, _vp, _sz, _vp)

@@ -235,6 +235,20 @@ class _Plan:
                 ((in_re, "in_re"), (in_im, "in_im"), (out_re, "out_re"), (out_im, "out_im"))]
         _n.check(_n.lib.fg_fft_exec_split(self._p, *ptrs, d, int(bool(normalize)), ctypes.c_void_p(stream or None)))
 
+    def execute_split_noalloc(self, in_re, in_im, out_re, out_im, direction="forward", normalize=False,
+                              stream: int = 0) -> None:
+        """execute_split() that allocates nothing (fg_fft_exec_split_noalloc):
+        multi-launch plans stage through the library's fixed 64 MiB device
+        scratch area instead of a buffer of their own, so the call may be
+        captured into a graph on any use.  Calls that overlap in time on one
+        GPU share that area and race."""
+        d = _direction(direction)
+        half = self._nbytes // 2
+        ptrs = [_ptr_sized(b, half, name) for b, name in
+                ((in_re, "in_re"), (in_im, "in_im"), (out_re, "out_re"), (out_im, "out_im"))]
+        _n.check(_n.lib.fg_fft_exec_split_noalloc(self._p, *ptrs, d, int(bool(normalize)),
+                                                  ctypes.c_void_p(stream or None)))
+
     def capture_graph(self, d_in, d_out, direction="forward", normalize=False, reps: int = 1) -> "Graph":
         """A HIP graph of ``reps`` back-to-back ``execute(d_in, d_out, ...)``
         calls, replayed with one submission by ``Graph.launch``.  The graph

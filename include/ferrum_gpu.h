@@ -265,6 +265,23 @@ FG_API int fg_fft_exec_split(fg_fft_plan_t plan, const void *d_in_re, const void
                              void *d_out_re, void *d_out_im, int direction, int normalize,
                              fg_stream_t stream);
 
+/* fg_fft_exec_split that allocates nothing, on any call.  No counterpart in
+ * the reference; it is for callers that cannot allocate device memory: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Multi-launch plans stage through a fixed device scratch area
+ * of 64 MiB (67108864 bytes) that the library holds on each GPU it opens,
+ * from fg_device_open until the process ends, instead of the plan's lazily
+ * allocated buffer; a plan whose batch needs more staging (8 bytes per
+ * element of batch * elements) is refused with FG_ERR_INVALID_ARGUMENT.
+ * Single-pass plans need no staging and run as fg_fft_exec_split does.
+ * Same results as fg_fft_exec_split, bit for bit.  All callers on one GPU
+ * share its scratch area, which keeps the last call's contents: calls that
+ * overlap in time on one GPU (different streams, threads or plans) race;
+ * calls ordered on one stream do not.  Stream-ordered, asynchronous. */
+FG_API int fg_fft_exec_split_noalloc(fg_fft_plan_t plan, const void *d_in_re, const void *d_in_im,
+                                     void *d_out_re, void *d_out_im, int direction, int normalize,
+                                     fg_stream_t stream);
+
 /* Elementwise kernels over n complex elements (kernels_body.rs:1612-1672).
  * Products are evaluated as re = ar*br - ai*bi, im = ar*bi + ai*br in f32
  * without fused multiply-add, like the reference.  Any alignment of complex64
