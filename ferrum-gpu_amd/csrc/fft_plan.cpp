@@ -29,9 +29,11 @@ struct StockhamGeom {
 // N = 16 .. 128 hold 4 or 8 elements per thread: 16 (the larger sizes' choice)
 // measured 217 / 232 / 234 / 211 us per 512 MiB batch against 182 / 183 / 171
 // / 173 us for the entries below (N = 256 .. 4096 measured best at 16).
+// N = 8192 / 16384 ({5, 1}): 32 elements per thread with the exchanges in
+// halves (fg_fft_n13 / fg_fft_n14, kernels/fft_stockham.hpp).
 constexpr StockhamGeom kStockham[kMaxLogNSingle + 1] = {
     {0, 0}, {0, 0},          // log_n 0, 1: unsupported
-    {2, 64}, {3, 64}, {3, 32}, {3, 16}, {2, 4}, {3, 4}, {4, 4}, {4, 2}, {4, 2}, {4, 1}, {4, 1},
+    {2, 64}, {3, 64}, {3, 32}, {3, 16}, {2, 4}, {3, 4}, {4, 4}, {4, 2}, {4, 2}, {4, 1}, {4, 1}, {5, 1}, {5, 1},
 };
 // Latency geometry (fg_fft_n<L>_lat, one transform per workgroup, fewer
 // elements per thread: more threads per transform, shorter serial chains),
@@ -40,7 +42,7 @@ constexpr StockhamGeom kStockham[kMaxLogNSingle + 1] = {
 // N = 1024 3.94 -> 3.65 us, N = 4096 10.94 -> 10.69 us.
 constexpr StockhamGeom kStockhamLatency[kMaxLogNSingle + 1] = {
     {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0},
-    {2, 1}, {0, 0}, {3, 1}, {0, 0}, {3, 1},
+    {2, 1}, {0, 0}, {3, 1}, {0, 0}, {3, 1}, {0, 0}, {0, 0},
 };
 
 // The code object named by FERRUM_GPU_CODE_OBJECT, read once per process (a
@@ -84,6 +86,19 @@ std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e) {
         const uint64_t L = 1ull << logl, R = 1ull << logr, M = L * R;
         // Row exponents (kernels/fft_stockham.hpp, tw_row_len): factored rows
         // for radix 16 and 8, full rows below.
+        if (L >= 1024) {
+            // Two-level block (kernels/fft_stockham.hpp, tw_two_level):
+            // W_M^{64 h} for h < L/64, then W_M^l for l < 64.
+            for (uint64_t h = 0; h < L / 64; ++h) {
+                const double ang = 2.0 * M_PI * (double)((64 * h) % M) / (double)M;
+                t.push_back(Cf32{(float)cos(ang), (float)-sin(ang)});
+            }
+            for (uint64_t l = 0; l < 64; ++l) {
+                const double ang = 2.0 * M_PI * (double)l / (double)M;
+                t.push_back(Cf32{(float)cos(ang), (float)-sin(ang)});
+            }
+            continue;
+        }
         std::vector<uint64_t> ps;
         if (R == 16) ps = {1, 2, 3, 4, 8, 12};
         else if (R == 8) ps = {1, 2, 3, 4};
@@ -259,7 +274,8 @@ void FftPlan::add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64
     s.fpb = g.fpb;
     s.src = src;
     s.dst = dst;
-    s.tw = stage_table(log_l, g.log_e);
+    // 32-element kernels (log_e 5) run the radix-16 list of the 16-element layout.
+    s.tw = stage_table(log_l, std::min<uint32_t>(g.log_e, 4));
     s.per_unit = per_unit;
     steps_.push_back(s);
 }

@@ -34,9 +34,9 @@ struct Cf32 {
 KernelArtifact fft_code_object();
 
 // Supported shapes (the reference: 1D [2, 12], plan.rs:58; 2D [4, 12],
-// crates/ferrum-gpu-py/src/lib.rs:537).  1D is widened to 2^24 by the
-// multi-pass decomposition.
-constexpr uint32_t kMinLogN1D = 2, kMaxLogN1D = 24, kMaxLogNSingle = 12;
+// crates/ferrum-gpu-py/src/lib.rs:537).  1D is widened to 2^24: single-pass
+// up to 2^14 (the whole transform in one workgroup's LDS), multi-pass beyond.
+constexpr uint32_t kMinLogN1D = 2, kMaxLogN1D = 24, kMaxLogNSingle = 14;
 constexpr uint32_t kMinLogN2D = 4, kMaxLogN2D = 12;
 
 class FftPlan {
@@ -166,11 +166,12 @@ private:
 // per stage s >= 1 (L = 2^(s*log_e), R = that stage's radix) one row per k < L
 // of W_{L*R}^{p*k} for p in {1,2,3,4,8,12} (R = 16), {1,2,3,4} (R = 8) or
 // [0, R) (R <= 4), computed in fp64 and rounded to f32 (the kernels form the
-// remaining exponents as products; kernels/fft_stockham.hpp).
+// remaining exponents as products; kernels/fft_stockham.hpp).  A stage with
+// L >= 1024 stores the two-level block W^{64 h} (h < L/64), W^l (l < 64).
 std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e);
 // Two-level root table: [j] = W_4096^j, [4096 + j] = W_{2^24}^j, j < 4096.
 std::vector<Cf32> big_twiddles();
-// Digit split (log2 sizes, slowest digit first) of a 1D length 2^log_n > 4096.
+// Digit split (log2 sizes, slowest digit first) of a 1D length 2^log_n > 16384.
 std::vector<uint32_t> split_1d(uint32_t log_n);
 // Columns per tile for a pass of length 2^log_l that reads HBM.
 uint32_t tile_columns(uint32_t log_l);

@@ -54,6 +54,26 @@ FG_STOCKHAM(9, 4, 2)     // N=512:  32 threads
 FG_STOCKHAM(10, 4, 2)    // N=1024: 64 threads (one wave) per transform, 2 per workgroup
 FG_STOCKHAM(11, 4, 1)    // N=2048: 128 threads
 FG_STOCKHAM(12, 4, 1)    // N=4096: 256 threads
+// N = 8192 / 16384: one transform per workgroup of N/32 threads with 32
+// elements each and the exchanges in halves (fft_row_halves_body), at most
+// 128 VGPRs (four waves per SIMD): 34 / 68 KB of LDS, four / two workgroups
+// per CU.  The stage table is the 16-element layout's (kStockham holds
+// log_e = 5 for the geometry; the host builds the table with log_e = 4).
+#define FG_STOCKHAM_HALVES(LOGN)                                                               \
+    extern "C" __global__ __launch_bounds__(HalvesShape<LOGN>::T) __attribute__((amdgpu_waves_per_eu(4))) \
+    void fg_fft_n##LOGN(const float2* __restrict__ in, float2* __restrict__ out,               \
+                        const float2* __restrict__ tw, uint64_t batch, float scale, uint32_t flags) { \
+        fft_row_halves_body<LOGN>(InterleavedIO{in, out}, tw, batch, scale, flags);            \
+    }                                                                                          \
+    extern "C" __global__ __launch_bounds__(HalvesShape<LOGN>::T) __attribute__((amdgpu_waves_per_eu(4))) \
+    void fg_fft_n##LOGN##_split(const float* __restrict__ in_re, const float* __restrict__ in_im, \
+                                float* __restrict__ out_re, float* __restrict__ out_im,        \
+                                const float2* __restrict__ tw, uint64_t batch, float scale,     \
+                                uint32_t flags) {                                               \
+        fft_row_halves_body<LOGN>(SplitIO{in_re, in_im, out_re, out_im}, tw, batch, scale, flags); \
+    }
+FG_STOCKHAM_HALVES(13)   // N=8192:  256 threads
+FG_STOCKHAM_HALVES(14)   // N=16384: 512 threads
 // fg_fft_n<L>_lat[_split]: one transform per workgroup with fewer elements per
 // thread (kStockhamLatency in fft_plan.cpp), for batches too small to fill the
 // GPU; the split twin keeps split and interleaved results bit-identical.
@@ -276,7 +296,6 @@ FG_TILE_HALVES(9, 16)
 FG_TILE_HALVES(10, 16)
 // Row passes (last 1D digit: rows contiguous, transposed store): the widths
 // for HBM-resident input, then those for cache-resident input.
-FG_TILE(6, 64, true, r)
 FG_TILE(7, 64, true, r)
 FG_TILE(8, 32, true, r)
 FG_TILE(9, 16, true, r)

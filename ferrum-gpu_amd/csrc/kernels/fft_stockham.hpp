@@ -55,13 +55,24 @@ __device__ __forceinline__ int lds_pos(int p) { return p + (p >> SH); }
 // against 12 KB factored.
 __host__ __device__ constexpr int tw_row_len(int R) { return R == 16 ? 6 : (R == 8 ? 4 : R); }
 
+// A stage whose butterflies span L >= 1024 (the last, radix-2 or radix-4 stage
+// of N = 2^13 and 2^14) would need L rows -- 64 / 128 KB that every
+// workgroup streams through its L1.  Such a stage stores a two-level table
+// instead, A[h] = W_M^{64 h} for h < L/64 followed by B[l] = W_M^l for
+// l < 64 (M = L*R), and forms W^k = A[k >> 6] * B[k & 63], W^{2k} = (W^k)^2,
+// W^{3k} = W^{2k} * W^k (up to five f32 roundings, under 6e-7).
+__host__ __device__ constexpr bool tw_two_level(int L) { return L >= 1024; }
+__host__ __device__ constexpr int tw_stage_entries(int L, int R) {
+    return tw_two_level(L) ? L / 64 + 64 : L * tw_row_len(R);
+}
+
 template <int LOGN, int LOGE>
 __host__ __device__ constexpr int stockham_tw_offset(int s) {
     int off = 0;
     for (int i = 1; i < s; ++i) {
         int logl = i * LOGE;
         int logr = (i < LOGN / LOGE) ? LOGE : (LOGN % LOGE);
-        off += (1 << logl) * tw_row_len(1 << logr);
+        off += tw_stage_entries(1 << logl, 1 << logr);
     }
     return off;
 }
@@ -98,6 +109,24 @@ __device__ __forceinline__ void apply_stage_twiddles(float2* u, const float2* __
     }
 }
 
+// Multiplies input p of a radix-R butterfly with k = b mod L by W_{L*R}^{p*k},
+// from the block of the stage's table at `stage`.
+template <int R, int L>
+__device__ __forceinline__ void apply_stage_twiddles_at(float2* u, const float2* __restrict__ stage, int k) {
+    if constexpr (tw_two_level(L)) {
+        static_assert(R == 2 || R == 4, "two-level stages are radix 2 or 4");
+        const float2 w1 = cmul(stage[k >> 6], stage[L / 64 + (k & 63)]);
+        u[1] = cmul(u[1], w1);
+        if constexpr (R == 4) {
+            const float2 w2 = cmul(w1, w1);
+            u[2] = cmul(u[2], w2);
+            u[3] = cmul(u[3], cmul(w2, w1));
+        }
+    } else {
+        apply_stage_twiddles<R>(u, stage + k * tw_row_len(R));
+    }
+}
+
 // Processes one stage's butterflies for a thread: x holds the E gathered
 // elements (position t + T*m at index m); on return x holds the outputs laid
 // out so that output q of butterfly i sits at index i + NB*q.
@@ -117,7 +146,7 @@ __device__ __forceinline__ void stockham_stage_regs(float2* x, int t, const floa
         if constexpr (L > 1) {
             const int b = t + Sh::T * i;
             const int k = b & (L - 1);
-            apply_stage_twiddles<R>(u, tw + stockham_tw_offset<LOGN, LOGE>(S) + k * tw_row_len(R));
+            apply_stage_twiddles_at<R, L>(u, tw + stockham_tw_offset<LOGN, LOGE>(S), k);
         }
         Dft<R>::run(u);
 #pragma unroll
@@ -282,6 +311,136 @@ __device__ __forceinline__ void fft_stockham_body(const IO io, const float2* __r
             if (cs) v = cscale(cconj(v), scale);
             io.store(f * Sh::N + t + Sh::T * m, v);
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 32 elements per thread, exchanges in halves.  T = L/32 threads hold 32
+// elements each (positions t + T*m) and run NB = 32/R butterflies
+// b = t + T*i of every stage of the radix list (16, ..., 16, r).  Butterfly b
+// of stage s writes to j*L_s*R + k + q*L_s (j = b / L_s, k = b % L_s), below
+// L/2 exactly when i < NB/2 (b < T), so every exchange can run in two rounds
+// through LDS holding L/2 positions: round h writes butterflies
+// i in [h*NB/2, (h+1)*NB/2), then each thread reads its elements
+// m in [16h, 16h + 16).  The last stage's outputs are the thread's own
+// positions t + T*m.  Used by the first pass of 1D multi-pass plans
+// (fft_tile.hpp, G columns per workgroup) and by the single-pass 8192- and
+// 16384-point transforms (fft_row_halves_body below): half the LDS of the
+// 16-element layout, so twice the workgroups per CU.
+template <int LOGL>
+struct HalvesShape {
+    static constexpr int N = 1 << LOGL, E = 32, T = N / E, HALF = N / 2;
+    static constexpr int NFULL = LOGL / 4, REM = LOGL % 4;
+    static constexpr int NSTAGES = NFULL + (REM ? 1 : 0);
+    static_assert((LOGL >= 7 && LOGL <= 10) || LOGL == 13 || LOGL == 14,
+                  "half exchanges: 128 .. 1024-point tile columns, 8192 / 16384-point rows");
+};
+
+template <int LOGL, int S>
+struct HalvesStage {
+    static constexpr int LOGR = (S < HalvesShape<LOGL>::NFULL) ? 4 : HalvesShape<LOGL>::REM;
+    static constexpr int R = 1 << LOGR;
+    static constexpr int NB = HalvesShape<LOGL>::E / R;  // butterflies per thread
+    static constexpr int L = 1 << (4 * S);              // product of the earlier radices
+};
+
+// Stage S: y[i + NB*q] = output q of butterfly i (inputs x[i + NB*p]).  The
+// twiddles come from the table of the radix list (16, ..., 16, r), the one
+// the 16-element geometry uses.
+template <int LOGL, int S>
+__device__ __forceinline__ void halves_stage(const float2* x, float2* y, int t, const float2* __restrict__ tw) {
+    using H = HalvesShape<LOGL>;
+    using St = HalvesStage<LOGL, S>;
+#pragma unroll
+    for (int i = 0; i < St::NB; ++i) {
+        float2 u[St::R];
+#pragma unroll
+        for (int p = 0; p < St::R; ++p) u[p] = x[i + St::NB * p];
+        if constexpr (St::L > 1) {
+            const int k = (t + H::T * i) & (St::L - 1);
+            apply_stage_twiddles_at<St::R, St::L>(u, tw + stockham_tw_offset<LOGL, 4>(S), k);
+        }
+        Dft<St::R>::run(u);
+#pragma unroll
+        for (int q = 0; q < St::R; ++q) y[i + St::NB * q] = u[q];
+    }
+}
+
+// Exchange after stage S of one contiguous transform: x[m] = the element at
+// position t + T*m.  The LDS holds L/2 positions, one pad slot per 16
+// (lds_pos): lds_pos(d + q*L_s) = lds_pos(d) + q*(L_s + L_s/16) for L_s a
+// multiple of 16, and at stage 0 (L_s = 1) butterfly b writes 16b + q, slot
+// 17b + q.
+template <int LOGN, int S>
+__device__ __forceinline__ void row_halves_exchange(const float2* y, float2* x, int t, float2* __restrict__ lds) {
+    using H = HalvesShape<LOGN>;
+    using St = HalvesStage<LOGN, S>;
+    static_assert(St::R == 16 && H::T % 16 == 0, "exchanges follow radix-16 stages");
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (S > 0 || h > 0) __syncthreads();  // the previous round's readers are done
+#pragma unroll
+        for (int ii = 0; ii < St::NB / 2; ++ii) {
+            const int i = h * (St::NB / 2) + ii;
+            const int b = t + H::T * i;
+            float2* base;
+            if constexpr (St::L == 1) {
+                base = lds + 17 * (b - (H::HALF / 16) * h);
+#pragma unroll
+                for (int q = 0; q < 16; ++q) base[q] = y[i + St::NB * q];
+            } else {
+                const int d0 = (b >> (4 * S)) * St::L * 16 + (b & (St::L - 1)) - H::HALF * h;
+                base = lds + lds_pos<>(d0);
+#pragma unroll
+                for (int q = 0; q < 16; ++q) base[q * (St::L + St::L / 16)] = y[i + St::NB * q];
+            }
+        }
+        __syncthreads();
+        const float2* rbase = lds + lds_pos<>(t);
+#pragma unroll
+        for (int m = 0; m < H::E / 2; ++m) x[(H::E / 2) * h + m] = rbase[m * (H::T + H::T / 16)];
+    }
+}
+
+template <int LOGN, int S>
+struct RowHalvesStages {
+    __device__ __forceinline__ static void run(float2* x, float2* y, int t, const float2* __restrict__ tw,
+                                               float2* __restrict__ lds) {
+        halves_stage<LOGN, S>(x, y, t, tw);
+        if constexpr (S + 1 < HalvesShape<LOGN>::NSTAGES) {
+            row_halves_exchange<LOGN, S>(y, x, t, lds);
+            RowHalvesStages<LOGN, S + 1>::run(x, y, t, tw, lds);
+        }
+    }
+};
+
+// One transform of N = 2^LOGN (8192 or 16384) points per workgroup of N/32
+// threads, 32 elements per thread, LDS of N/2 + N/32 positions (68 KB at
+// 16384: two workgroups per CU where the 16-element layout's 136 KB allows
+// one).  IO and flags as fft_stockham_body; the stage table is the radix
+// list (16, 16, 16, r) of the 16-element layout.
+template <int LOGN, class IO>
+__device__ __forceinline__ void fft_row_halves_body(const IO io, const float2* __restrict__ tw, uint64_t batch,
+                                                    float scale, uint32_t flags) {
+    using H = HalvesShape<LOGN>;
+    __shared__ float2 lds[H::HALF + H::HALF / 16];
+    const int t = threadIdx.x;
+    const uint64_t f = blockIdx.x;
+    if (f >= batch) return;  // uniform over the workgroup (the host launches batch of them)
+    float2 x[H::E], y[H::E];
+#pragma unroll
+    for (int m = 0; m < H::E; ++m) x[m] = io.load(f * H::N + t + H::T * m);
+    if (flags & FG_PASS_CONJ_IN) {
+#pragma unroll
+        for (int m = 0; m < H::E; ++m) x[m] = cconj(x[m]);
+    }
+    RowHalvesStages<LOGN, 0>::run(x, y, t, tw, lds);
+    const bool cs = (flags & FG_PASS_CONJ_SCALE_OUT) != 0;
+#pragma unroll
+    for (int m = 0; m < H::E; ++m) {
+        float2 v = y[m];
+        if (cs) v = cscale(cconj(v), scale);
+        io.store(f * H::N + t + H::T * m, v);
     }
 }
 

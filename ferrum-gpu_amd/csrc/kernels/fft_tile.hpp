@@ -231,56 +231,13 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
 
 // ---------------------------------------------------------------------------
 // Column pass with the Stockham exchanges in halves (the first pass of a 1D
-// multi-pass plan, which reads the caller's input from HBM).  T = L/32
-// threads per column hold 32 elements each (positions t + T*m) and run
-// NB = 32/R butterflies b = t + T*i of every stage of the radix list
-// (16, ..., 16, r).  Butterfly b of stage s writes to j*L_s*R + k + q*L_s
-// (j = b / L_s, k = b % L_s), below L/2 exactly when i < NB/2, so every
-// exchange runs in two rounds through an LDS tile of L/2 positions: round h
-// writes butterflies i in [h*NB/2, (h+1)*NB/2), then each thread reads its
-// elements m in [16h, 16h + 16).  Half the LDS of the 16-element tile: four
-// 33 KB workgroups per CU instead of two for 128 / 256 points (64 / 32
-// columns), two 68 KB ones instead of one for 1024 (16 columns), so more of a
-// CU's tiles are loading while others compute.  The last stage's outputs are
-// the thread's own positions t + T*m.
-template <int LOGL>
-struct HalvesShape {
-    static constexpr int N = 1 << LOGL, E = 32, T = N / E, HALF = N / 2;
-    static constexpr int NFULL = LOGL / 4, REM = LOGL % 4;
-    static constexpr int NSTAGES = NFULL + (REM ? 1 : 0);
-    static_assert(LOGL >= 7 && LOGL <= 10, "half exchanges: 128 .. 1024 points");
-};
-
-template <int LOGL, int S>
-struct HalvesStage {
-    static constexpr int LOGR = (S < HalvesShape<LOGL>::NFULL) ? 4 : HalvesShape<LOGL>::REM;
-    static constexpr int R = 1 << LOGR;
-    static constexpr int NB = HalvesShape<LOGL>::E / R;  // butterflies per thread
-    static constexpr int L = 1 << (4 * S);              // product of the earlier radices
-};
-
-// Stage S: y[i + NB*q] = output q of butterfly i (inputs x[i + NB*p]).  The
-// twiddles come from the table of the radix list (16, ..., 16, r), the one
-// the 16-element geometry uses.
-template <int LOGL, int S>
-__device__ __forceinline__ void halves_stage(const float2* x, float2* y, int t, const float2* __restrict__ tw) {
-    using H = HalvesShape<LOGL>;
-    using St = HalvesStage<LOGL, S>;
-#pragma unroll
-    for (int i = 0; i < St::NB; ++i) {
-        float2 u[St::R];
-#pragma unroll
-        for (int p = 0; p < St::R; ++p) u[p] = x[i + St::NB * p];
-        if constexpr (St::L > 1) {
-            const int k = (t + H::T * i) & (St::L - 1);
-            apply_stage_twiddles<St::R>(u, tw + stockham_tw_offset<LOGL, 4>(S) + k * tw_row_len(St::R));
-        }
-        Dft<St::R>::run(u);
-#pragma unroll
-        for (int q = 0; q < St::R; ++q) y[i + St::NB * q] = u[q];
-    }
-}
-
+// multi-pass plan, which reads the caller's input from HBM): the 32-element
+// stages of fft_stockham.hpp (HalvesShape, halves_stage) on every column of
+// the tile, each exchange in two rounds through an LDS tile of L/2
+// positions.  Half the LDS of the 16-element tile: four 33 KB workgroups per
+// CU instead of two for 128 / 256 points (64 / 32 columns), two 68 KB ones
+// instead of one for 1024 (16 columns), so more of a CU's tiles are loading
+// while others compute.
 // Exchange after stage S: x[m] = the element at position t + T*m.
 template <int LOGL, int S, int G>
 __device__ __forceinline__ void halves_exchange(const float2* y, float2* x, int t, int c, float2* __restrict__ lds) {

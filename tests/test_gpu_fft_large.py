@@ -1,4 +1,4 @@
-"""GPU parity of the multi-pass paths: 1D lengths 2^13 .. 2^24 and 2D images.
+"""GPU parity of the multi-pass paths: 1D lengths 2^13 .. 2^24 (one pass up to 2^14) and 2D images.
 
 Bar: relative L2 <= 1e-4 against the CPU oracle (the reference's radix-2
 Stockham, crates/ferrum-gpu-fft/src/cpu.rs and cpu_2d.rs) on identical seeded
@@ -174,7 +174,7 @@ def test_host_path_plan_cache_eviction(gpu_device):
     import ferrum_gpu
 
     rng = np.random.default_rng(77)
-    log_n = 14
+    log_n = 15
     batches = list(range(1, 12)) + [3, 1, 11]
     for batch in batches:
         x = uniform_c64(rng, batch << log_n)

@@ -121,14 +121,19 @@ def use_halves_tile(log_l, g, rowwise, reads_input):
 
 
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None):
-    """The kernel of every pass of a multi-launch plan (1D N > 4096, or 2D with
-    2^log_n rows and 2^log_cols columns), in launch order."""
+    """The kernel of every pass of a plan of 1D length 2^log_n (one pass up to
+    16384 points, several beyond) or of 2D images with 2^log_n rows and
+    2^log_cols columns, in launch order."""
     def tile(p, pol, reads_input=False):
         kind = "h" if use_halves_tile(p["log_l"], p["g"], p["rowwise"], reads_input) else \
             ("r" if p["rowwise"] else "c")
         return f"fg_tile_l{p['log_l']}_g{p['g']}_{kind}{pol}"
 
     if not two_d:
+        if log_n <= 14:
+            # single pass: the Stockham kernel (fg_fft_n13 / n14: 32 elements
+            # per thread, exchanges in halves; test_tile_halves_model)
+            return [f"fg_fft_n{log_n}"]
         passes = tile_geometry_1d(log_n, 1, cached)
         return [tile(p, pass_policy(i, len(passes), cached, p["g"]), reads_input=(i == 0))
                 for i, p in enumerate(passes)]
@@ -192,7 +197,7 @@ def run_geometry(buf_in, passes, batch, elems):
 
 
 @pytest.mark.parametrize("cached", [True, False], ids=["chunked", "unchunked"])
-@pytest.mark.parametrize("log_n", [13, 14, 15, 16, 17, 18, 20])
+@pytest.mark.parametrize("log_n", [15, 16, 17, 18, 20])
 def test_1d_multipass_matches_oracle(log_n, cached):
     rng = np.random.default_rng(log_n)
     batch = 2
@@ -264,7 +269,7 @@ def test_long_column_widths():
 
 
 def test_split_sizes_fit_the_tile_kernel():
-    for log_n in range(13, 25):
+    for log_n in range(15, 25):
         logs = split_1d(log_n)
         assert sum(logs) == log_n
         assert all(4 <= l <= 10 for l in logs), (log_n, logs)   # wide tiles only

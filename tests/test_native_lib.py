@@ -69,6 +69,8 @@ def test_version_and_backend():
 def instantiated_kernels():
     src = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
     names = {f"fg_fft_n{m.group(1)}" for m in re.finditer(r"^FG_STOCKHAM\((\d+),", src, flags=re.M)}
+    # 8192 / 16384 points: 32 elements per thread, exchanges in halves
+    names |= {f"fg_fft_n{m.group(1)}" for m in re.finditer(r"^FG_STOCKHAM_HALVES\((\d+)\)", src, flags=re.M)}
     names |= {f"{n}_split" for n in names}
     names |= {f"fg_fft_n{m.group(1)}_sc" for m in re.finditer(r"^FG_STOCKHAM_SC\((\d+),", src, flags=re.M)}
     for m in re.finditer(r"^FG_STOCKHAM_LAT\((\d+),", src, flags=re.M):
@@ -91,7 +93,7 @@ def planned_kernels():
     from test_multipass_model import plan_kernel_names
     from test_stockham_model import LATENCY_GEOM
 
-    names = {f"fg_fft_n{l}" for l in range(2, 13)} | {f"fg_fft_n{l}_split" for l in range(2, 13)}
+    names = {f"fg_fft_n{l}" for l in range(2, 15)} | {f"fg_fft_n{l}_split" for l in range(2, 15)}
     names |= {f"fg_fft_n{l}_lat{sfx}" for l in LATENCY_GEOM for sfx in ("", "_split")}
     for cached in (False, True):
         for log_n in range(13, 25):

@@ -21,6 +21,10 @@ from conftest import rel_l2, uniform_c64
 # kStockham in fft_plan.cpp / FG_STOCKHAM in fft_kernels.hip: (log_e, fpb)
 GEOM = {2: (2, 64), 3: (3, 64), 4: (3, 32), 5: (3, 16), 6: (2, 4), 7: (3, 4), 8: (4, 4),
         9: (4, 2), 10: (4, 2), 11: (4, 1), 12: (4, 1)}
+# kStockham entries of the 32-element kernels with the exchanges in halves
+# (FG_STOCKHAM_HALVES, one transform per workgroup; modelled in
+# test_tile_halves_model.py)
+HALVES_GEOM = {13: (5, 1), 14: (5, 1)}
 # kStockhamLatency / FG_STOCKHAM_LAT: single-pass plans too small to fill the GPU
 LATENCY_GEOM = {8: (2, 1), 10: (3, 1), 12: (3, 1)}
 
@@ -30,6 +34,11 @@ def row_exponents(r):
     return [1, 2, 3, 4, 8, 12] if r == 16 else [1, 2, 3, 4] if r == 8 else list(range(r))
 
 
+def two_level(L):
+    """A stage spanning L >= 1024 stores W^{64 h} (h < L/64), then W^l (l < 64)."""
+    return L >= 1024
+
+
 def stockham_table(log_n, log_e):
     nfull, rem = divmod(log_n, log_e)
     nst = nfull + (1 if rem else 0)
@@ -37,6 +46,11 @@ def stockham_table(log_n, log_e):
     for s in range(1, nst):
         logl, logr = s * log_e, (log_e if s < nfull else rem)
         L, R = 1 << logl, 1 << logr
+        if two_level(L):
+            e = np.concatenate([(64 * np.arange(L // 64)) % (L * R), np.arange(64)])
+            out.append(np.exp(-2j * np.pi * e / (L * R)).astype(np.complex64))
+            offs.append(offs[-1] + L // 64 + 64)
+            continue
         ps = np.array(row_exponents(R))
         k, p = np.meshgrid(np.arange(L), ps, indexing="ij")
         e = (p * k) % (L * R)
@@ -45,10 +59,21 @@ def stockham_table(log_n, log_e):
     return (np.concatenate(out) if out else np.ones(1, np.complex64)), offs
 
 
-def stage_twiddles(tw, off, k, r):
+def stage_twiddles(tw, off, k, r, L=None):
     """(T, r) twiddles W^{p*k} as the kernel forms them from the table rows at
     off + k * row_len: a stored entry, or for radix 16 / 8 the product
-    W^{k*(p & 3)} * W^{k*4*(p >> 2)} of two stored entries."""
+    W^{k*(p & 3)} * W^{k*4*(p >> 2)} of two stored entries.  A two-level stage
+    (L >= 1024, radix 2 or 4) forms W^k = A[k >> 6] * B[k & 63] and its powers
+    by f32 products, as apply_stage_twiddles_at does."""
+    if L is not None and two_level(L):
+        assert r in (2, 4)
+        a, b = tw[off + (k >> 6)], tw[off + L // 64 + (k & 63)]
+        w1 = (a * b).astype(np.complex64)
+        cols = [np.ones(k.shape, np.complex64), w1]
+        if r == 4:
+            w2 = (w1 * w1).astype(np.complex64)
+            cols += [w2, (w2 * w1).astype(np.complex64)]
+        return np.stack(cols, axis=1).astype(np.complex128)
     ps = row_exponents(r)
     rows = tw[off + k[:, None] * len(ps) + np.arange(len(ps))[None, :]].astype(np.complex128)
     if r not in (8, 16):
@@ -88,8 +113,9 @@ def model(x, log_n, log_e, sh=4):
             b = t + t_per * i
             k = b & (L - 1)
             if L > 1:
-                w = stage_twiddles(tw, offs[s], k, r)
-                assert offs[s] + (k.max() + 1) * len(row_exponents(r)) <= offs[s + 1] <= tw.size
+                w = stage_twiddles(tw, offs[s], k, r, L)
+                used = (L // 64 + 64) if two_level(L) else (k.max() + 1) * len(row_exponents(r))
+                assert offs[s] + used <= offs[s + 1] <= tw.size
                 u = u * w[None, :, :]
             y = np.fft.fft(u, axis=2)
             j = b >> (s * log_e)
@@ -148,15 +174,18 @@ def test_twiddle_rows_are_16_byte_aligned():
 
 def test_factored_twiddles_equal_the_full_rows():
     # the products the kernel forms reproduce W^{p*k} for every p (to f32 rounding)
-    for log_n, log_e in [(12, 4), (11, 4), (10, 4), (9, 3), (12, 3)]:
+    for log_n, log_e in [(12, 4), (11, 4), (10, 4), (9, 3), (12, 3), (13, 4), (14, 4)]:
         tw, offs = stockham_table(log_n, log_e)
         nfull, rem = divmod(log_n, log_e)
         for s in range(1, nfull + (1 if rem else 0)):
             L, R = 1 << (s * log_e), 1 << (log_e if s < nfull else rem)
             k = np.arange(L)
-            w = stage_twiddles(tw, offs[s], k, R)
+            w = stage_twiddles(tw, offs[s], k, R, L)
             exact = np.exp(-2j * np.pi * ((k[:, None] * np.arange(R)[None, :]) % (L * R)) / (L * R))
-            assert np.max(np.abs(w - exact)) < 3e-7, (log_n, s)
+            # stored or one product: 3e-7; two-level (W^k from two entries, then
+            # W^2k and W^3k as products): up to five f32 roundings, 6e-7
+            tol = 6e-7 if two_level(L) else 3e-7
+            assert np.max(np.abs(w - exact)) < tol, (log_n, s)
 
 
 def test_stage_table_sizes():
@@ -166,6 +195,19 @@ def test_stage_table_sizes():
     # N = 1024 (16, 16, 4): 16 rows of 6, then 256 full rows of 4
     _, offs = stockham_table(10, 4)
     assert offs == [0, 0, 96, 96 + 1024]
+    # N = 16384 (16, 16, 16, 4): the last stage (L = 4096) is two-level, 64 + 64
+    # entries instead of 4096 rows of 4
+    tw, offs = stockham_table(14, 4)
+    assert offs == [0, 0, 96, 96 + 1536, 96 + 1536 + 128] and tw.size == offs[-1]
+    # no stage of the kernels up to 4096 points is two-level (their tables are
+    # unchanged): the single-pass geometries, the tile passes (log_e 4, up to
+    # 4096 points) and the one-pass 2D kernels (log_e 3 or 4, up to 1024 points)
+    geoms = set(GEOM.items()) | set(LATENCY_GEOM.items())
+    geoms = {(n, g[0]) for n, g in geoms} | {(n, 4) for n in range(4, 13)} | \
+        {(n, e) for n in range(4, 11) for e in (3, 4)}
+    for log_n, log_e in geoms:
+        nstages = log_n // log_e + (1 if log_n % log_e else 0)
+        assert all(not two_level(1 << (s * log_e)) for s in range(1, nstages)), (log_n, log_e)
 
 
 def test_staged_block_mapping_covers_each_element_once():
@@ -205,7 +247,9 @@ def test_geometry_tables_match_the_sources():
         body = re.sub(r"//[^\n]*", "", body)
         return [tuple(int(v) for v in m) for m in re.findall(r"\{(\d+), (\d+)\}", body)]
 
-    assert {n: g for n, g in enumerate(table("kStockham")) if g != (0, 0)} == GEOM
+    assert {n: g for n, g in enumerate(table("kStockham")) if g != (0, 0)} == {**GEOM, **HALVES_GEOM}
+    halves = {int(a): (5, 1) for a in re.findall(r"^FG_STOCKHAM_HALVES\((\d+)\)", hip, flags=re.M)}
+    assert halves == HALVES_GEOM
     assert {n: g for n, g in enumerate(table("kStockhamLatency")) if g != (0, 0)} == LATENCY_GEOM
     inst = {int(a): (int(b), int(c)) for a, b, c in re.findall(r"^FG_STOCKHAM\((\d+), (\d+), (\d+)\)", hip, flags=re.M)}
     assert inst == GEOM

@@ -101,6 +101,92 @@ def halves_model(cols, log_l):
     return res
 
 
+def row_halves_model(lanes, log_n):
+    """The single-pass 8192 / 16384-point kernel (fft_row_halves_body): the same
+    stages on one contiguous transform per workgroup, the LDS holding L/2
+    positions with one pad slot per 16 (lds_pos); lanes: (B, L) complex."""
+    b_, n = lanes.shape
+    T, half = n // E, n // 2
+    tw, offs = stockham_table(log_n, 4)
+    t = np.arange(T)
+    natural = t[:, None] + T * np.arange(E)[None, :]
+    regs = lanes.astype(np.complex128)[:, natural]
+    rs = radices(log_n)
+    slots = half + half // 16
+    L = 1
+    for s, R in enumerate(rs):
+        NB = E // R
+        out = np.empty_like(regs)
+        dst = np.empty((T, E), dtype=np.int64)
+        for i in range(NB):
+            u = regs[:, :, [i + NB * p for p in range(R)]]
+            b = t + T * i
+            k = b & (L - 1)
+            if L > 1:
+                u = u * stage_twiddles(tw, offs[s], k, R, L)[None, :, :]
+            y = np.fft.fft(u, axis=2)
+            j = b // L
+            for q in range(R):
+                out[:, :, i + NB * q] = y[:, :, q]
+                dst[:, i + NB * q] = j * L * R + k + q * L
+        assert np.array_equal(np.sort(dst.reshape(-1)), np.arange(n))
+        if s + 1 == len(rs):
+            assert np.array_equal(dst, natural)
+            regs = out
+            break
+        assert R == 16
+        new = np.empty_like(regs)
+        for h in range(2):
+            lds = np.zeros((b_, slots), np.complex128)
+            written = np.zeros(slots, dtype=bool)
+            for i in range(h * NB // 2, (h + 1) * NB // 2):
+                b = t + T * i
+                for q in range(R):
+                    d = dst[:, i + NB * q]
+                    assert np.all((d >= half * h) & (d < half * (h + 1))), (log_n, s, i, q)
+                    # the kernel's slot: stage 0 writes 17 * (b - HALF/16 * h) + q,
+                    # later stages lds_pos(d0) + q * (L + L/16)
+                    if L == 1:
+                        idx = 17 * (b - (half // 16) * h) + q
+                    else:
+                        d0 = (b >> (4 * s)) * L * 16 + (b & (L - 1)) - half * h
+                        idx = d0 + (d0 >> 4) + q * (L + L // 16)
+                    assert np.array_equal(idx, (d - half * h) + ((d - half * h) >> 4))
+                    assert idx.max() < slots and not written[idx].any()
+                    written[idx] = True
+                    lds[:, idx] = out[:, :, i + NB * q]
+            assert written.sum() == half
+            for m in range(E // 2):
+                idx = (t + t // 16) + m * (T + T // 16)
+                assert np.array_equal(idx, (t + T * m) + ((t + T * m) >> 4))
+                assert written[idx].all()
+                new[:, :, (E // 2) * h + m] = lds[:, idx]
+        regs = new
+        L *= R
+    res = np.empty((b_, n), np.complex128)
+    res[:, natural] = regs
+    return res
+
+
+@pytest.mark.parametrize("log_n", [13, 14])
+def test_row_halves_model_matches_oracle(log_n):
+    rng = np.random.default_rng(log_n)
+    n = 1 << log_n
+    lanes = uniform_c64(rng, 2 * n).reshape(2, n)
+    got = row_halves_model(lanes, log_n)
+    want = oracle.fft_1d(lanes.reshape(-1), log_n).reshape(2, n)
+    assert rel_l2(got, want) < 1e-5
+
+
+@pytest.mark.parametrize("log_n", [13, 14])
+def test_row_halves_fit_the_hardware(log_n):
+    # N/32 threads (at most 1024), N/2 + N/32 LDS slots, at least two workgroups per CU
+    n = 1 << log_n
+    assert n // E <= 1024
+    lds = (n // 2 + n // 32) * 8
+    assert 2 * lds <= 160 * 1024, lds
+
+
 # (log_l, G): the instantiated kernels (FG_TILE_HALVES), the widths of the
 # passes that read HBM
 CASES = [(7, 64), (8, 32), (9, 16), (10, 16)]
