@@ -5,7 +5,8 @@ Default workload (the one the north-star target is quoted
 on): batched 1D forward C2C complex64 FFT, N = 1024, batch = 65536 (512 MiB in,
 512 MiB out), re/im iid N(0,1) from seed 3, device-resident buffers.
 `--workload` selects the other BASELINE configurations (cfg1, cfg2_256,
-cfg2_4096, cfg4, cfg5), 2D images on the one-pass path (2d_64, 2d_128: 512 MiB
+cfg2_4096, cfg4, cfg5), 1D lengths 8192 / 16384 on the single-pass path (1d_8192,
+1d_16384: 512 MiB batches), 2D images on the one-pass path (2d_64, 2d_128: 512 MiB
 batches of 64x64 / 128x128 images) and the operations beside the path (cfg3_split: config 3
 in the split layout; cmul, cmul_split, deinterleave, interleave: the pointwise
 kernels over config 3's 2^26 elements; transpose: an 8192 x 8192 complex64
@@ -61,6 +62,10 @@ FFT_WORKLOADS = {
              "1D forward C2C FFT N=2^24 batch=4 complex64, re/im iid N(0,1) seed 4"),
     "cfg5": (2, 12, 2, 5, "uniform", [("forward", False)], "interleaved",
              "2D forward C2C FFT 4096x4096 batch=2 complex64, re/im iid U[-1,1) seed 5"),
+    "1d_8192": (1, 13, 8192, 8, "normal", [("forward", False)], "interleaved",
+                "1D forward C2C FFT N=8192 batch=8192 complex64 (single pass), re/im iid N(0,1) seed 8"),
+    "1d_16384": (1, 14, 4096, 9, "normal", [("forward", False)], "interleaved",
+                 "1D forward C2C FFT N=16384 batch=4096 complex64 (single pass), re/im iid N(0,1) seed 9"),
     "2d_64": (2, 6, 16384, 6, "uniform", [("forward", False)], "interleaved",
               "2D forward C2C FFT 64x64 batch=16384 complex64 (one-pass path), re/im iid U[-1,1) seed 6"),
     "2d_128": (2, 7, 4096, 7, "uniform", [("forward", False)], "interleaved",
@@ -555,8 +560,7 @@ def clock_ramp(N, dev, wl, stream, ramp_ms: float):
     step of the workload and not timed; reported in the JSON line."""
     if ramp_ms <= 0:
         return None
-    src, dst, nbytes = wl.copy_bufs
-    nbytes = min(nbytes, 256 << 20)
+    src, dst, nbytes = wl.copy_bufs   # the yardstick's own size: every fg_copy_f4 dispatch moves the same bytes
     t0 = time.perf_counter()
     copies = 0
     while (time.perf_counter() - t0) * 1e3 < ramp_ms:
@@ -586,6 +590,16 @@ def steady_state(np, per_kernel, dominant_key: str, graph: bool):
             "pre_ramp": bool(ratio is not None and ratio > 1.02)}
 
 
+def gate_check(result, min_frac):
+    """The throughput gate of --min-frac: None without one, else whether the
+    dominant kernel's roofline fraction reached it."""
+    if min_frac is None:
+        return None
+    frac = result["roofline"]["frac"]
+    return {"min_frac": min_frac, "frac": frac, "kernel": result["roofline"]["kernel"],
+            "passed": bool(frac >= min_frac)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -601,6 +615,10 @@ def main() -> int:
     ap.add_argument("--ramp-ms", type=float, default=40.0,
                     help="before the warmup steps, run the plain copy kernel for this long (wall ms) so "
                          "that the shader clock leaves its idle level; reported as clock_ramp, 0 = off")
+    ap.add_argument("--min-frac", type=float, default=None, metavar="F",
+                    help="throughput gate: after printing the JSON line, exit with status 3 if the dominant "
+                         "kernel's roofline fraction is below F (the reference's perf-gate, "
+                         "crates/ferrum-gpu-bench/src/bin/perf-gate.rs, gates a ratio the same way)")
     ap.add_argument("--graph", type=int, default=0, metavar="G",
                     help="record G steps into one HIP graph and time replays of it (for launch-bound "
                          "workloads); --steps must be a multiple of G.  0: one host launch per kernel")
@@ -777,7 +795,13 @@ def main() -> int:
     else:
         result["launch_mode"] = "one host launch per kernel, one event after each"
 
+    gate = gate_check(result, args.min_frac)
+    if gate is not None:
+        result["gate"] = gate
     print(json.dumps(result), flush=True)
+    if gate is not None and not gate["passed"]:
+        print(f"bench.py: gate failed: roofline frac {gate['frac']} < {gate['min_frac']}", file=sys.stderr)
+        return 3
     return 0
 
 

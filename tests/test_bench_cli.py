@@ -65,3 +65,21 @@ def test_clock_sampler_without_sysfs_reports_nothing():
     with c:
         pass
     assert c.report() is None
+
+
+def test_throughput_gate():
+    # --min-frac: the JSON line carries the gate; the exit status fails it
+    import bench
+
+    res = {"roofline": {"frac": 0.7643, "kernel": "fg_fft_n10"}}
+    assert bench.gate_check(res, None) is None
+    assert bench.gate_check(res, 0.70) == {"min_frac": 0.70, "frac": 0.7643, "kernel": "fg_fft_n10", "passed": True}
+    assert bench.gate_check(res, 0.80)["passed"] is False
+
+
+def test_single_pass_workloads():
+    import bench
+
+    for name, log_n, batch in (("1d_8192", 13, 8192), ("1d_16384", 14, 4096)):
+        dims, ln, b, *_ = bench.FFT_WORKLOADS[name]
+        assert (dims, ln, b) == (1, log_n, batch) and b << ln == 1 << 26   # 512 MiB
