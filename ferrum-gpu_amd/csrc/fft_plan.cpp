@@ -114,6 +114,19 @@ std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e) {
     return t;
 }
 
+std::vector<Cf32> fft1024_x2_twiddles() {
+    auto w = [](uint64_t M, uint64_t e) {
+        const double a = 2.0 * M_PI * (double)(e % M) / (double)M;
+        return Cf32{(float)cos(a), (float)-sin(a)};
+    };
+    std::vector<Cf32> t;
+    for (uint64_t k = 0; k < 8; ++k)
+        for (uint64_t p : {1, 2, 3, 4, 8, 12}) t.push_back(w(128, p * k));
+    for (uint64_t k = 0; k < 128; ++k)
+        for (uint64_t p : {1, 2, 3, 4}) t.push_back(w(1024, p * k));
+    return t;
+}
+
 std::vector<Cf32> big_twiddles() {
     std::vector<Cf32> t(8192);
     for (int j = 0; j < 4096; ++j) {
@@ -235,11 +248,12 @@ std::string tile_name(uint32_t log_l, uint32_t g, char kind, const char* policy)
 
 const void* FftPlan::stage_table(uint32_t log_l, uint32_t log_e) {
     // One table per (length, elements per thread): the radix list, and so the
-    // table, depends on both.
+    // table, depends on both.  log_e == kX2Layout: the 8 * 16 * 8 list of the
+    // two-transform 1024-point kernel.
     const uint32_t key = log_l * 64 + log_e;
     for (auto& e : stage_tables_)
         if (e.first == key) return e.second.data();
-    auto tw = stockham_twiddles(log_l, log_e);
+    auto tw = log_e == kX2Layout ? fft1024_x2_twiddles() : stockham_twiddles(log_l, log_e);
     Buffer<Cf32, HipBackend> b = dev_->alloc<Cf32>(tw.size());
     b.copy_from_host(tw.data(), tw.size());
     stage_tables_.emplace_back(key, std::move(b));
@@ -274,8 +288,9 @@ void FftPlan::add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64
     s.fpb = g.fpb;
     s.src = src;
     s.dst = dst;
-    // 32-element kernels (log_e 5) run the radix-16 list of the 16-element layout.
-    s.tw = stage_table(log_l, std::min<uint32_t>(g.log_e, 4));
+    // 32-element kernels (log_e 5) run the radix-16 list of the 16-element
+    // layout; the 1024-point throughput kernels the 8 * 16 * 8 list.
+    s.tw = (log_l == 10 && !latency) ? stage_table(10, kX2Layout) : stage_table(log_l, std::min<uint32_t>(g.log_e, 4));
     s.per_unit = per_unit;
     steps_.push_back(s);
 }

@@ -169,6 +169,13 @@ private:
 // remaining exponents as products; kernels/fft_stockham.hpp).  A stage with
 // L >= 1024 stores the two-level block W^{64 h} (h < L/64), W^l (l < 64).
 std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e);
+// Stage table of the 1024-point throughput kernels (fg_fft_n10, _split, _sc;
+// radix list 8 * 16 * 8, kernels/fft_stockham.hpp fft1024_x2_body): rows
+// k < 8 of W_128^{p k}, p in {1,2,3,4,8,12}, then rows k < 128 of
+// W_1024^{p k}, p in {1,2,3,4}.
+std::vector<Cf32> fft1024_x2_twiddles();
+// stage_table key for that layout (in place of elements per thread).
+constexpr uint32_t kX2Layout = 63;
 // Two-level root table: [j] = W_4096^j, [4096 + j] = W_{2^24}^j, j < 4096.
 std::vector<Cf32> big_twiddles();
 // Digit split (log2 sizes, slowest digit first) of a 1D length 2^log_n > 16384.

@@ -51,7 +51,27 @@ FG_STOCKHAM(6, 2, 4)     // N=64:   16 threads (4 elements each)
 FG_STOCKHAM(7, 3, 4)     // N=128:  16 threads (8 elements each)
 FG_STOCKHAM(8, 4, 4)     // N=256:  16 threads
 FG_STOCKHAM(9, 4, 2)     // N=512:  32 threads
-FG_STOCKHAM(10, 4, 2)    // N=1024: 64 threads (one wave) per transform, 2 per workgroup
+// N=1024: two transforms per 128-thread workgroup, radix list 8 * 16 * 8
+// (fft1024_x2_body): fg_fft_n10, its split twin and the cached-store variant
+// fg_fft_n10_sc share the body, so they give the same bits.
+#define FG_STOCKHAM_X2_1024()                                                                        \
+    extern "C" __global__ __launch_bounds__(128) void fg_fft_n10(                                   \
+        const float2* __restrict__ in, float2* __restrict__ out, const float2* __restrict__ tw,      \
+        uint64_t batch, float scale, uint32_t flags) {                                              \
+        fft1024_x2_body(InterleavedIO{in, out}, tw, batch, scale, flags);                           \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(128) void fg_fft_n10_split(                             \
+        const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ out_re, \
+        float* __restrict__ out_im, const float2* __restrict__ tw, uint64_t batch, float scale,     \
+        uint32_t flags) {                                                                           \
+        fft1024_x2_body(SplitIO{in_re, in_im, out_re, out_im}, tw, batch, scale, flags);            \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(128) void fg_fft_n10_sc(                                \
+        const float2* __restrict__ in, float2* __restrict__ out, const float2* __restrict__ tw,      \
+        uint64_t batch, float scale, uint32_t flags) {                                              \
+        fft1024_x2_body(InterleavedIOT<false, true>{in, out}, tw, batch, scale, flags);             \
+    }
+FG_STOCKHAM_X2_1024()
 FG_STOCKHAM(11, 4, 1)    // N=2048: 128 threads
 FG_STOCKHAM(12, 4, 1)    // N=4096: 256 threads
 // N = 8192 / 16384: one transform per workgroup of N/32 threads with 32
@@ -102,7 +122,6 @@ FG_STOCKHAM_SC(6, 2, 4)
 FG_STOCKHAM_SC(7, 3, 4)
 FG_STOCKHAM_SC(8, 4, 4)
 FG_STOCKHAM_SC(9, 4, 2)
-FG_STOCKHAM_SC(10, 4, 2)
 FG_STOCKHAM_SC(11, 4, 1)
 FG_STOCKHAM_SC(12, 4, 1)
 

@@ -71,7 +71,13 @@ def instantiated_kernels():
     names = {f"fg_fft_n{m.group(1)}" for m in re.finditer(r"^FG_STOCKHAM\((\d+),", src, flags=re.M)}
     # 8192 / 16384 points: 32 elements per thread, exchanges in halves
     names |= {f"fg_fft_n{m.group(1)}" for m in re.finditer(r"^FG_STOCKHAM_HALVES\((\d+)\)", src, flags=re.M)}
+    # 1024 points: two transforms per workgroup, radix list 8 * 16 * 8 (with its _sc variant)
+    x2 = re.search(r"^FG_STOCKHAM_X2_1024\(\)", src, flags=re.M) is not None
+    if x2:
+        names.add("fg_fft_n10")
     names |= {f"{n}_split" for n in names}
+    if x2:
+        names.add("fg_fft_n10_sc")
     names |= {f"fg_fft_n{m.group(1)}_sc" for m in re.finditer(r"^FG_STOCKHAM_SC\((\d+),", src, flags=re.M)}
     for m in re.finditer(r"^FG_STOCKHAM_LAT\((\d+),", src, flags=re.M):
         names |= {f"fg_fft_n{m.group(1)}_lat", f"fg_fft_n{m.group(1)}_lat_split"}

@@ -21,6 +21,10 @@ from conftest import rel_l2, uniform_c64
 # kStockham in fft_plan.cpp / FG_STOCKHAM in fft_kernels.hip: (log_e, fpb)
 GEOM = {2: (2, 64), 3: (3, 64), 4: (3, 32), 5: (3, 16), 6: (2, 4), 7: (3, 4), 8: (4, 4),
         9: (4, 2), 10: (4, 2), 11: (4, 1), 12: (4, 1)}
+# kStockham[10] = {4, 2} launches the 1024-point kernel with two transforms per
+# 128-thread workgroup and the radix list 8 * 16 * 8 (FG_STOCKHAM_X2_1024;
+# modelled in test_x2_model.py); GEOM keeps it for the launch shape.
+X2_GEOM = {10: (4, 2)}
 # kStockham entries of the 32-element kernels with the exchanges in halves
 # (FG_STOCKHAM_HALVES, one transform per workgroup; modelled in
 # test_tile_halves_model.py)
@@ -252,6 +256,8 @@ def test_geometry_tables_match_the_sources():
     assert halves == HALVES_GEOM
     assert {n: g for n, g in enumerate(table("kStockhamLatency")) if g != (0, 0)} == LATENCY_GEOM
     inst = {int(a): (int(b), int(c)) for a, b, c in re.findall(r"^FG_STOCKHAM\((\d+), (\d+), (\d+)\)", hip, flags=re.M)}
+    if re.search(r"^FG_STOCKHAM_X2_1024\(\)", hip, flags=re.M):
+        inst.update(X2_GEOM)
     assert inst == GEOM
     lat = {int(a): (int(b), 1) for a, b in re.findall(r"^FG_STOCKHAM_LAT\((\d+), (\d+)\)", hip, flags=re.M)}
     assert lat == LATENCY_GEOM
