@@ -587,6 +587,9 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
 
 void FftPlan::check_split(const void* in_re, const void* in_im, const void* out_re, const void* out_im) const {
     if (!in_re || !in_im || !out_re || !out_im) invalid("fft exec_split: null buffer");
+    if ((reinterpret_cast<uintptr_t>(in_re) | reinterpret_cast<uintptr_t>(in_im) | reinterpret_cast<uintptr_t>(out_re) |
+         reinterpret_cast<uintptr_t>(out_im)) & 3u)
+        invalid("fft exec_split: arrays must be 4-byte aligned (f32)");
     const uint64_t nb = 4ull * elems() * batch_;
     auto overlap = [nb](const void* a, const void* b) {
         const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);

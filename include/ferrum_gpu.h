@@ -255,7 +255,8 @@ FG_API int fg_transpose_c64(fg_device_t dev, const void *d_in, void *d_out, uint
  * (the reference's fft_c2c_{256_r16s,1024,4096_4step_reg}_split kernels,
  * crates/ferrum-gpu-fft-kernels/src/kernels_body.rs:509-626, 986-1130,
  * 1463-1610, for every plan).  Same results as fg_fft_exec on the interleaved
- * data.  d_out_re / d_out_im may equal d_in_re / d_in_im; no other overlap.
+ * data.  Each array 4-byte aligned (FG_ERR_INVALID_ARGUMENT otherwise);
+ * d_out_re / d_out_im may equal d_in_re / d_in_im; no other overlap.
  * Single-pass plans (1D, N <= 16384; 2D images of up to 16384 points) run one
  * launch; other plans stage through an interleaved buffer the plan allocates
  * at its first split call (synchronously: that first call is refused with
