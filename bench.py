@@ -389,7 +389,7 @@ class OpWorkload:
             self.d_in[0].copy_from_host(a)
             self.d_out = [DeviceBuffer(dev, 8 * n)]
             self.algo_bytes = 16 * n
-            kernel = "fg_transpose_c64"
+            kernel = "fg_transpose_c64_t128"   # 128 x 128 tiles for sides of at least 128
         self.kernels = [kernel]
         self.launch_names = [kernel]
         self.launch_keys = [f"0:{kernel}"]

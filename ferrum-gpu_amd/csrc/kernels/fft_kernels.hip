@@ -175,6 +175,60 @@ extern "C" __global__ __launch_bounds__(256) void fg_transpose_c64(const float2*
     }
 }
 
+// The same transpose for matrices of at least 128 x 128: 128 x 128 tiles
+// (1024 threads, 132 KB of LDS, pitch 129), each global read and write a
+// 1 KB row piece, and the tiles walked in super-tiles of sc x sr tiles
+// (8 x 8, fewer along a dimension with fewer tiles), tile column fastest
+// inside a super-tile and super-tiles row-major, so the workgroups in flight
+// cover a square region of both the input and the output.  On an 8192 x 8192
+// matrix this moved 6.1 TB/s against 4.4 TB/s for the 64 x 64 tiles in row
+// order (copy probes and the kernel itself).  Grid = image blocks * batch,
+// image blocks = ceil(tiles_c / sc) sc * ceil(tiles_r / sr) sr; blocks past
+// the last tile of a row or column of tiles exit at once.
+extern "C" __global__ __launch_bounds__(1024) void fg_transpose_c64_t128(
+    const float2* __restrict__ in, float2* __restrict__ out, uint32_t rows, uint32_t cols, uint32_t tiles_c,
+    uint32_t tiles_r, uint32_t sc, uint32_t sr, uint32_t supers_c, uint32_t image_blocks) {
+    __shared__ float2 tile[128][129];
+    const uint32_t b = blockIdx.x % image_blocks;
+    const uint64_t img = (uint64_t)(blockIdx.x / image_blocks) * rows * cols;
+    const uint32_t per = sc * sr, sb = b / per, k = b % per;
+    const uint32_t tc = (sb % supers_c) * sc + k % sc, tr = (sb / supers_c) * sr + k / sc;
+    if (tc >= tiles_c || tr >= tiles_r) return;  // whole workgroup, before any barrier
+    const uint32_t tx = threadIdx.x & 127, ty = threadIdx.x >> 7;
+    const uint32_t c = tc * 128 + tx;
+    // Interior tiles (every tile of a matrix whose sides are multiples of 128)
+    // issue all sixteen loads, then all sixteen stores, with no per-element
+    // test; edge tiles test each element.
+    const bool full = (tr + 1) * 128 <= rows && (tc + 1) * 128 <= cols;
+    if (full) {
+        float2 v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = load_stream(in + img + (uint64_t)(tr * 128 + ty + 8 * i) * cols + c);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tile[ty + 8 * i][tx] = v[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t r = tr * 128 + ty + 8 * i;
+            if (r < rows && c < cols) tile[ty + 8 * i][tx] = load_stream(in + img + (uint64_t)r * cols + c);
+        }
+    }
+    __syncthreads();
+    const uint32_t ocol = tr * 128 + tx;  // output column = input row
+    if (full) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            store_stream(out + img + (uint64_t)(tc * 128 + ty + 8 * i) * rows + ocol, tile[tx][ty + 8 * i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t orow = tc * 128 + ty + 8 * i;  // output row = input column
+            if (orow < cols && ocol < rows)
+                store_stream(out + img + (uint64_t)orow * rows + ocol, tile[tx][ty + 8 * i]);
+        }
+    }
+}
+
 // c = a + b over n floats: the substrate smoke kernel (the reference's
 // hand-written vector_add, examples/vector-add/src/main.rs:17-60).
 extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __restrict__ a,

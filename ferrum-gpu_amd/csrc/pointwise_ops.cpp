@@ -1,6 +1,8 @@
 // pointwise_ops.cpp -- see pointwise_ops.hpp.
 #include "pointwise_ops.hpp"
 
+#include <algorithm>
+
 #include <initializer_list>
 #include <string>
 
@@ -50,6 +52,7 @@ Pointwise::Pointwise(const HipBackend::Module& mod) {
     }
     fill_ = HipBackend::get_kernel(mod, "fg_fill_c64");
     transpose_ = HipBackend::get_kernel(mod, "fg_transpose_c64");
+    transpose128_ = HipBackend::get_kernel(mod, "fg_transpose_c64_t128");
     copy_ = HipBackend::get_kernel(mod, "fg_copy_f4");
 }
 
@@ -125,6 +128,19 @@ void Pointwise::transpose_c64(const HipBackend::DeviceHandle& dev, const void* i
     if (rows == 0 || cols == 0 || batch == 0) invalid("transpose: rows, cols and batch must be positive");
     const uint64_t nb = 8ull * rows * cols * batch;
     if (overlap(in, nb, out, nb)) invalid("transpose: in and out must not overlap");
+    if (rows >= 128 && cols >= 128) {
+        // 128 x 128 tiles walked in super-tiles of up to 8 x 8 (fg_transpose_c64_t128)
+        const uint32_t tc = (cols + 127) / 128, tr = (rows + 127) / 128;
+        const uint32_t sc = std::min<uint32_t>(8, tc), sr = std::min<uint32_t>(8, tr);
+        const uint32_t supers_c = (tc + sc - 1) / sc, supers_r = (tr + sr - 1) / sr;
+        const uint64_t image_blocks = (uint64_t)supers_c * sc * supers_r * sr;
+        if (image_blocks * batch > 0x7fffffffull) invalid("transpose: too many tiles for one launch");
+        uint32_t ib = (uint32_t)image_blocks;
+        void* args[] = {(void*)&in, &out, &rows, &cols, (void*)&tc, (void*)&tr, (void*)&sc, (void*)&sr,
+                        (void*)&supers_c, &ib};
+        HipBackend::launch(dev, stream, transpose128_, Dim3((uint32_t)(image_blocks * batch)), Dim3(1024), 0, args);
+        return;
+    }
     const uint32_t tc = (cols + 63) / 64, tr = (rows + 63) / 64;
     const uint64_t tiles = (uint64_t)tc * tr * batch;
     if (tiles > 0x7fffffffull) invalid("transpose: too many tiles for one launch");

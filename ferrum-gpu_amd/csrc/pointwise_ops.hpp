@@ -60,6 +60,7 @@ private:
     HipBackend::KernelHandle interleave_[2] = {nullptr, nullptr};
     HipBackend::KernelHandle fill_ = nullptr;
     HipBackend::KernelHandle transpose_ = nullptr;
+    HipBackend::KernelHandle transpose128_ = nullptr;
     HipBackend::KernelHandle copy_ = nullptr;
 };
 

@@ -103,8 +103,11 @@ def test_square_api_equals_rect_api(gpu_device):
     assert np.array_equal(a, b)
 
 
+# 64 x 64 tiles below 128 rows or columns; 128 x 128 tiles in super-tiles of
+# up to 8 x 8 above (full and partial super-tiles, ragged edge tiles, batches)
 @pytest.mark.parametrize("rows,cols,batch", [(64, 64, 1), (4096, 4096, 1), (1000, 37, 3), (1, 5000, 2),
-                                             (513, 1, 1), (128, 4096, 2)])
+                                             (513, 1, 1), (128, 4096, 2), (1100, 1300, 2), (129, 200, 3),
+                                             (8192, 136, 1), (300, 8192, 1), (127, 4096, 1)])
 def test_transpose_exact(gpu_device, rows, cols, batch):
     import ferrum_gpu
     from ferrum_gpu.hip import DeviceBuffer

@@ -123,7 +123,7 @@ def test_code_object_is_embedded_for_gfx950():
     data = open(N.LIB_PATH, "rb").read()
     assert data.count(b"\x7fELF") >= 2
     assert b"gfx950" in data
-    for k in sorted(instantiated_kernels()) + ["fg_copy_f4", "fg_vector_add", "fg_transpose_c64", "fg_fill_c64"] \
+    for k in sorted(instantiated_kernels()) + ["fg_copy_f4", "fg_vector_add", "fg_transpose_c64", "fg_transpose_c64_t128", "fg_fill_c64"] \
             + POINTWISE:
         assert k.encode() in data, k
 
