@@ -66,6 +66,8 @@ FFT_WORKLOADS = {
                 "1D forward C2C FFT N=8192 batch=8192 complex64 (single pass), re/im iid N(0,1) seed 8"),
     "1d_16384": (1, 14, 4096, 9, "normal", [("forward", False)], "interleaved",
                  "1D forward C2C FFT N=16384 batch=4096 complex64 (single pass), re/im iid N(0,1) seed 9"),
+    "1d_32768": (1, 15, 2048, 10, "normal", [("forward", False)], "interleaved",
+                 "1D forward C2C FFT N=32768 batch=2048 complex64 (single pass), re/im iid N(0,1) seed 10"),
     "2d_64": (2, 6, 16384, 6, "uniform", [("forward", False)], "interleaved",
               "2D forward C2C FFT 64x64 batch=16384 complex64 (one-pass path), re/im iid U[-1,1) seed 6"),
     "2d_128": (2, 7, 4096, 7, "uniform", [("forward", False)], "interleaved",

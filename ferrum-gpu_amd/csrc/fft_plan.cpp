@@ -29,11 +29,13 @@ struct StockhamGeom {
 // N = 16 .. 128 hold 4 or 8 elements per thread: 16 (the larger sizes' choice)
 // measured 217 / 232 / 234 / 211 us per 512 MiB batch against 182 / 183 / 171
 // / 173 us for the entries below (N = 256 .. 4096 measured best at 16).
-// N = 8192 / 16384 ({5, 1}): 32 elements per thread with the exchanges in
-// halves (fg_fft_n13 / fg_fft_n14, kernels/fft_stockham.hpp).
+// N = 8192 / 16384 / 32768 ({5, 1}): 32 elements per thread with the
+// exchanges in halves (fg_fft_n13 / n14 / n15, kernels/fft_stockham.hpp);
+// 32768 points run one 1024-thread, 136 KB workgroup per CU and measured
+// 270 us per 512 MiB against 352 us for the two tile passes they replace.
 constexpr StockhamGeom kStockham[kMaxLogNSingle + 1] = {
     {0, 0}, {0, 0},          // log_n 0, 1: unsupported
-    {2, 64}, {3, 64}, {3, 32}, {3, 16}, {2, 4}, {3, 4}, {4, 4}, {4, 2}, {4, 2}, {4, 1}, {4, 1}, {5, 1}, {5, 1},
+    {2, 64}, {3, 64}, {3, 32}, {3, 16}, {2, 4}, {3, 4}, {4, 4}, {4, 2}, {4, 2}, {4, 1}, {4, 1}, {5, 1}, {5, 1}, {5, 1},
 };
 // Latency geometry (fg_fft_n<L>_lat, one transform per workgroup, fewer
 // elements per thread: more threads per transform, shorter serial chains),
@@ -42,7 +44,7 @@ constexpr StockhamGeom kStockham[kMaxLogNSingle + 1] = {
 // N = 1024 3.94 -> 3.65 us, N = 4096 10.94 -> 10.69 us.
 constexpr StockhamGeom kStockhamLatency[kMaxLogNSingle + 1] = {
     {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0},
-    {2, 1}, {0, 0}, {3, 1}, {0, 0}, {3, 1}, {0, 0}, {0, 0},
+    {2, 1}, {0, 0}, {3, 1}, {0, 0}, {3, 1}, {0, 0}, {0, 0}, {0, 0},
 };
 
 // The code object named by FERRUM_GPU_CODE_OBJECT, read once per process (a
@@ -88,8 +90,9 @@ std::vector<Cf32> stockham_twiddles(uint32_t log_n, uint32_t log_e) {
         // for radix 16 and 8, full rows below.
         if (L >= 1024) {
             // Two-level block (kernels/fft_stockham.hpp, tw_two_level):
-            // W_M^{64 h} for h < L/64, then W_M^l for l < 64.
-            for (uint64_t h = 0; h < L / 64; ++h) {
+            // W_M^{64 h} for h < L/64 (radix 8: h < M/64, tw_two_level_high),
+            // then W_M^l for l < 64.
+            for (uint64_t h = 0; h < (R == 8 ? M : L) / 64; ++h) {
                 const double ang = 2.0 * M_PI * (double)((64 * h) % M) / (double)M;
                 t.push_back(Cf32{(float)cos(ang), (float)-sin(ang)});
             }

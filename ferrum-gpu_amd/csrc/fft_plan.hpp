@@ -35,8 +35,9 @@ KernelArtifact fft_code_object();
 
 // Supported shapes (the reference: 1D [2, 12], plan.rs:58; 2D [4, 12],
 // crates/ferrum-gpu-py/src/lib.rs:537).  1D is widened to 2^24: single-pass
-// up to 2^14 (the whole transform in one workgroup's LDS), multi-pass beyond.
-constexpr uint32_t kMinLogN1D = 2, kMaxLogN1D = 24, kMaxLogNSingle = 14;
+// up to 2^15 (the whole transform in one workgroup: its registers and LDS),
+// multi-pass beyond.
+constexpr uint32_t kMinLogN1D = 2, kMaxLogN1D = 24, kMaxLogNSingle = 15;
 constexpr uint32_t kMinLogN2D = 4, kMaxLogN2D = 12;
 
 class FftPlan {
@@ -178,7 +179,7 @@ std::vector<Cf32> fft1024_x2_twiddles();
 constexpr uint32_t kX2Layout = 63;
 // Two-level root table: [j] = W_4096^j, [4096 + j] = W_{2^24}^j, j < 4096.
 std::vector<Cf32> big_twiddles();
-// Digit split (log2 sizes, slowest digit first) of a 1D length 2^log_n > 16384.
+// Digit split (log2 sizes, slowest digit first) of a 1D length 2^log_n > 32768.
 std::vector<uint32_t> split_1d(uint32_t log_n);
 // Columns per tile for a pass of length 2^log_l that reads HBM.
 uint32_t tile_columns(uint32_t log_l);

@@ -165,6 +165,14 @@ struct InterleavedIOT {
     float2* out;
     __device__ __forceinline__ float2 load(uint64_t i) const { return gload<LOAD_CACHED>(in + i); }
     __device__ __forceinline__ void store(uint64_t i, float2 v) const { gstore<STORE_CACHED>(out + i, v); }
+    // Element row + lane with `row` the same for the whole wave: a scalar base
+    // plus a 32-bit lane offset, no 64-bit vector address per access.
+    __device__ __forceinline__ float2 load_row(uint64_t row, uint32_t lane) const {
+        return gload<LOAD_CACHED>(reinterpret_cast<const float2*>(reinterpret_cast<const char*>(in + row) + lane * 8u));
+    }
+    __device__ __forceinline__ void store_row(uint64_t row, uint32_t lane, float2 v) const {
+        gstore<STORE_CACHED>(reinterpret_cast<float2*>(reinterpret_cast<char*>(out + row) + lane * 8u), v);
+    }
 };
 using InterleavedIO = InterleavedIOT<false, false>;
 struct SplitIO {
@@ -178,6 +186,16 @@ struct SplitIO {
     __device__ __forceinline__ void store(uint64_t i, float2 v) const {
         store_stream(out_re + i, v.x);
         store_stream(out_im + i, v.y);
+    }
+    __device__ __forceinline__ float2 load_row(uint64_t row, uint32_t lane) const {
+        const uint32_t b = lane * 4u;
+        return make_float2(load_stream(reinterpret_cast<const float*>(reinterpret_cast<const char*>(in_re + row) + b)),
+                           load_stream(reinterpret_cast<const float*>(reinterpret_cast<const char*>(in_im + row) + b)));
+    }
+    __device__ __forceinline__ void store_row(uint64_t row, uint32_t lane, float2 v) const {
+        const uint32_t b = lane * 4u;
+        store_stream(reinterpret_cast<float*>(reinterpret_cast<char*>(out_re + row) + b), v.x);
+        store_stream(reinterpret_cast<float*>(reinterpret_cast<char*>(out_im + row) + b), v.y);
     }
 };
 

@@ -94,6 +94,7 @@ FG_STOCKHAM(12, 4, 1)    // N=4096: 256 threads
     }
 FG_STOCKHAM_HALVES(13)   // N=8192:  256 threads
 FG_STOCKHAM_HALVES(14)   // N=16384: 512 threads
+FG_STOCKHAM_HALVES(15)   // N=32768: 1024 threads, 136 KB of LDS
 // fg_fft_n<L>_lat[_split]: one transform per workgroup with fewer elements per
 // thread (kStockhamLatency in fft_plan.cpp), for batches too small to fill the
 // GPU; the split twin keeps split and interleaved results bit-identical.

@@ -62,8 +62,12 @@ __host__ __device__ constexpr int tw_row_len(int R) { return R == 16 ? 6 : (R ==
 // l < 64 (M = L*R), and forms W^k = A[k >> 6] * B[k & 63], W^{2k} = (W^k)^2,
 // W^{3k} = W^{2k} * W^k (up to five f32 roundings, under 6e-7).
 __host__ __device__ constexpr bool tw_two_level(int L) { return L >= 1024; }
+// Entries W^{64 h} of a two-level block: h < L/64 covers the exponents k < L
+// of radix 2 and 4 (their W^2k, W^3k are products of W^k); radix 8 looks up
+// W^2k and W^4k as well, so its block covers every exponent below L*R.
+__host__ __device__ constexpr int tw_two_level_high(int L, int R) { return R == 8 ? L * R / 64 : L / 64; }
 __host__ __device__ constexpr int tw_stage_entries(int L, int R) {
-    return tw_two_level(L) ? L / 64 + 64 : L * tw_row_len(R);
+    return tw_two_level(L) ? tw_two_level_high(L, R) + 64 : L * tw_row_len(R);
 }
 
 template <int LOGN, int LOGE>
@@ -114,9 +118,24 @@ __device__ __forceinline__ void apply_stage_twiddles(float2* u, const float2* __
 template <int R, int L>
 __device__ __forceinline__ void apply_stage_twiddles_at(float2* u, const float2* __restrict__ stage, int k) {
     if constexpr (tw_two_level(L)) {
-        static_assert(R == 2 || R == 4, "two-level stages are radix 2 or 4");
-        const float2 w1 = cmul(stage[k >> 6], stage[L / 64 + (k & 63)]);
+        static_assert(R == 2 || R == 4 || R == 8, "two-level stages are radix 2, 4 or 8");
+        constexpr int HI = tw_two_level_high(L, R);
+        const float2 w1 = cmul(stage[k >> 6], stage[HI + (k & 63)]);
         u[1] = cmul(u[1], w1);
+        if constexpr (R == 8) {
+            // W^2k and W^4k looked up too, the other powers one product away:
+            // at most three roundings from the table (2.4e-7 at 32768 points,
+            // against 7e-7 for W^7k by repeated products of W^k)
+            const float2 w2 = cmul(stage[(2 * k) >> 6], stage[HI + ((2 * k) & 63)]);
+            const float2 w4 = cmul(stage[(4 * k) >> 6], stage[HI + ((4 * k) & 63)]);
+            const float2 w3 = cmul(w1, w2);
+            u[2] = cmul(u[2], w2);
+            u[3] = cmul(u[3], w3);
+            u[4] = cmul(u[4], w4);
+            u[5] = cmul(u[5], cmul(w1, w4));
+            u[6] = cmul(u[6], cmul(w2, w4));
+            u[7] = cmul(u[7], cmul(w3, w4));
+        }
         if constexpr (R == 4) {
             const float2 w2 = cmul(w1, w1);
             u[2] = cmul(u[2], w2);
@@ -324,16 +343,17 @@ __device__ __forceinline__ void fft_stockham_body(const IO io, const float2* __r
 // i in [h*NB/2, (h+1)*NB/2), then each thread reads its elements
 // m in [16h, 16h + 16).  The last stage's outputs are the thread's own
 // positions t + T*m.  Used by the first pass of 1D multi-pass plans
-// (fft_tile.hpp, G columns per workgroup) and by the single-pass 8192- and
-// 16384-point transforms (fft_row_halves_body below): half the LDS of the
-// 16-element layout, so twice the workgroups per CU.
+// (fft_tile.hpp, G columns per workgroup) and by the single-pass 8192- to
+// 32768-point transforms (fft_row_halves_body below): half the LDS of the
+// 16-element layout, so twice the workgroups per CU (32768 points: the one
+// layout that fits a CU at all).
 template <int LOGL>
 struct HalvesShape {
     static constexpr int N = 1 << LOGL, E = 32, T = N / E, HALF = N / 2;
     static constexpr int NFULL = LOGL / 4, REM = LOGL % 4;
     static constexpr int NSTAGES = NFULL + (REM ? 1 : 0);
-    static_assert((LOGL >= 7 && LOGL <= 10) || LOGL == 13 || LOGL == 14,
-                  "half exchanges: 128 .. 1024-point tile columns, 8192 / 16384-point rows");
+    static_assert((LOGL >= 7 && LOGL <= 10) || (LOGL >= 13 && LOGL <= 15),
+                  "half exchanges: 128 .. 1024-point tile columns, 8192 .. 32768-point rows");
 };
 
 template <int LOGL, int S>
@@ -414,11 +434,12 @@ struct RowHalvesStages {
     }
 };
 
-// One transform of N = 2^LOGN (8192 or 16384) points per workgroup of N/32
-// threads, 32 elements per thread, LDS of N/2 + N/32 positions (68 KB at
+// One transform of N = 2^LOGN (8192, 16384 or 32768) points per workgroup of
+// N/32 threads, 32 elements per thread, LDS of N/2 + N/32 positions (68 KB at
 // 16384: two workgroups per CU where the 16-element layout's 136 KB allows
-// one).  IO and flags as fft_stockham_body; the stage table is the radix
-// list (16, 16, 16, r) of the 16-element layout.
+// one; 136 KB and 1024 threads at 32768).  IO and flags as
+// fft_stockham_body; the stage table is the radix list (16, 16, 16, r) of
+// the 16-element layout.
 template <int LOGN, class IO>
 __device__ __forceinline__ void fft_row_halves_body(const IO io, const float2* __restrict__ tw, uint64_t batch,
                                                     float scale, uint32_t flags) {
@@ -429,7 +450,7 @@ __device__ __forceinline__ void fft_row_halves_body(const IO io, const float2* _
     if (f >= batch) return;  // uniform over the workgroup (the host launches batch of them)
     float2 x[H::E], y[H::E];
 #pragma unroll
-    for (int m = 0; m < H::E; ++m) x[m] = io.load(f * H::N + t + H::T * m);
+    for (int m = 0; m < H::E; ++m) x[m] = io.load_row(f * H::N + H::T * m, t);
     if (flags & FG_PASS_CONJ_IN) {
 #pragma unroll
         for (int m = 0; m < H::E; ++m) x[m] = cconj(x[m]);
@@ -440,7 +461,7 @@ __device__ __forceinline__ void fft_row_halves_body(const IO io, const float2* _
     for (int m = 0; m < H::E; ++m) {
         float2 v = y[m];
         if (cs) v = cscale(cconj(v), scale);
-        io.store(f * H::N + t + H::T * m, v);
+        io.store_row(f * H::N + H::T * m, t, v);
     }
 }
 

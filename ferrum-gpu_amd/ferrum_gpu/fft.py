@@ -359,7 +359,7 @@ def transpose(device: Device, d_in, d_out, rows: int, cols: int, batch: int = 1,
 
 
 def set_chunk_bytes(nbytes: int) -> None:
-    """Chunk limit, in bytes, for multi-launch plans (1D N > 16384, 2D) created
+    """Chunk limit, in bytes, for multi-launch plans (1D N > 32768, 2D) created
     from now on, process-wide.  Such a plan runs every pass over one chunk of
     whole transforms (images) of at most ``nbytes`` before the next chunk, so
     the chunk's intermediate array stays in the GPU's Infinity Cache.  0 turns

@@ -150,7 +150,7 @@ FG_API int fg_fft_plan_destroy(fg_fft_plan_t plan);
  * d_in and d_out each hold batch*N (2D: batch*N*N) complex64, 8-byte aligned;
  * they may be equal (in place) but must not otherwise overlap.
  * direction: FG_FORWARD or FG_INVERSE.  stream NULL = device default stream.
- * A multi-launch plan (1D N > 16384, 2D images above 16384 points) keeps one
+ * A multi-launch plan (1D N > 32768, 2D images above 16384 points) keeps one
  * workspace (and one split-layout staging buffer): executions of one plan
  * must be ordered, one stream at a time; run concurrent work on separate
  * plans. */
@@ -199,7 +199,7 @@ FG_API int fg_graph_capture_end(fg_device_t dev, fg_stream_t capture_stream, fg_
 /* Number of nodes in the captured graph. */
 FG_API int fg_graph_node_count(fg_graph_t graph, size_t *nodes);
 FG_API int fg_graph_destroy(fg_graph_t graph);
-/* Chunked execution of multi-launch plans (1D N > 16384, 2D images above
+/* Chunked execution of multi-launch plans (1D N > 32768, 2D images above
  * 16384 points).  No
  * counterpart in the reference, whose GPU path has no multi-pass plans
  * (crates/ferrum-gpu-fft/src/plan.rs:58).  Such a plan runs all of its passes
@@ -257,7 +257,7 @@ FG_API int fg_transpose_c64(fg_device_t dev, const void *d_in, void *d_out, uint
  * 1463-1610, for every plan).  Same results as fg_fft_exec on the interleaved
  * data.  Each array 4-byte aligned (FG_ERR_INVALID_ARGUMENT otherwise);
  * d_out_re / d_out_im may equal d_in_re / d_in_im; no other overlap.
- * Single-pass plans (1D, N <= 16384; 2D images of up to 16384 points) run one
+ * Single-pass plans (1D, N <= 32768; 2D images of up to 16384 points) run one
  * launch; other plans stage through an interleaved buffer the plan allocates
  * at its first split call (synchronously: that first call is refused with
  * FG_ERR_INVALID_ARGUMENT, before any allocation, when `stream` is being

@@ -80,6 +80,6 @@ def test_throughput_gate():
 def test_single_pass_workloads():
     import bench
 
-    for name, log_n, batch in (("1d_8192", 13, 8192), ("1d_16384", 14, 4096)):
+    for name, log_n, batch in (("1d_8192", 13, 8192), ("1d_16384", 14, 4096), ("1d_32768", 15, 2048)):
         dims, ln, b, *_ = bench.FFT_WORKLOADS[name]
         assert (dims, ln, b) == (1, log_n, batch) and b << ln == 1 << 26   # 512 MiB

@@ -56,7 +56,7 @@ def _run(dev, x, log_n, batch, two_d, direction="forward", normalize=False, in_p
 # (two_d, log_n, batch): transform sizes 64 KiB .. 128 MiB, batches that
 # do and do not divide into chunks.
 CASES = [
-    (False, 15, 37),
+    (False, 17, 37),
     (False, 16, 64),
     (False, 20, 3),
     (True, 8, 40),
@@ -117,7 +117,7 @@ def test_chunked_split_layout(gpu_device, chunk_limit):
     import ferrum_gpu
     from ferrum_gpu.hip import DeviceBuffer
 
-    log_n, batch = 15, 12
+    log_n, batch = 16, 12
     n = batch << log_n
     chunk_limit(4 * 8 << log_n)
     rng = np.random.default_rng(977)

@@ -26,7 +26,7 @@ def _fft(x, log_n, direction="forward", normalize=False, device=None):
     return ferrum_gpu.fft.fft_1d_c2c_pow2(x, log_n, direction=direction, normalize=normalize, device=device)
 
 
-@pytest.mark.parametrize("log_n", list(range(2, 15)))
+@pytest.mark.parametrize("log_n", list(range(2, 16)))
 @pytest.mark.parametrize("batch", [1, 7, 257])
 def test_forward_matches_oracle(gpu_device, log_n, batch):
     rng = np.random.default_rng(1000 * log_n + batch)
@@ -37,7 +37,7 @@ def test_forward_matches_oracle(gpu_device, log_n, batch):
     assert rel_l2(got, oracle.fft_1d(x, log_n)) <= TOL
 
 
-@pytest.mark.parametrize("log_n", list(range(2, 15)))
+@pytest.mark.parametrize("log_n", list(range(2, 16)))
 @pytest.mark.parametrize("normalize", [False, True])
 def test_inverse_matches_oracle(gpu_device, log_n, normalize):
     rng = np.random.default_rng(77 + log_n)
@@ -57,7 +57,7 @@ def test_roundtrip(gpu_device, log_n):
 
 def test_fp64_direct_dft_spot_check(gpu_device):
     rng = np.random.default_rng(64)
-    for log_n in (4, 8, 10, 12, 13, 14):
+    for log_n in (4, 8, 10, 12, 13, 14, 15):
         n = 1 << log_n
         x = normal_c64(rng, 6 * n)
         got = _fft(x, log_n, device=gpu_device).reshape(6, n)

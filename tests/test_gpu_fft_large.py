@@ -174,7 +174,7 @@ def test_host_path_plan_cache_eviction(gpu_device):
     import ferrum_gpu
 
     rng = np.random.default_rng(77)
-    log_n = 15
+    log_n = 16
     batches = list(range(1, 12)) + [3, 1, 11]
     for batch in batches:
         x = uniform_c64(rng, batch << log_n)

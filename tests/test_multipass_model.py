@@ -130,9 +130,9 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None):
         return f"fg_tile_l{p['log_l']}_g{p['g']}_{kind}{pol}"
 
     if not two_d:
-        if log_n <= 14:
-            # single pass: the Stockham kernel (fg_fft_n13 / n14: 32 elements
-            # per thread, exchanges in halves; test_tile_halves_model)
+        if log_n <= 15:
+            # single pass: the Stockham kernel (fg_fft_n13 / n14 / n15: 32
+            # elements per thread, exchanges in halves; test_tile_halves_model)
             return [f"fg_fft_n{log_n}"]
         passes = tile_geometry_1d(log_n, 1, cached)
         return [tile(p, pass_policy(i, len(passes), cached, p["g"]), reads_input=(i == 0))

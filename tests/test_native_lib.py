@@ -99,7 +99,7 @@ def planned_kernels():
     from test_multipass_model import plan_kernel_names
     from test_stockham_model import LATENCY_GEOM
 
-    names = {f"fg_fft_n{l}" for l in range(2, 15)} | {f"fg_fft_n{l}_split" for l in range(2, 15)}
+    names = {f"fg_fft_n{l}" for l in range(2, 16)} | {f"fg_fft_n{l}_split" for l in range(2, 16)}
     names |= {f"fg_fft_n{l}_lat{sfx}" for l in LATENCY_GEOM for sfx in ("", "_split")}
     for cached in (False, True):
         for log_n in range(13, 25):

@@ -28,7 +28,7 @@ X2_GEOM = {10: (4, 2)}
 # kStockham entries of the 32-element kernels with the exchanges in halves
 # (FG_STOCKHAM_HALVES, one transform per workgroup; modelled in
 # test_tile_halves_model.py)
-HALVES_GEOM = {13: (5, 1), 14: (5, 1)}
+HALVES_GEOM = {13: (5, 1), 14: (5, 1), 15: (5, 1)}
 # kStockhamLatency / FG_STOCKHAM_LAT: single-pass plans too small to fill the GPU
 LATENCY_GEOM = {8: (2, 1), 10: (3, 1), 12: (3, 1)}
 
@@ -39,8 +39,14 @@ def row_exponents(r):
 
 
 def two_level(L):
-    """A stage spanning L >= 1024 stores W^{64 h} (h < L/64), then W^l (l < 64)."""
+    """A stage spanning L >= 1024 stores W^{64 h} (h < L/64; radix 8: h < 8L/64),
+    then W^l (l < 64)."""
     return L >= 1024
+
+
+def two_level_high(L, R):
+    """Entries W^{64 h} of a two-level block (tw_two_level_high)."""
+    return L * R // 64 if R == 8 else L // 64
 
 
 def stockham_table(log_n, log_e):
@@ -51,9 +57,10 @@ def stockham_table(log_n, log_e):
         logl, logr = s * log_e, (log_e if s < nfull else rem)
         L, R = 1 << logl, 1 << logr
         if two_level(L):
-            e = np.concatenate([(64 * np.arange(L // 64)) % (L * R), np.arange(64)])
+            hi = two_level_high(L, R)
+            e = np.concatenate([(64 * np.arange(hi)) % (L * R), np.arange(64)])
             out.append(np.exp(-2j * np.pi * e / (L * R)).astype(np.complex64))
-            offs.append(offs[-1] + L // 64 + 64)
+            offs.append(offs[-1] + hi + 64)
             continue
         ps = np.array(row_exponents(R))
         k, p = np.meshgrid(np.arange(L), ps, indexing="ij")
@@ -67,16 +74,29 @@ def stage_twiddles(tw, off, k, r, L=None):
     """(T, r) twiddles W^{p*k} as the kernel forms them from the table rows at
     off + k * row_len: a stored entry, or for radix 16 / 8 the product
     W^{k*(p & 3)} * W^{k*4*(p >> 2)} of two stored entries.  A two-level stage
-    (L >= 1024, radix 2 or 4) forms W^k = A[k >> 6] * B[k & 63] and its powers
-    by f32 products, as apply_stage_twiddles_at does."""
+    (L >= 1024) forms W^k = A[k >> 6] * B[k & 63]; radix 4 forms W^2k and
+    W^3k as products of it, radix 8 looks up W^2k and W^4k the same way and
+    forms W^3k = W^k W^2k, W^5k = W^k W^4k, W^6k = W^2k W^4k,
+    W^7k = W^3k W^4k -- all in f32, as apply_stage_twiddles_at does."""
     if L is not None and two_level(L):
-        assert r in (2, 4)
-        a, b = tw[off + (k >> 6)], tw[off + L // 64 + (k & 63)]
-        w1 = (a * b).astype(np.complex64)
+        assert r in (2, 4, 8)
+        hi = two_level_high(L, r)
+
+        def look(e):
+            return (tw[off + (e >> 6)] * tw[off + hi + (e & 63)]).astype(np.complex64)
+
+        def mul(a, b):
+            return (a * b).astype(np.complex64)
+
+        w1 = look(k)
         cols = [np.ones(k.shape, np.complex64), w1]
         if r == 4:
-            w2 = (w1 * w1).astype(np.complex64)
-            cols += [w2, (w2 * w1).astype(np.complex64)]
+            w2 = mul(w1, w1)
+            cols += [w2, mul(w2, w1)]
+        if r == 8:
+            w2, w4 = look(2 * k), look(4 * k)
+            w3 = mul(w1, w2)
+            cols += [w2, w3, w4, mul(w1, w4), mul(w2, w4), mul(w3, w4)]
         return np.stack(cols, axis=1).astype(np.complex128)
     ps = row_exponents(r)
     rows = tw[off + k[:, None] * len(ps) + np.arange(len(ps))[None, :]].astype(np.complex128)
@@ -178,7 +198,7 @@ def test_twiddle_rows_are_16_byte_aligned():
 
 def test_factored_twiddles_equal_the_full_rows():
     # the products the kernel forms reproduce W^{p*k} for every p (to f32 rounding)
-    for log_n, log_e in [(12, 4), (11, 4), (10, 4), (9, 3), (12, 3), (13, 4), (14, 4)]:
+    for log_n, log_e in [(12, 4), (11, 4), (10, 4), (9, 3), (12, 3), (13, 4), (14, 4), (15, 4)]:
         tw, offs = stockham_table(log_n, log_e)
         nfull, rem = divmod(log_n, log_e)
         for s in range(1, nfull + (1 if rem else 0)):
@@ -187,7 +207,8 @@ def test_factored_twiddles_equal_the_full_rows():
             w = stage_twiddles(tw, offs[s], k, R, L)
             exact = np.exp(-2j * np.pi * ((k[:, None] * np.arange(R)[None, :]) % (L * R)) / (L * R))
             # stored or one product: 3e-7; two-level (W^k from two entries, then
-            # W^2k and W^3k as products): up to five f32 roundings, 6e-7
+            # W^2k and W^3k as products): up to five f32 roundings, 6e-7 (radix
+            # 8 at 32768 points, W^7k from three lookups: 2.4e-7)
             tol = 6e-7 if two_level(L) else 3e-7
             assert np.max(np.abs(w - exact)) < tol, (log_n, s)
 
@@ -203,6 +224,10 @@ def test_stage_table_sizes():
     # entries instead of 4096 rows of 4
     tw, offs = stockham_table(14, 4)
     assert offs == [0, 0, 96, 96 + 1536, 96 + 1536 + 128] and tw.size == offs[-1]
+    # N = 32768 (16, 16, 16, 8): the radix-8 two-level stage holds W^{64 h} for
+    # every exponent below L*R = 32768 (512 entries), then 64
+    tw, offs = stockham_table(15, 4)
+    assert offs == [0, 0, 96, 96 + 1536, 96 + 1536 + 512 + 64] and tw.size == offs[-1]
     # no stage of the kernels up to 4096 points is two-level (their tables are
     # unchanged): the single-pass geometries, the tile passes (log_e 4, up to
     # 4096 points) and the one-pass 2D kernels (log_e 3 or 4, up to 1024 points)
