@@ -75,7 +75,13 @@ def fpi(lr, lc):
 
 
 def shapes():
-    return [(lr, lc) for lr in range(4, 11) for lc in range(4, 11) if lr + lc <= MAX_LOG]
+    """The LDS-resident kernel's shapes: up to 8192 points (16384-point images
+    run fft2d_halves_body, tests/test_fft2d_halves_model.py)."""
+    return [(lr, lc) for lr in range(4, 11) for lc in range(4, 11) if lr + lc < MAX_LOG]
+
+
+def halves_shapes():
+    return [(lr, MAX_LOG - lr) for lr in range(4, 11)]
 
 
 def small2d_model(images, lr, lc):
@@ -156,3 +162,7 @@ def test_small2d_mirror_matches_the_sources():
     hip = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
     inst = {(int(a), int(b)) for a, b in re.findall(r"^FG_FFT2D\((\d+), (\d+)\)", hip, flags=re.M)}
     assert inst == set(shapes())
+    halves = {(int(a), int(b)) for a, b in re.findall(r"^FG_FFT2D_HALVES\((\d+), (\d+)\)", hip, flags=re.M)}
+    assert halves == set(halves_shapes())
+    # 512 threads per 16384-point image (FG_SMALL2D_TPI), one image per workgroup
+    assert "#define FG_SMALL2D_TPI(lr, lc) (((lr) + (lc)) >= 14 ? 512 :" in geom

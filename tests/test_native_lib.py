@@ -86,7 +86,7 @@ def instantiated_kernels():
         # cache policies (FG_TILE_P): all four, or _cc alone for narrow tiles
         names |= {base + "_cc"} if m.group(1) else {base + pol for pol in ("", "_sc", "_cc", "_cs")}
     # one-pass 2D FFTs of small images
-    for a, b in re.findall(r"^FG_FFT2D\((\d+), (\d+)\)", src, flags=re.M):
+    for a, b in re.findall(r"^FG_FFT2D(?:_HALVES)?\((\d+), (\d+)\)", src, flags=re.M):
         names |= {f"fg_fft2d_l{a}_{b}", f"fg_fft2d_l{a}_{b}_split"}
     # first-pass tiles with the exchanges in halves: unchunked and _sc
     for m in re.finditer(r"^FG_TILE_HALVES\((\d+), (\d+)\)", src, flags=re.M):
@@ -361,3 +361,14 @@ def test_c_example_is_built_against_the_library():
         needed = os.popen(f"readelf -d {f}").read()
         assert "libferrum_gpu.so" in needed, f
     assert hasattr(ctypes.CDLL(so), "fft_c_abi_example")
+
+
+def test_host_objects_depend_on_the_shared_geometry_header():
+    # fft_plan.hpp includes kernels/tile_geom.h, whose launch geometry the
+    # kernels are compiled against: the Makefile must rebuild the host objects
+    # when it changes, or a stale host launches a kernel with the old block size
+    mk = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "Makefile")).read()
+    host_hdr = re.search(r"^HOST_HDR\s*:=(.*)$", mk, flags=re.M).group(1)
+    assert "kernels/tile_geom.h" in host_hdr
+    plan_hpp = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "fft_plan.hpp")).read()
+    assert '#include "kernels/tile_geom.h"' in plan_hpp
