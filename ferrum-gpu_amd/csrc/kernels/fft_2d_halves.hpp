@@ -1,13 +1,14 @@
 // fft_2d_halves.hpp -- the whole 2D FFT of one image of R x C = 2^LR x 2^LC =
-// 16384 points per workgroup, in registers, with the exchanges in halves.
+// 8192 or 16384 points per workgroup, in registers, with the exchanges in
+// halves.
 //
-// Holding such an image in LDS (fft_2d_small.hpp) takes 141 KB, one workgroup
-// per CU, whose load, transform and store phases then cannot overlap with
-// another workgroup's.  Here T = 512 threads hold 32 elements each at
-// positions t + T*m of the row-major image (coalesced loads), and the
-// exchanges run in two rounds through N/2 + N/32 LDS slots (68 KB), so two
-// workgroups share a CU, as in the single-pass 16384-point 1D kernel
-// (fft_row_halves_body).
+// Holding such an image in LDS (fft_2d_small.hpp) takes 70 / 141 KB: two /
+// one workgroups per CU, whose load, transform and store phases then barely
+// overlap with another workgroup's.  Here T = N/32 threads (256 / 512) hold
+// 32 elements each at positions t + T*m of the row-major image (coalesced
+// loads), and the exchanges run in two rounds through N/2 + N/32 LDS slots
+// (34 / 68 KB), so four / two workgroups share a CU, as in the single-pass
+// 8192- / 16384-point 1D kernels (fft_row_halves_body).
 //
 // The 2D DFT is one Stockham pass over all N positions whose radix list is
 // R's list (16, .., 16, r) followed by C's:
@@ -39,7 +40,8 @@ struct Halves2D {
     static constexpr int SR = LR / 4 + (LR % 4 ? 1 : 0);  // stages over the row index
     static constexpr int SC = LC / 4 + (LC % 4 ? 1 : 0);  // stages over the column index
     static constexpr int NSTAGES = SR + SC;
-    static_assert(LR + LC == 14 && LR >= 4 && LC >= 4, "16384-point images, at least 16 per side");
+    static_assert((LR + LC == 13 || LR + LC == 14) && LR >= 4 && LC >= 4,
+                  "8192- or 16384-point images, at least 16 per side");
     static_assert(T % 16 == 0, "reads at lds_pos(t) + m (T + T/16)");
 };
 
@@ -175,7 +177,7 @@ struct Halves2DStages {
     }
 };
 
-// One 2^LR x 2^LC image per workgroup of 512 threads.  tw_rows / tw_cols are
+// One 2^LR x 2^LC image per workgroup of N/32 threads.  tw_rows / tw_cols are
 // the stage tables for lengths C and R (the host's small-2D tables); IO and
 // flags as fft_stockham_body.
 template <int LR, int LC, class IO>

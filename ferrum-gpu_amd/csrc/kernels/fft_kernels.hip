@@ -264,16 +264,17 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
         fft2d_small_body<LR, LC, FG_SMALL2D_LOGE(LR, LC), FG_SMALL2D_FPI(LR, LC)>(                    \
             SplitIO{in_re, in_im, out_re, out_im}, tw_rows, tw_cols, batch, scale, flags);            \
     }
-// 16384-point images: one per 512-thread workgroup, in registers, the
-// exchanges in halves (fft2d_halves_body); two workgroups per CU.
+// 8192- and 16384-point images: one per workgroup of N/32 threads, in
+// registers, the exchanges in halves (fft2d_halves_body); four / two
+// workgroups per CU.
 #define FG_FFT2D_HALVES(LR, LC)                                                                     \
-    extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void      \
+    extern "C" __global__ __launch_bounds__(FG_SMALL2D_BLOCK(LR, LC)) __attribute__((amdgpu_waves_per_eu(4))) void \
         fg_fft2d_l##LR##_##LC(const float2* __restrict__ in, float2* __restrict__ out,              \
                               const float2* __restrict__ tw_rows, const float2* __restrict__ tw_cols, \
                               uint64_t batch, float scale, uint32_t flags) {                         \
         fft2d_halves_body<LR, LC>(InterleavedIO{in, out}, tw_rows, tw_cols, batch, scale, flags);    \
     }                                                                                                 \
-    extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void      \
+    extern "C" __global__ __launch_bounds__(FG_SMALL2D_BLOCK(LR, LC)) __attribute__((amdgpu_waves_per_eu(4))) void \
         fg_fft2d_l##LR##_##LC##_split(const float* __restrict__ in_re, const float* __restrict__ in_im, \
                                       float* __restrict__ out_re, float* __restrict__ out_im,        \
                                       const float2* __restrict__ tw_rows,                             \
@@ -287,27 +288,27 @@ FG_FFT2D(4, 5)
 FG_FFT2D(4, 6)
 FG_FFT2D(4, 7)
 FG_FFT2D(4, 8)
-FG_FFT2D(4, 9)
+FG_FFT2D_HALVES(4, 9)
 FG_FFT2D_HALVES(4, 10)
 FG_FFT2D(5, 4)
 FG_FFT2D(5, 5)
 FG_FFT2D(5, 6)
 FG_FFT2D(5, 7)
-FG_FFT2D(5, 8)
+FG_FFT2D_HALVES(5, 8)
 FG_FFT2D_HALVES(5, 9)
 FG_FFT2D(6, 4)
 FG_FFT2D(6, 5)
 FG_FFT2D(6, 6)
-FG_FFT2D(6, 7)
+FG_FFT2D_HALVES(6, 7)
 FG_FFT2D_HALVES(6, 8)
 FG_FFT2D(7, 4)
 FG_FFT2D(7, 5)
-FG_FFT2D(7, 6)
+FG_FFT2D_HALVES(7, 6)
 FG_FFT2D_HALVES(7, 7)
 FG_FFT2D(8, 4)
-FG_FFT2D(8, 5)
+FG_FFT2D_HALVES(8, 5)
 FG_FFT2D_HALVES(8, 6)
-FG_FFT2D(9, 4)
+FG_FFT2D_HALVES(9, 4)
 FG_FFT2D_HALVES(9, 5)
 FG_FFT2D_HALVES(10, 4)
 

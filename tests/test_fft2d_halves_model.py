@@ -1,9 +1,10 @@
-"""CPU model of the one-pass 2D FFT of 16384-point images with the exchanges
-in halves (fft2d_halves_body in ferrum-gpu_amd/csrc/kernels/fft_2d_halves.hpp),
-checked against the oracle before any launch.
+"""CPU model of the one-pass 2D FFT of 8192- and 16384-point images with the
+exchanges in halves (fft2d_halves_body in
+ferrum-gpu_amd/csrc/kernels/fft_2d_halves.hpp), checked against the oracle
+before any launch.
 
-One workgroup of T = N/32 = 512 threads holds one image of R x C = 2^lr x 2^lc
-points (lr + lc = 14) in registers, 32 per thread at positions t + T m of the
+One workgroup of T = N/32 threads holds one image of R x C = 2^lr x 2^lc
+points (lr + lc = 13 or 14) in registers, 32 per thread at positions t + T m of the
 row-major image (coalesced loads).  The 2D DFT is a 1D Stockham pass over all
 N positions whose radix list is the row-length digits' list for R (16, ..,
 16, r), then C's: the first block takes the DFT over the row index (the top
@@ -55,7 +56,7 @@ def lds_pos(p):
 def model(images, lr, lc):
     """images: (B, N) complex, row-major; returns the kernel's (B, N) output."""
     b_, n = images.shape
-    assert n == 1 << (lr + lc) == 16384
+    assert n == 1 << (lr + lc) and lr + lc in (13, 14)
     T, half = n // E, n // 2
     slots = half + half // 16
     nr, nc = 1 << lr, 1 << lc
@@ -122,13 +123,13 @@ def model(images, lr, lc):
     return res
 
 
-SHAPES = [(lr, 14 - lr) for lr in range(4, 11)]
+SHAPES = [(lr, bits - lr) for bits in (13, 14) for lr in range(4, bits - 3)]
 
 
 @pytest.mark.parametrize("lr,lc", SHAPES)
 def test_model_matches_oracle(lr, lc):
     rng = np.random.default_rng(lr * 16 + lc)
-    n = 1 << 14
+    n = 1 << (lr + lc)
     x = uniform_c64(rng, 2 * n)
     got = model(x.reshape(2, n), lr, lc).reshape(-1)
     want = np.stack([np.fft.fft2(x[i * n:(i + 1) * n].reshape(1 << lr, 1 << lc)).reshape(-1) for i in range(2)])
@@ -142,14 +143,14 @@ def test_transposing_exchange_round_of_each_output():
     # k_r = (t + T m) mod R in the upper half of the rows -> round 1, i.e.
     # Q = k_r C + k_c in the upper half of the image; for R <= T = 512 the
     # round is the same for all 32 outputs of a thread, for R = 1024 it is m's parity
-    T = 512
-    for lr in range(4, 11):
-        nr, nc = 1 << lr, 1 << (14 - lr)
+    for lr, lc in SHAPES:
+        nr, nc, n = 1 << lr, 1 << lc, 1 << (lr + lc)
+        T = n // E
         t = np.arange(T)
         P = t[:, None] + T * np.arange(E)[None, :]
         Q = (P % nr) * nc + P // nr
         rnd = (P % nr) >= nr // 2
-        assert np.array_equal(rnd, Q >= 8192)
+        assert np.array_equal(rnd, Q >= n // 2)
         if nr <= T:
             assert np.array_equal(rnd, np.repeat(((t % nr) >= nr // 2)[:, None], E, axis=1))
         else:
@@ -160,17 +161,17 @@ def test_transposing_exchange_slots():
     # the kernel's closed forms for the last exchange's slots equal
     # tpos(Q - HALF h) = Q' + Q' / C, and a wave's 16-lane groups of writes
     # hit 16 distinct bank pairs (32 four-byte banks, 8-byte slots)
-    T = 512
-    for lr in range(4, 11):
-        nr, nc = 1 << lr, 1 << (14 - lr)
+    for lr, lc in SHAPES:
+        nr, nc, n = 1 << lr, 1 << lc, 1 << (lr + lc)
+        T = n // E
         t = np.arange(T)
         for h in range(2):
             for m in range(E):
                 P = t + T * m
-                Q = (P % nr) * nc + P // nr - 8192 * h
+                Q = (P % nr) * nc + P // nr - (n // 2) * h
                 mine = ((P % nr) >= nr // 2) == (h == 1)
                 if nr <= T:
-                    q0 = (t & (nr - 1)) * nc + (t >> lr) - 8192 * h
+                    q0 = (t & (nr - 1)) * nc + (t >> lr) - (n // 2) * h
                     slot = q0 + q0 // nc + (T // nr) * m
                 else:
                     slot = t * (nc + 1) + (m >> 1)

@@ -64,8 +64,9 @@ def lanes(timg, threads_per_line, thread_major):
 
 
 def loge(lr, lc):
-    """FG_SMALL2D_LOGE: 8 elements per thread, 16 for 16384-point images."""
-    return 4 if lr + lc >= 14 else 3
+    """FG_SMALL2D_LOGE: 8 elements per thread for the LDS-resident shapes (4:
+    the radix-16 tables of the register-resident 8192- / 16384-point kernel)."""
+    return 4 if lr + lc >= HALVES_LOG else 3
 
 
 def fpi(lr, lc):
@@ -74,14 +75,17 @@ def fpi(lr, lc):
     return 1 if t >= 256 else 256 // t
 
 
+HALVES_LOG = 13
+
+
 def shapes():
-    """The LDS-resident kernel's shapes: up to 8192 points (16384-point images
-    run fft2d_halves_body, tests/test_fft2d_halves_model.py)."""
-    return [(lr, lc) for lr in range(4, 11) for lc in range(4, 11) if lr + lc < MAX_LOG]
+    """The LDS-resident kernel's shapes: up to 4096 points (8192- and
+    16384-point images run fft2d_halves_body, tests/test_fft2d_halves_model.py)."""
+    return [(lr, lc) for lr in range(4, 11) for lc in range(4, 11) if lr + lc < HALVES_LOG]
 
 
 def halves_shapes():
-    return [(lr, MAX_LOG - lr) for lr in range(4, 11)]
+    return [(lr, bits - lr) for bits in (HALVES_LOG, MAX_LOG) for lr in range(4, bits - 3)]
 
 
 def small2d_model(images, lr, lc):
@@ -156,13 +160,14 @@ def test_small2d_geometry_fits(lr, lc):
 
 def test_small2d_mirror_matches_the_sources():
     geom = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "tile_geom.h")).read()
-    m = re.search(r"#define FG_SMALL2D_LOGE\(lr, lc\) \(\(\(lr\) \+ \(lc\)\) >= (\d+) \? (\d+) : (\d+)\)", geom)
-    assert m and m.groups() == ("14", "4", "3")
+    m = re.search(r"#define FG_SMALL2D_LOGE\(lr, lc\) \(\(\(lr\) \+ \(lc\)\) >= FG_SMALL2D_HALVES_LOG \? (\d+) : (\d+)\)", geom)
+    assert m and m.groups() == ("4", "3")
+    assert re.search(r"#define FG_SMALL2D_HALVES_LOG (\d+)", geom).group(1) == str(HALVES_LOG)
     assert re.search(r"#define FG_SMALL2D_MAX_LOG (\d+)", geom).group(1) == str(MAX_LOG)
     hip = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
     inst = {(int(a), int(b)) for a, b in re.findall(r"^FG_FFT2D\((\d+), (\d+)\)", hip, flags=re.M)}
     assert inst == set(shapes())
     halves = {(int(a), int(b)) for a, b in re.findall(r"^FG_FFT2D_HALVES\((\d+), (\d+)\)", hip, flags=re.M)}
     assert halves == set(halves_shapes())
-    # 512 threads per 16384-point image (FG_SMALL2D_TPI), one image per workgroup
-    assert "#define FG_SMALL2D_TPI(lr, lc) (((lr) + (lc)) >= 14 ? 512 :" in geom
+    # N/32 threads per 8192- or 16384-point image (FG_SMALL2D_TPI), one image per workgroup
+    assert "(((lr) + (lc)) >= FG_SMALL2D_HALVES_LOG ? (1 << ((lr) + (lc))) / 32 :" in geom
