@@ -1,14 +1,14 @@
 // fft_2d_halves.hpp -- the whole 2D FFT of one image of R x C = 2^LR x 2^LC =
-// 8192 or 16384 points per workgroup, in registers, with the exchanges in
-// halves.
+// 4096, 8192 or 16384 points per workgroup, in registers, with the exchanges
+// in halves.
 //
-// Holding such an image in LDS (fft_2d_small.hpp) takes 70 / 141 KB: two /
-// one workgroups per CU, whose load, transform and store phases then barely
-// overlap with another workgroup's.  Here T = N/32 threads (256 / 512) hold
-// 32 elements each at positions t + T*m of the row-major image (coalesced
-// loads), and the exchanges run in two rounds through N/2 + N/32 LDS slots
-// (34 / 68 KB), so four / two workgroups share a CU, as in the single-pass
-// 8192- / 16384-point 1D kernels (fft_row_halves_body).
+// Holding such an image in LDS (fft_2d_small.hpp) takes 35 / 70 / 141 KB:
+// four / two / one workgroups per CU, whose load, transform and store phases
+// then barely overlap with another workgroup's.  Here T = N/32 threads
+// (128 / 256 / 512) hold 32 elements each at positions t + T*m of the
+// row-major image (coalesced loads), and the exchanges run in two rounds
+// through N/2 + N/32 LDS slots (17 / 34 / 68 KB), as in the single-pass 1D
+// kernels of 8192 points and up (fft_row_halves_body).
 //
 // The 2D DFT is one Stockham pass over all N positions whose radix list is
 // R's list (16, .., 16, r) followed by C's:
@@ -40,8 +40,8 @@ struct Halves2D {
     static constexpr int SR = LR / 4 + (LR % 4 ? 1 : 0);  // stages over the row index
     static constexpr int SC = LC / 4 + (LC % 4 ? 1 : 0);  // stages over the column index
     static constexpr int NSTAGES = SR + SC;
-    static_assert((LR + LC == 13 || LR + LC == 14) && LR >= 4 && LC >= 4,
-                  "8192- or 16384-point images, at least 16 per side");
+    static_assert(LR + LC >= 12 && LR + LC <= 14 && LR >= 4 && LC >= 4,
+                  "4096- to 16384-point images, at least 16 per side");
     static_assert(T % 16 == 0, "reads at lds_pos(t) + m (T + T/16)");
 };
 
@@ -188,7 +188,9 @@ __device__ __forceinline__ void fft2d_halves_body(const IO io, const float2* __r
     __shared__ float2 lds[H::HALF + H::HALF / 16];
     const int t = threadIdx.x;
     const uint64_t f = blockIdx.x;
-    if (f >= batch) return;  // uniform over the workgroup (the host launches batch of them)
+    // uniform over the workgroup (the host launches batch of them, N/32 threads each;
+    // a larger block would only leave its extra threads idle, never out of bounds)
+    if (f >= batch || t >= H::T) return;
     float2 x[H::E], y[H::E];
 #pragma unroll
     for (int m = 0; m < H::E; ++m) x[m] = io.load_row(f * H::N + H::T * m, t);
