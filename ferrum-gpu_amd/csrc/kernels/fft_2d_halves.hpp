@@ -1,14 +1,16 @@
 // fft_2d_halves.hpp -- the whole 2D FFT of one image of R x C = 2^LR x 2^LC =
-// 4096, 8192 or 16384 points per workgroup, in registers, with the exchanges
-// in halves.
+// 2048 to 16384 points per workgroup, in registers, with the exchanges in
+// halves.
 //
-// Holding such an image in LDS (fft_2d_small.hpp) takes 35 / 70 / 141 KB:
-// four / two / one workgroups per CU, whose load, transform and store phases
-// then barely overlap with another workgroup's.  Here T = N/32 threads
-// (128 / 256 / 512) hold 32 elements each at positions t + T*m of the
-// row-major image (coalesced loads), and the exchanges run in two rounds
-// through N/2 + N/32 LDS slots (17 / 34 / 68 KB), as in the single-pass 1D
-// kernels of 8192 points and up (fft_row_halves_body).
+// Holding such an image in LDS (fft_2d_small.hpp) takes up to 141 KB (one
+// workgroup per CU at 16384 points, two at 8192, four at 4096), and the
+// workgroups' load, transform and store phases then barely overlap.  Here
+// T = N/32 threads (64 .. 512) hold 32 elements each at positions t + T*m of
+// the row-major image (coalesced loads), and the exchanges run in two rounds
+// through N/2 + N/32 LDS slots (8.5 .. 68 KB), as in the single-pass 1D
+// kernels of 8192 points and up (fft_row_halves_body).  Below 2048 points
+// (T < 64: part of a wave per image) the LDS-resident kernel measured as fast
+// or faster.
 //
 // The 2D DFT is one Stockham pass over all N positions whose radix list is
 // R's list (16, .., 16, r) followed by C's:
@@ -40,8 +42,8 @@ struct Halves2D {
     static constexpr int SR = LR / 4 + (LR % 4 ? 1 : 0);  // stages over the row index
     static constexpr int SC = LC / 4 + (LC % 4 ? 1 : 0);  // stages over the column index
     static constexpr int NSTAGES = SR + SC;
-    static_assert(LR + LC >= 12 && LR + LC <= 14 && LR >= 4 && LC >= 4,
-                  "4096- to 16384-point images, at least 16 per side");
+    static_assert(LR + LC >= 11 && LR + LC <= 14 && LR >= 4 && LC >= 4,
+                  "2048- to 16384-point images, at least 16 per side");
     static_assert(T % 16 == 0, "reads at lds_pos(t) + m (T + T/16)");
 };
 

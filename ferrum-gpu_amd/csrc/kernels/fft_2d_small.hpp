@@ -1,9 +1,9 @@
-// fft_2d_small.hpp -- the whole 2D FFT of images of R x C <= 2048 points in
+// fft_2d_small.hpp -- the whole 2D FFT of images of R x C <= 1024 points in
 // one pass through HBM: a row pass and a column pass would each move every
 // byte once; here a workgroup loads FPI whole images into LDS, transforms
 // their rows and then their columns there, and stores them.  E = 8 elements
-// per thread (the template also takes 16).  Images of 4096 points and more
-// run fft_2d_halves.hpp: held in LDS they left one to four workgroups per CU.
+// per thread (the template also takes 16).  Images of 2048 points and more
+// run fft_2d_halves.hpp: held in LDS they left few workgroups per CU.
 //
 // Per image the LDS holds R rows of pitch P (the shape's Small2DLayout):
 //   1. coalesced load of the workgroup's images (64 lanes x 8 contiguous bytes

@@ -264,7 +264,7 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
         fft2d_small_body<LR, LC, FG_SMALL2D_LOGE(LR, LC), FG_SMALL2D_FPI(LR, LC)>(                    \
             SplitIO{in_re, in_im, out_re, out_im}, tw_rows, tw_cols, batch, scale, flags);            \
     }
-// 4096- to 16384-point images: one per workgroup of N/32 threads, in
+// 2048- to 16384-point images: one per workgroup of N/32 threads, in
 // registers, the exchanges in halves (fft2d_halves_body).
 #define FG_FFT2D_HALVES(LR, LC)                                                                     \
     extern "C" __global__ __launch_bounds__(FG_SMALL2D_BLOCK(LR, LC)) __attribute__((amdgpu_waves_per_eu(4))) void \
@@ -285,22 +285,22 @@ extern "C" __global__ __launch_bounds__(256) void fg_vector_add(const float* __r
 FG_FFT2D(4, 4)
 FG_FFT2D(4, 5)
 FG_FFT2D(4, 6)
-FG_FFT2D(4, 7)
+FG_FFT2D_HALVES(4, 7)
 FG_FFT2D_HALVES(4, 8)
 FG_FFT2D_HALVES(4, 9)
 FG_FFT2D_HALVES(4, 10)
 FG_FFT2D(5, 4)
 FG_FFT2D(5, 5)
-FG_FFT2D(5, 6)
+FG_FFT2D_HALVES(5, 6)
 FG_FFT2D_HALVES(5, 7)
 FG_FFT2D_HALVES(5, 8)
 FG_FFT2D_HALVES(5, 9)
 FG_FFT2D(6, 4)
-FG_FFT2D(6, 5)
+FG_FFT2D_HALVES(6, 5)
 FG_FFT2D_HALVES(6, 6)
 FG_FFT2D_HALVES(6, 7)
 FG_FFT2D_HALVES(6, 8)
-FG_FFT2D(7, 4)
+FG_FFT2D_HALVES(7, 4)
 FG_FFT2D_HALVES(7, 5)
 FG_FFT2D_HALVES(7, 6)
 FG_FFT2D_HALVES(7, 7)

@@ -28,15 +28,15 @@ typedef struct TileGeom {
     uint32_t remap;         /* 1: XCD-aware tile order (grid a multiple of 8; fft_tile.hpp) */
 } TileGeom;
 
-/* One-pass 2D FFT of images of 2^lr x 2^lc <= 16384 points: up to 2048
+/* One-pass 2D FFT of images of 2^lr x 2^lc <= 16384 points: up to 1024
  * points (fft_2d_small.hpp) 2^FG_SMALL2D_LOGE(lr, lc) = 8 elements per thread
  * and FG_SMALL2D_FPI(lr, lc) images per workgroup (256 threads, or one image
- * when it needs more); 4096 to 16384 points (fft_2d_halves.hpp) one image
+ * when it needs more); 2048 to 16384 points (fft_2d_halves.hpp) one image
  * per workgroup of N/32 threads with 32 elements each.  FG_SMALL2D_LOGE also
- * names the stage tables' radix list: (8, ..., r) up to 2048 points,
+ * names the stage tables' radix list: (8, ..., r) up to 1024 points,
  * (16, ..., r) above. */
 #define FG_SMALL2D_MAX_LOG 14
-#define FG_SMALL2D_HALVES_LOG 12
+#define FG_SMALL2D_HALVES_LOG 11
 #define FG_SMALL2D_LOGE(lr, lc) (((lr) + (lc)) >= FG_SMALL2D_HALVES_LOG ? 4 : 3)
 #define FG_SMALL2D_TPI(lr, lc) \
     (((lr) + (lc)) >= FG_SMALL2D_HALVES_LOG ? (1 << ((lr) + (lc))) / 32 : (1 << ((lr) + (lc))) >> FG_SMALL2D_LOGE(lr, lc))

@@ -1,10 +1,10 @@
-"""CPU model of the one-pass 2D FFT of 4096- to 16384-point images with the
+"""CPU model of the one-pass 2D FFT of 2048- to 16384-point images with the
 exchanges in halves (fft2d_halves_body in
 ferrum-gpu_amd/csrc/kernels/fft_2d_halves.hpp), checked against the oracle
 before any launch.
 
 One workgroup of T = N/32 threads holds one image of R x C = 2^lr x 2^lc
-points (12 <= lr + lc <= 14) in registers, 32 per thread at positions t + T m of the
+points (11 <= lr + lc <= 14) in registers, 32 per thread at positions t + T m of the
 row-major image (coalesced loads).  The 2D DFT is a 1D Stockham pass over all
 N positions whose radix list is the row-length digits' list for R (16, ..,
 16, r), then C's: the first block takes the DFT over the row index (the top
@@ -56,7 +56,7 @@ def lds_pos(p):
 def model(images, lr, lc):
     """images: (B, N) complex, row-major; returns the kernel's (B, N) output."""
     b_, n = images.shape
-    assert n == 1 << (lr + lc) and 12 <= lr + lc <= 14
+    assert n == 1 << (lr + lc) and 11 <= lr + lc <= 14
     T, half = n // E, n // 2
     slots = half + half // 16
     nr, nc = 1 << lr, 1 << lc
@@ -123,7 +123,7 @@ def model(images, lr, lc):
     return res
 
 
-SHAPES = [(lr, bits - lr) for bits in (12, 13, 14) for lr in range(4, bits - 3)]
+SHAPES = [(lr, bits - lr) for bits in (11, 12, 13, 14) for lr in range(4, bits - 3)]
 
 
 @pytest.mark.parametrize("lr,lc", SHAPES)

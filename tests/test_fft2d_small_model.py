@@ -75,11 +75,11 @@ def fpi(lr, lc):
     return 1 if t >= 256 else 256 // t
 
 
-HALVES_LOG = 12
+HALVES_LOG = 11
 
 
 def shapes():
-    """The LDS-resident kernel's shapes: up to 2048 points (4096- to
+    """The LDS-resident kernel's shapes: up to 1024 points (2048- to
     16384-point images run fft2d_halves_body, tests/test_fft2d_halves_model.py)."""
     return [(lr, lc) for lr in range(4, 11) for lc in range(4, 11) if lr + lc < HALVES_LOG]
 
@@ -169,5 +169,5 @@ def test_small2d_mirror_matches_the_sources():
     assert inst == set(shapes())
     halves = {(int(a), int(b)) for a, b in re.findall(r"^FG_FFT2D_HALVES\((\d+), (\d+)\)", hip, flags=re.M)}
     assert halves == set(halves_shapes())
-    # N/32 threads per image of 4096 points and more (FG_SMALL2D_TPI), one image per workgroup
+    # N/32 threads per image of 2048 points and more (FG_SMALL2D_TPI), one image per workgroup
     assert "(((lr) + (lc)) >= FG_SMALL2D_HALVES_LOG ? (1 << ((lr) + (lc))) / 32 :" in geom
