@@ -154,7 +154,7 @@ __device__ __forceinline__ void halves2d_transpose(const float2* y, float2* x, i
         }
         __syncthreads();
         // reads of t + T m - HALF h, m in [0, 16): tpos = t + t / C + m (T + T / C)
-        // for C <= T; C = 1024 (T = 512): t + 512 m + m / 2
+        // for C <= T; otherwise C = 2T (R = 16): t + T m + m / 2
 #pragma unroll
         for (int m = 0; m < H::E / 2; ++m) {
             int slot;
@@ -190,8 +190,8 @@ __device__ __forceinline__ void fft2d_halves_body(const IO io, const float2* __r
     __shared__ float2 lds[H::HALF + H::HALF / 16];
     const int t = threadIdx.x;
     const uint64_t f = blockIdx.x;
-    // uniform over the workgroup (the host launches batch of them, N/32 threads each;
-    // a larger block would only leave its extra threads idle, never out of bounds)
+    // f is uniform over the workgroup (the host launches batch of them, N/32
+    // threads each); threads beyond N/32 in a larger block would only idle
     if (f >= batch || t >= H::T) return;
     float2 x[H::E], y[H::E];
 #pragma unroll
