@@ -159,10 +159,10 @@ uint32_t tile_columns(uint32_t log_l) {
     // plan).  Up to 1024 points: measured on gfx950 at 2^24 = 256^3, 32 columns of 256
     // points (two 66 KB workgroups per CU) beat 64 (one 133 KB workgroup);
     // fewer than 16 columns (128-byte segments) loses HBM efficiency, so the
-    // floor is 16.  2048 / 4096 points (2D columns only): 8 / 4 columns, the
-    // most a 136 KB LDS tile holds -- narrow tiles, which are read in
-    // XCD-aware order through the caches (add_tile).
-    if (log_l > 10) return 16384u >> log_l;
+    // floor is 16.  2048 / 4096 points (2D columns only): 8 columns with the
+    // exchanges in halves (68 / 136 KB of LDS) -- narrow tiles, which are
+    // read in XCD-aware order through the caches (add_tile).
+    if (log_l > 10) return 8u;
     uint32_t g = 8192u >> log_l;
     if (g > 64) g = 64;
     if (g < 16) g = 16;
@@ -184,14 +184,17 @@ uint32_t cached_tile_columns(uint32_t log_l, bool rowwise) {
     //    points 16 rows gain nothing over 64.
     if (log_l < 7) return tile_columns(log_l);
     if (rowwise) return log_l == 9 ? 8u : 16u;
-    return log_l > 10 ? 16384u >> log_l : 8u;
+    return 8u;
 }
 
 bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise, bool reads_input) {
     // Measured on gfx950 against the 16-element tiles at 512 MiB per plan (the
     // first pass, us per 128 MiB chunk): 128 points 54.3 -> 50.6, 256: 57.0 ->
     // 54.4 (config 4's pass: 52.8 -> 48.4), 512: 63.4 -> 59.4, 1024: 68.4 ->
-    // 61.0; whole plans 1-5 % faster for every 1D length 2^13 .. 2^24.
+    // 61.0; whole plans 1-5 % faster for every 1D length 2^13 .. 2^24.  The
+    // 2D column passes of 2048 / 4096 points always exchange in halves: twice
+    // the columns per tile in the same LDS (add_tile gives the timings).
+    if (!rowwise && log_l > 10) return true;
     return reads_input && !rowwise && log_l >= 7 && log_l <= 10 && g == tile_columns(log_l);
 }
 
@@ -318,7 +321,17 @@ void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g
     const bool halves = use_halves_tile(log_l, g, rowwise, src == Buf::In);
     Step s;
     s.tile = true;
-    s.xcd_remap = narrow;
+    if (narrow) {
+        // the 16-element tiles: one contiguous tile range per XCD; the halves
+        // tiles (2D columns of 2048 / 4096 points): line groups dealt over the
+        // XCDs, measured on gfx950 at 128 MiB per launch, us per pass over
+        // 4096 / 2048 rows of 128 .. 4096 columns: 8 columns in halves with
+        // line groups 53.8 .. 57.1 / 47.7 .. 51.0, with XCD ranges 52.0 ..
+        // 72.5 / 44.5 .. 56.8 (slowest at 16 MiB images), the 16-element
+        // tiles (4 / 8 columns, XCD ranges) 60.8 .. 69.7 / 54.0 .. 62.5
+        s.tile_order = halves ? FG_TILE_ORDER_LINE_GROUPS : FG_TILE_ORDER_XCD_RANGES;
+        s.order_unit = halves ? 8 * (16 / g) : 8;
+    }
     s.name = tile_name(log_l, g, halves ? 'h' : (rowwise ? 'r' : 'c'), policy);
     s.fn = HipBackend::get_kernel(mod, s.name.c_str());
     s.block = Dim3(g * ((1u << log_l) >> (halves ? 5 : elems_per_thread_log(log_l))));
@@ -575,7 +588,7 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
                 g.flags = flags;
                 g.scale = scale;
                 const uint64_t tiles = s.per_unit * units;
-                g.remap = (s.xcd_remap && tiles % 8 == 0) ? 1u : 0u;
+                g.remap = (s.tile_order != 0 && tiles % s.order_unit == 0) ? s.tile_order : 0u;
                 void* args[] = {&src, &dst, (void*)&tw, (void*)&big, &g};
                 const Dim3 grid((uint32_t)(s.per_unit * units));
                 if (events)

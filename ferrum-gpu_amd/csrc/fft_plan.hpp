@@ -114,7 +114,8 @@ private:
         // Per unit (one transform, or one 2D image): Stockham transforms, or
         // tiles of a tile pass.  A launch over u units has per_unit * u of them.
         uint64_t per_unit = 0;
-        bool xcd_remap = false;                 // tile: XCD-aware tile order when the grid allows
+        uint32_t tile_order = 0;                // tile: TileGeom::remap (FG_TILE_ORDER_*) when the grid
+        uint32_t order_unit = 1;                // is a multiple of order_unit, else the natural order
         TileGeom geom{};                        // tile: addressing (flags/scale/remap set at exec)
     };
 

@@ -352,8 +352,7 @@ struct HalvesShape {
     static constexpr int N = 1 << LOGL, E = 32, T = N / E, HALF = N / 2;
     static constexpr int NFULL = LOGL / 4, REM = LOGL % 4;
     static constexpr int NSTAGES = NFULL + (REM ? 1 : 0);
-    static_assert((LOGL >= 7 && LOGL <= 10) || (LOGL >= 13 && LOGL <= 15),
-                  "half exchanges: 128 .. 1024-point tile columns, 8192 .. 32768-point rows");
+    static_assert(LOGL >= 7 && LOGL <= 15, "half exchanges: 128 .. 4096-point tile columns, 8192 .. 32768-point rows");
 };
 
 template <int LOGL, int S>

@@ -130,15 +130,21 @@ struct TileCoords {
     uint64_t ib, ob;
 };
 
+template <int G>
 __device__ __forceinline__ TileCoords tile_coords(const TileGeom& g) {
     uint32_t b = blockIdx.x;
-    if (g.remap) {
-        // XCD-aware order: workgroups are dealt round-robin over the 8 XCDs,
-        // so XCD x (blockIdx % 8) takes the contiguous tile range
-        // [x * grid/8, (x + 1) * grid/8).  Narrow tiles (4 or 8 columns, 32 or
+    if (g.remap == FG_TILE_ORDER_XCD_RANGES) {
+        // XCD x (blockIdx % 8) takes the contiguous tile range
+        // [x * grid/8, (x + 1) * grid/8): narrow tiles (4 or 8 columns, 32 or
         // 64 bytes of a 128-byte line) then share each line fill of their
         // XCD's L2 instead of each XCD fetching it (host: grid % 8 == 0).
         b = (b & 7u) * (gridDim.x >> 3) + (b >> 3);
+    } else if (g.remap == FG_TILE_ORDER_LINE_GROUPS) {
+        // the S tiles of a line group on one XCD, neighbouring groups on
+        // neighbouring XCDs (host: grid % (8 S) == 0)
+        constexpr uint32_t S = G < 16 ? 16 / G : 1;
+        const uint32_t j = b >> 3;
+        b = ((j / S) * 8u + (b & 7u)) * S + j % S;
     }
     TileCoords tc;
     tc.t0 = b % g.t0n;
@@ -172,7 +178,7 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
     const int tid = threadIdx.x;
     const int c = tid % G;
     const int q = tid / G;
-    const TileCoords tc = tile_coords(g);
+    const TileCoords tc = tile_coords<G>(g);
     const uint32_t t0 = tc.t0, t1 = tc.t1;
     const char* in_tile = reinterpret_cast<const char*>(in + tc.ib);
     char* out_tile = reinterpret_cast<char*>(out + tc.ob);
@@ -238,15 +244,24 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
 // CU instead of two for 128 / 256 points (64 / 32 columns), two 68 KB ones
 // instead of one for 1024 (16 columns), so more of a CU's tiles are loading
 // while others compute.
+// at(d + q*L, c) - at(d, c) for the outputs q of a halves butterfly.  L = 1
+// (stage 0, radix 16) on a position-padded layout: d = 16 b - HALF h is a
+// multiple of 16, so lds_pos(d + q) = lds_pos(d) + q for q < 16.
+template <class Lay, int L, int G>
+constexpr int halves_scatter_step() {
+    if constexpr (Lay::PADPOS && L == 1) return G;
+    else return Lay::template step<L>();
+}
+
 // Exchange after stage S: x[m] = the element at position t + T*m.
 template <int LOGL, int S, int G>
 __device__ __forceinline__ void halves_exchange(const float2* y, float2* x, int t, int c, float2* __restrict__ lds) {
     using H = HalvesShape<LOGL>;
     using St = HalvesStage<LOGL, S>;
     using Lay = TileLayout<LOGL - 1, G>;
-    static_assert(G >= 16, "wide tiles (pitch G + 1)");
-    // at(d + q*L, c) - at(d, c): output q of a butterfly is q*L positions further.
-    constexpr int QSTEP = Lay::template step<St::L>();
+    static_assert(!Lay::PADPOS || St::L > 1 || St::R == 16, "position-padded scatter of stage 0 needs radix 16");
+    static_assert(H::T % 16 == 0 || !Lay::PADPOS, "position-padded reads step by T, a multiple of 16");
+    constexpr int QSTEP = halves_scatter_step<Lay, St::L, G>();
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         if (S > 0 || h > 0) __syncthreads();  // the previous round's readers are done
@@ -286,7 +301,7 @@ __device__ __forceinline__ void fft_tile_halves_body(const float2* __restrict__ 
     const int tid = threadIdx.x;
     const int c = tid % G;
     const int t = tid / G;
-    const TileCoords tc = tile_coords(g);
+    const TileCoords tc = tile_coords<G>(g);
     const char* in_tile = reinterpret_cast<const char*>(in + tc.ib);
     char* out_tile = reinterpret_cast<char*>(out + tc.ob);
 

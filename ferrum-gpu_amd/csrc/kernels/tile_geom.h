@@ -14,6 +14,18 @@ namespace fg {
 #define FG_PASS_CONJ_IN 1u        /* conjugate every element on load */
 #define FG_PASS_CONJ_SCALE_OUT 2u /* conjugate, then multiply by `scale`, on store */
 
+/* Tile orders of narrow tiles (G < 16 columns: 128 / (8 G) tiles share each
+ * 128-byte line).  Workgroups are dealt round-robin over the 8 XCDs, so
+ * workgroup b runs on XCD b % 8 as that XCD's (b / 8)-th.
+ *   XCD_RANGES: XCD x takes the contiguous tile range [x grid/8, (x+1) grid/8)
+ *     (grid a multiple of 8);
+ *   LINE_GROUPS: the groups of s = 16 / G tiles that share lines are dealt
+ *     round-robin over the XCDs: XCD x's j-th workgroup takes tile
+ *     s (8 (j / s) + x) + j mod s (grid a multiple of 8 s), so the XCDs work
+ *     on neighbouring line groups at the same time. */
+#define FG_TILE_ORDER_XCD_RANGES 1u
+#define FG_TILE_ORDER_LINE_GROUPS 2u
+
 /* Addressing of one multi-pass tile pass (see fft_tile.hpp). */
 typedef struct TileGeom {
     uint64_t is0, is1, is2; /* input base = t0*is0 + t1*is1 + t2*is2 */
@@ -25,7 +37,7 @@ typedef struct TileGeom {
     uint32_t log_m;         /* twiddle W_M^(r*k), M = 2^log_m; 0 = none */
     uint32_t flags;         /* FG_PASS_* */
     float scale;
-    uint32_t remap;         /* 1: XCD-aware tile order (grid a multiple of 8; fft_tile.hpp) */
+    uint32_t remap;         /* tile order (fft_tile.hpp, tile_coords): 0 natural, FG_TILE_ORDER_* */
 } TileGeom;
 
 /* One-pass 2D FFT of images of 2^lr x 2^lc <= 16384 points: up to 1024

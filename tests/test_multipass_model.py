@@ -26,9 +26,9 @@ from conftest import rel_l2, uniform_c64
 
 def tile_columns(log_l):
     """Columns per tile of a pass that reads HBM (tile_columns in fft_plan.cpp):
-    16..64 up to 1024 points, 8 / 4 (narrow tiles) for 2048 / 4096."""
+    16..64 up to 1024 points, 8 (narrow tiles) for 2048 / 4096."""
     if log_l > 10:
-        return 16384 >> log_l
+        return 8
     return max(16, min(64, 8192 >> log_l))
 
 
@@ -39,7 +39,7 @@ def cached_tile_columns(log_l, rowwise):
         return tile_columns(log_l)
     if rowwise:
         return 8 if log_l == 9 else 16
-    return 16384 >> log_l if log_l > 10 else 8
+    return 8
 
 
 def split_1d(log_n):
@@ -116,7 +116,10 @@ def pass_policy(i, n, cached, g):
 
 def use_halves_tile(log_l, g, rowwise, reads_input):
     """use_halves_tile in fft_plan.cpp: the column pass that reads the plan's
-    input runs the 32-element kernel with the exchanges in halves."""
+    input, and every column pass of 2048 / 4096 points, runs the 32-element
+    kernel with the exchanges in halves."""
+    if not rowwise and log_l > 10:
+        return True
     return reads_input and not rowwise and 7 <= log_l <= 10 and g == tile_columns(log_l)
 
 
@@ -148,8 +151,28 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None):
 
 
 def xcd_remap(b, grid):
-    """Tile handled by workgroup b under the XCD-aware order (kernels/fft_tile.hpp)."""
+    """Tile handled by workgroup b under the XCD-range order (FG_TILE_ORDER_XCD_RANGES,
+    tile_coords in kernels/fft_tile.hpp)."""
     return (b & 7) * (grid >> 3) + (b >> 3)
+
+
+def line_group_order(b, g):
+    """Tile handled by workgroup b under the line-group order
+    (FG_TILE_ORDER_LINE_GROUPS): groups of s = 16 / g tiles dealt over the XCDs."""
+    s = 16 // g if g < 16 else 1
+    j = b >> 3
+    return ((j // s) * 8 + (b & 7)) * s + j % s
+
+
+def tile_order(log_l, g, rowwise, reads_input, tiles):
+    """TileGeom::remap of a pass (add_tile / exec in fft_plan.cpp): narrow tiles
+    take the line-group order in halves, the XCD-range order otherwise, each
+    only when the grid is a multiple of its unit; wide tiles the natural one."""
+    if g >= 16:
+        return 0
+    if use_halves_tile(log_l, g, rowwise, reads_input):
+        return 2 if tiles % (8 * (16 // g)) == 0 else 0
+    return 1 if tiles % 8 == 0 else 0
 
 
 def tile_lds_index(log_l, g, pos, c):
@@ -250,7 +273,41 @@ def test_xcd_remap_is_a_permutation_grouping_neighbours(grid):
         assert (b & 7) * per <= tiles[b] < ((b & 7) + 1) * per
 
 
-@pytest.mark.parametrize("log_l,g", [(12, 4), (11, 8), (10, 16), (10, 8), (9, 8), (8, 32), (8, 16), (8, 8),
+@pytest.mark.parametrize("grid,g", [(16, 8), (32, 8), (512, 8), (1024, 8), (8 * 1000, 8), (32, 4), (4096, 4)])
+def test_line_group_order_is_a_permutation_keeping_lines_on_one_xcd(grid, g):
+    s = 16 // g
+    assert grid % (8 * s) == 0
+    tiles = [line_group_order(b, g) for b in range(grid)]
+    assert sorted(tiles) == list(range(grid))
+    for b in range(grid):
+        # the tiles sharing a 128-byte line (one group of s) run on one XCD,
+        # as consecutive workgroups of that XCD
+        grp, r = divmod(tiles[b], s)
+        assert grp % 8 == b % 8
+        assert (b >> 3) % s == r
+    # each dispatch round of 8 s workgroups covers 8 neighbouring line groups
+    for base in range(0, grid, 8 * s):
+        assert sorted(tiles[base:base + 8 * s]) == list(range(base, base + 8 * s))
+
+
+def test_tile_orders_of_the_2d_column_passes():
+    # 4096 / 2048 rows: 8 columns in halves, line groups when the grid allows
+    for log_rows in (11, 12):
+        for log_cols in range(4, 13):
+            p = tile_geometry_2d(log_rows, 1, log_cols)[0]
+            assert p["g"] == 8 and use_halves_tile(log_rows, 8, False, False)
+            # a full 128 MiB chunk: 2^21 / R tiles whatever C, so always line groups
+            units = (128 << 20) // (8 << (log_rows + log_cols))
+            tiles = p["t0n"] * units
+            assert tiles == (1 << 21) >> log_rows
+            assert tile_order(log_rows, 8, False, False, tiles) == 2
+    # a short last chunk whose grid is no multiple of 16 keeps the natural order
+    assert tile_order(12, 8, False, False, 2 * 3) == 0
+    # 1024 rows: the 16-element narrow tile, XCD ranges
+    assert tile_order(10, 8, False, False, 1024) == 1
+
+
+@pytest.mark.parametrize("log_l,g", [(11, 8), (10, 16), (10, 8), (9, 8), (8, 32), (8, 16), (8, 8),
                                      (7, 8), (6, 64), (6, 16)])
 def test_tile_lds_layout_is_injective_and_fits(log_l, g):
     n = 1 << log_l
@@ -262,10 +319,12 @@ def test_tile_lds_layout_is_injective_and_fits(log_l, g):
 
 
 def test_long_column_widths():
-    # 2048 / 4096-point digits: 8 / 4 columns per tile, 1024 threads of 16 elements
-    for log_n, g in ((11, 8), (12, 4)):
-        assert tile_columns(log_n) == g == cached_tile_columns(log_n, False)
-        assert g * (1 << log_n) // 16 == 1024
+    # 2048 / 4096-point columns: 8 per tile, 32 elements per thread (512 / 1024
+    # threads), the halves of a 4096-point tile in 136 KB of LDS
+    for log_n, threads in ((11, 512), (12, 1024)):
+        assert tile_columns(log_n) == 8 == cached_tile_columns(log_n, False)
+        assert 8 * (1 << log_n) // 32 == threads
+    assert tile_lds_elems(11, 8) * 8 == 136 * 1024
 
 
 def test_split_sizes_fit_the_tile_kernel():

@@ -10,11 +10,16 @@ j*L_s*R + k + q*L_s (j = b / L_s, k = b % L_s), which lies below L/2 exactly
 when i < NB/2, so each exchange runs in two rounds through an LDS tile of
 L/2 positions: round h writes butterflies i in [h*NB/2, (h+1)*NB/2), then
 every thread reads its elements m in [16h, 16h + 16).  The model keeps that
-bookkeeping with the kernel's LDS layout (positions x columns, pitch G + 1;
-G >= 16) and checks every write in bounds and distinct
-within its round, every read written in the same round, and the last
-stage's outputs at the thread's own positions t + T*m.  Only the DFT-R is
-numpy's; the stage twiddles come from the host's table for the radix list.
+bookkeeping with the kernel's LDS layouts (TileLayout<LOGL - 1, G>: positions
+x columns with pitch G + 1 for G >= 16; pitch G with one pad row per 16
+positions for the narrow 2048 / 4096-point tiles, G = 8), forms every write
+address the way halves_exchange does (a base at the butterfly's first output
+plus q times a compile-time step) and every read address as a base plus m
+times step<T>, checks each against the layout's own index of the position,
+every write in bounds and distinct within its round, every read written in
+the same round, and the last stage's outputs at the thread's own positions
+t + T*m.  Only the DFT-R is numpy's; the stage twiddles come from the host's
+table for the radix list.
 """
 
 from __future__ import annotations
@@ -34,13 +39,28 @@ def radices(log_l):
 
 
 def lds_index(pos, c, g):
-    """TileLayout<LOGL - 1, G>::at for G >= 16."""
-    assert g >= 16
+    """TileLayout<LOGL - 1, G>::at: pitch G + 1 for G >= 16, else lds_pos(pos) * G."""
+    if g < 16:
+        return (pos + (pos >> 4)) * g + c
     return pos * (g + 1) + c
 
 
 def lds_elems(log_l, g):
-    return (1 << (log_l - 1)) * (g + 1)
+    half = 1 << (log_l - 1)
+    return (half + half // 16) * g if g < 16 else half * (g + 1)
+
+
+def layout_step(d, g):
+    """TileLayout::step<D>: at(pos + D, c) - at(pos, c) for D a multiple of 16."""
+    if g < 16:
+        assert d % 16 == 0
+        return (d + d // 16) * g
+    return d * (g + 1)
+
+
+def scatter_step(L, g):
+    """halves_scatter_step: the step between a butterfly's outputs q and q + 1."""
+    return g if (g < 16 and L == 1) else layout_step(L, g)
 
 
 def halves_model(cols, log_l):
@@ -76,14 +96,18 @@ def halves_model(cols, log_l):
             break
         new = np.empty_like(regs)
         lds = np.zeros(lds_elems(log_l, g), np.complex128)
+        assert g >= 16 or L > 1 or R == 16
         for h in range(2):
             written = np.zeros(lds.size, dtype=bool)
             for i in range(h * NB // 2, (h + 1) * NB // 2):
+                b = t + T * i
+                d0 = (b >> (4 * s)) * L * R + (b & (L - 1)) - half * h
                 for q in range(R):
                     d = dst[:, i + NB * q]
                     assert np.all((d >= half * h) & (d < half * (h + 1))), (log_l, s, i, q)
                     for c in range(g):
-                        idx = lds_index(d - half * h, c, g)
+                        idx = lds_index(d0, c, g) + q * scatter_step(L, g)
+                        assert np.array_equal(idx, lds_index(d - half * h, c, g))
                         assert idx.max() < lds.size
                         assert not written[idx].any()
                         written[idx] = True
@@ -91,7 +115,8 @@ def halves_model(cols, log_l):
             assert written.sum() == half * g
             for m in range(E // 2):
                 for c in range(g):
-                    idx = lds_index(t + T * m, c, g)
+                    idx = lds_index(t, c, g) + m * layout_step(T, g)
+                    assert np.array_equal(idx, lds_index(t + T * m, c, g))
                     assert written[idx].all()
                     new[c, :, (E // 2) * h + m] = lds[idx]
         regs = new
@@ -188,9 +213,10 @@ def test_row_halves_fit_the_hardware(log_n):
     assert (2 if log_n < 15 else 1) * lds <= 160 * 1024, lds
 
 
-# (log_l, G): the instantiated kernels (FG_TILE_HALVES), the widths of the
-# passes that read HBM
-CASES = [(7, 64), (8, 32), (9, 16), (10, 16)]
+# (log_l, G): the instantiated kernels, FG_TILE_HALVES (the widths of the
+# passes that read HBM) and FG_TILE_HALVES_NARROW (2D columns of 2048 / 4096
+# points)
+CASES = [(7, 64), (8, 32), (9, 16), (10, 16), (11, 8), (12, 8)]
 
 
 @pytest.mark.parametrize("log_l,g", CASES)
@@ -209,3 +235,26 @@ def test_halves_tiles_halve_the_lds(log_l, g):
     whole = (1 << log_l) * (g + 1) * 8
     assert lds_elems(log_l, g) * 8 * 2 == whole
     assert g * ((1 << log_l) // E) <= 1024
+
+
+@pytest.mark.parametrize("log_l,g,threads,kib", [(11, 8, 512, 68), (12, 8, 1024, 136)])
+def test_narrow_halves_tiles_fit_a_cu(log_l, g, threads, kib):
+    # twice the columns of the 16-element narrow tiles (8 / 4) in the same or
+    # half the LDS; the layout is injective and inside its array
+    assert g * ((1 << log_l) // E) == threads
+    assert lds_elems(log_l, g) * 8 == kib * 1024 <= 160 * 1024
+    half = 1 << (log_l - 1)
+    pos, c = np.meshgrid(np.arange(half), np.arange(g), indexing="ij")
+    idx = lds_index(pos, c, g)
+    assert len(np.unique(idx)) == half * g and idx.max() < lds_elems(log_l, g)
+
+
+def test_narrow_halves_kernels_are_instantiated():
+    import os
+    import re
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
+    got = {(int(a), int(b)) for a, b in re.findall(r"^FG_TILE_HALVES_NARROW\((\d+), (\d+)\)", src, flags=re.M)}
+    assert got == {(11, 8), (12, 8)}
+    hpp = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_tile.hpp")).read()
+    assert "if constexpr (Lay::PADPOS && L == 1) return G;" in hpp
