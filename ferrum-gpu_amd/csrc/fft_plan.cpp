@@ -191,11 +191,17 @@ bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise, bool reads_input)
     // Measured on gfx950 against the 16-element tiles at 512 MiB per plan (the
     // first pass, us per 128 MiB chunk): 128 points 54.3 -> 50.6, 256: 57.0 ->
     // 54.4 (config 4's pass: 52.8 -> 48.4), 512: 63.4 -> 59.4, 1024: 68.4 ->
-    // 61.0; whole plans 1-5 % faster for every 1D length 2^13 .. 2^24.  The
-    // 2D column passes of 2048 / 4096 points always exchange in halves: twice
-    // the columns per tile in the same LDS (add_tile gives the timings).
-    if (!rowwise && log_l > 10) return true;
-    return reads_input && !rowwise && log_l >= 7 && log_l <= 10 && g == tile_columns(log_l);
+    // 61.0; whole plans 1-5 % faster for every 1D length 2^13 .. 2^24.
+    //
+    // 2D column passes over cache-resident data in 8-column tiles: 2048 /
+    // 4096 points always exchange in halves (twice the columns per tile in
+    // the same LDS; add_tile gives the timings); 1024 points too, 46.6 ..
+    // 52.5 -> 44.7 .. 48.5 us per 128 MiB pass at 64 .. 4096 columns; 512
+    // points lose (41.5 .. 46.7 -> 45.8 .. 47.3).
+    if (rowwise) return false;
+    if (log_l > 10) return true;
+    if (reads_input) return log_l >= 7 && g == tile_columns(log_l);
+    return log_l == 10 && g == 8;
 }
 
 bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }
@@ -323,7 +329,7 @@ void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g
     s.tile = true;
     if (narrow) {
         // the 16-element tiles: one contiguous tile range per XCD; the halves
-        // tiles (2D columns of 2048 / 4096 points): line groups dealt over the
+        // tiles (2D columns of 1024 .. 4096 points): line groups dealt over the
         // XCDs, measured on gfx950 at 128 MiB per launch, us per pass over
         // 4096 / 2048 rows of 128 .. 4096 columns: 8 columns in halves with
         // line groups 53.8 .. 57.1 / 47.7 .. 51.0, with XCD ranges 52.0 ..

@@ -364,7 +364,6 @@ FG_TILE(10, 16, false, c)
 FG_TILE_NARROW(7, 8, false, c)
 FG_TILE_NARROW(8, 8, false, c)
 FG_TILE_NARROW(9, 8, false, c)
-FG_TILE_NARROW(10, 8, false, c)
 // First pass of a 1D multi-pass plan (input from HBM): the same column DFTs
 // and four-step twiddle with 32 elements per thread and the exchanges in
 // halves (fft_tile_halves_body): half the LDS of the tiles above, so twice
@@ -384,9 +383,11 @@ FG_TILE_HALVES(7, 64)
 FG_TILE_HALVES(8, 32)
 FG_TILE_HALVES(9, 16)
 FG_TILE_HALVES(10, 16)
-// 2D column passes of 2048 / 4096 rows (cached in and out, like every narrow
-// tile): 8 columns per tile, 512 / 1024 threads, 68 / 136 KB of LDS.
+// 2D column passes of 1024 / 2048 / 4096 rows (cached in and out, like every
+// narrow tile): 8 columns per tile, 256 / 512 / 1024 threads, 34 / 68 / 136 KB
+// of LDS.
 #define FG_TILE_HALVES_NARROW(LOGL, G) FG_TILE_HALVES_P(LOGL, G, _cc, true, true)
+FG_TILE_HALVES_NARROW(10, 8)
 FG_TILE_HALVES_NARROW(11, 8)
 FG_TILE_HALVES_NARROW(12, 8)
 // Row passes (last 1D digit: rows contiguous, transposed store): the widths

@@ -116,11 +116,15 @@ def pass_policy(i, n, cached, g):
 
 def use_halves_tile(log_l, g, rowwise, reads_input):
     """use_halves_tile in fft_plan.cpp: the column pass that reads the plan's
-    input, and every column pass of 2048 / 4096 points, runs the 32-element
-    kernel with the exchanges in halves."""
-    if not rowwise and log_l > 10:
+    input, and the cache-resident 8-column passes of 1024 .. 4096 points, run
+    the 32-element kernel with the exchanges in halves."""
+    if rowwise:
+        return False
+    if log_l > 10:
         return True
-    return reads_input and not rowwise and 7 <= log_l <= 10 and g == tile_columns(log_l)
+    if reads_input:
+        return 7 <= log_l and g == tile_columns(log_l)
+    return log_l == 10 and g == 8
 
 
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None):
@@ -292,7 +296,7 @@ def test_line_group_order_is_a_permutation_keeping_lines_on_one_xcd(grid, g):
 
 def test_tile_orders_of_the_2d_column_passes():
     # 4096 / 2048 rows: 8 columns in halves, line groups when the grid allows
-    for log_rows in (11, 12):
+    for log_rows in (10, 11, 12):
         for log_cols in range(4, 13):
             p = tile_geometry_2d(log_rows, 1, log_cols)[0]
             assert p["g"] == 8 and use_halves_tile(log_rows, 8, False, False)
@@ -303,8 +307,10 @@ def test_tile_orders_of_the_2d_column_passes():
             assert tile_order(log_rows, 8, False, False, tiles) == 2
     # a short last chunk whose grid is no multiple of 16 keeps the natural order
     assert tile_order(12, 8, False, False, 2 * 3) == 0
-    # 1024 rows: the 16-element narrow tile, XCD ranges
-    assert tile_order(10, 8, False, False, 1024) == 1
+    # 1024 rows: 8 columns in halves too; 512 rows: the 16-element narrow
+    # tile in XCD ranges
+    assert tile_order(10, 8, False, False, 2048) == 2
+    assert tile_order(9, 8, False, False, 4096) == 1
 
 
 @pytest.mark.parametrize("log_l,g", [(11, 8), (10, 16), (10, 8), (9, 8), (8, 32), (8, 16), (8, 8),

@@ -12,7 +12,7 @@ L/2 positions: round h writes butterflies i in [h*NB/2, (h+1)*NB/2), then
 every thread reads its elements m in [16h, 16h + 16).  The model keeps that
 bookkeeping with the kernel's LDS layouts (TileLayout<LOGL - 1, G>: positions
 x columns with pitch G + 1 for G >= 16; pitch G with one pad row per 16
-positions for the narrow 2048 / 4096-point tiles, G = 8), forms every write
+positions for the narrow 1024- to 4096-point tiles, G = 8), forms every write
 address the way halves_exchange does (a base at the butterfly's first output
 plus q times a compile-time step) and every read address as a base plus m
 times step<T>, checks each against the layout's own index of the position,
@@ -214,9 +214,9 @@ def test_row_halves_fit_the_hardware(log_n):
 
 
 # (log_l, G): the instantiated kernels, FG_TILE_HALVES (the widths of the
-# passes that read HBM) and FG_TILE_HALVES_NARROW (2D columns of 2048 / 4096
+# passes that read HBM) and FG_TILE_HALVES_NARROW (2D columns of 1024 .. 4096
 # points)
-CASES = [(7, 64), (8, 32), (9, 16), (10, 16), (11, 8), (12, 8)]
+CASES = [(7, 64), (8, 32), (9, 16), (10, 16), (10, 8), (11, 8), (12, 8)]
 
 
 @pytest.mark.parametrize("log_l,g", CASES)
@@ -237,7 +237,7 @@ def test_halves_tiles_halve_the_lds(log_l, g):
     assert g * ((1 << log_l) // E) <= 1024
 
 
-@pytest.mark.parametrize("log_l,g,threads,kib", [(11, 8, 512, 68), (12, 8, 1024, 136)])
+@pytest.mark.parametrize("log_l,g,threads,kib", [(10, 8, 256, 34), (11, 8, 512, 68), (12, 8, 1024, 136)])
 def test_narrow_halves_tiles_fit_a_cu(log_l, g, threads, kib):
     # twice the columns of the 16-element narrow tiles (8 / 4) in the same or
     # half the LDS; the layout is injective and inside its array
@@ -255,6 +255,6 @@ def test_narrow_halves_kernels_are_instantiated():
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     src = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
     got = {(int(a), int(b)) for a, b in re.findall(r"^FG_TILE_HALVES_NARROW\((\d+), (\d+)\)", src, flags=re.M)}
-    assert got == {(11, 8), (12, 8)}
+    assert got == {(10, 8), (11, 8), (12, 8)}
     hpp = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_tile.hpp")).read()
     assert "if constexpr (Lay::PADPOS && L == 1) return G;" in hpp
