@@ -236,14 +236,18 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
 }
 
 // ---------------------------------------------------------------------------
-// Column pass with the Stockham exchanges in halves (the first pass of a 1D
-// multi-pass plan, which reads the caller's input from HBM): the 32-element
-// stages of fft_stockham.hpp (HalvesShape, halves_stage) on every column of
-// the tile, each exchange in two rounds through an LDS tile of L/2
-// positions.  Half the LDS of the 16-element tile: four 33 KB workgroups per
-// CU instead of two for 128 / 256 points (64 / 32 columns), two 68 KB ones
-// instead of one for 1024 (16 columns), so more of a CU's tiles are loading
-// while others compute.
+// Column pass with the Stockham exchanges in halves: the 32-element stages of
+// fft_stockham.hpp (HalvesShape, halves_stage) on every column of the tile,
+// each exchange in two rounds through an LDS tile of L/2 positions.
+//  * The first pass of a 1D multi-pass plan (which reads the caller's input
+//    from HBM), wide tiles: half the LDS of the 16-element tile, four 33 KB
+//    workgroups per CU instead of two for 128 / 256 points (64 / 32
+//    columns), two 68 KB ones instead of one for 1024 (16 columns), so more
+//    of a CU's tiles are loading while others compute.
+//  * 2D column passes of 1024 .. 4096 points, narrow tiles (8 columns, the
+//    position-padded layout): twice the columns of the 16-element tile in the
+//    same LDS (136 KB at 4096 points), so 64-byte row pieces instead of 32.
+
 // at(d + q*L, c) - at(d, c) for the outputs q of a halves butterfly.  L = 1
 // (stage 0, radix 16) on a position-padded layout: d = 16 b - HALF h is a
 // multiple of 16, so lds_pos(d + q) = lds_pos(d) + q for q < 16.
