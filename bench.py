@@ -262,6 +262,12 @@ class FftWorkload:
         self.launch_names = kernels * len(steps)
         self.launch_keys = [f"{i % passes}:{k}" for _ in steps for i, k in enumerate(kernels)]
         self.bytes_per_launch = 16 * self.elems * units
+        # Two-stream plans run the odd chunks on the plan's second stream:
+        # launch i of an execution (chunk i // passes) stamps its event there.
+        self.streams = 1 if layout == "split" else self.describe["streams"]
+        L = len(kernels)
+        self.launch_streams = [(i // passes) % 2 if self.streams == 2 else 0 for _ in steps for i in range(L)]
+        self.exec_bounds = [(j * L, (j + 1) * L) for j in range(len(steps))]
 
     def bind_events(self, events):
         """The per-step form run() takes of one step's launch events (built
@@ -395,6 +401,9 @@ class OpWorkload:
         self.kernels = [kernel]
         self.launch_names = [kernel]
         self.launch_keys = [f"0:{kernel}"]
+        self.streams = 1
+        self.launch_streams = [0]
+        self.exec_bounds = [(0, 1)]
         self.bytes_per_launch = self.algo_bytes
         self.copy_bufs = (self.d_in[0], self.d_out[0], (min(self.d_in[0].nbytes, self.d_out[0].nbytes) // 16) * 16)
         self.describe = {"launches": 1, "main_kernel": kernel, "workspace_bytes": 0}
@@ -575,6 +584,26 @@ def clock_ramp(N, dev, wl, stream, ramp_ms: float):
             "note": "untimed plain-copy launches before the warmup steps (clock ramp), not workload steps"}
 
 
+def launch_durations(start, evs, wl) -> dict:
+    """Per-launch GPU time from the events stamped after each launch of the
+    timed steps (evs[k][i], launch i of step k): launch i ran from the
+    previous event on its own stream, or from the end of the previous plan
+    execution (the latest event of it, where a two-stream plan forks), to its
+    own event.  One-stream plans: the gap between consecutive events."""
+    t = [[start.elapsed_ms(e) for e in row] for row in evs]
+    out: dict[str, list[float]] = {}
+    exec_start = 0.0
+    for k in range(len(evs)):
+        for lo, hi in wl.exec_bounds:
+            last: dict[int, float] = {}
+            for i in range(lo, hi):
+                s = wl.launch_streams[i]
+                out.setdefault(wl.launch_keys[i], []).append(t[k][i] - last.get(s, exec_start))
+                last[s] = t[k][i]
+            exec_start = max(t[k][lo:hi])
+    return out
+
+
 def steady_state(np, per_kernel, dominant_key: str, graph: bool):
     """Whether the timed launches ran at a steady clock: the median duration of
     the dominant kernel's first quarter of timed launches against its last
@@ -677,11 +706,7 @@ def main() -> int:
             dev.sync()
             wall = time.perf_counter() - t0
         log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms")
-        prev = start
-        for k in range(args.steps):
-            for i, key in enumerate(wl.launch_keys):
-                per_kernel.setdefault(key, []).append(prev.elapsed_ms(evs[k][i]))
-                prev = evs[k][i]
+        per_kernel = launch_durations(start, evs, wl)
     else:
         # G steps per graph, replayed steps / G times between two events: the
         # GPU time per launch is the replay time over all the launches in it
@@ -795,7 +820,8 @@ def main() -> int:
     if args.graph:
         result["launch_mode"] = f"HIP graph of {args.graph} steps per replay"
     else:
-        result["launch_mode"] = "one host launch per kernel, one event after each"
+        result["launch_mode"] = "one host launch per kernel, one event after each" + (
+            "; odd chunks on the plan's second stream" if wl.streams == 2 else "")
 
     gate = gate_check(result, args.min_frac)
     if gate is not None:

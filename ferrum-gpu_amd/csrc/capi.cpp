@@ -662,6 +662,14 @@ int fg_fft_plan_chunking(fg_fft_plan_t plan, int* passes, size_t* units_per_chun
     });
 }
 
+int fg_fft_plan_streams(fg_fft_plan_t plan, int* streams) {
+    return guarded([&] {
+        need(plan, "plan");
+        need(streams, "streams");
+        *streams = plan->plan->streams();
+    });
+}
+
 int fg_fft_plan_describe(fg_fft_plan_t plan, int* launches, char* main_kernel, size_t cap,
                          size_t* workspace_bytes) {
     return guarded([&] {

@@ -349,6 +349,27 @@ void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g
     steps_.push_back(s);
 }
 
+FftPlan::ChunkStream::ChunkStream(const HipBackend::DeviceHandle& d) : dev(d) {
+    HipBackend::bind(dev);
+    hip_check(hipEventCreateWithFlags(&fork, hipEventDisableTiming), "hipEventCreateWithFlags");
+    hipError_t e = hipEventCreateWithFlags(&join, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);  // default priority
+    if (e != hipSuccess) {
+        if (join) (void)hipEventDestroy(join);
+        (void)hipEventDestroy(fork);
+        hip_check(e, "hipStreamCreateWithFlags");
+    }
+}
+
+FftPlan::ChunkStream::~ChunkStream() {
+    try {
+        HipBackend::destroy_stream(dev, stream);  // waits for the stream's work
+    } catch (...) {
+    }
+    (void)hipEventDestroy(fork);
+    (void)hipEventDestroy(join);
+}
+
 std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_n,
                                           size_t batch) {
     if (log_n < kMinLogN1D || log_n > kMaxLogN1D)
@@ -424,6 +445,19 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         t.ocs = 1;
         t.oes = N / L;
         p->add_tile(mod, log_l, g, true, t, (uint64_t)t.t0n * t.t1n, Buf::Work, Buf::Out, p->policy(P - 1, P));
+        if (p->chunks() > 1 && g >= 16) {
+            // Two chunks in flight, one per stream: their passes overlap, so
+            // one chunk's transform phases fill the other's memory phases.
+            // Measured on gfx950 at 512 MiB in chunks of 128 MiB (us per
+            // execution, one stream -> two): 2^16 347 -> 328, 2^17 380 -> 348,
+            // 2^20 446 -> 403, 2^21 .. 2^24 510 .. 519 -> 481 .. 485.  Not
+            // when the last pass stores 8-row tiles (512-point rows: 2^18,
+            // 2^19 went 397 / 405 -> 502 / 515), nor for 2D plans (four
+            // 4096 x 4096 images 425 -> 466): narrow pieces of one line meet
+            // in an XCD's L2 only while a single chunk streams through it.
+            p->work2_ = dev.alloc<Cf32>(N * p->chunk_);
+            p->aux_.reset(new ChunkStream(dev.handle()));
+        }
     }
     p->main_kernel_ = p->steps_[0].name;
     p->pw_ = Pointwise(mod);
@@ -551,15 +585,31 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
     const float scale = scale_for(dir, normalize);
     const void* big = big_.data();
     const uint64_t unit = elems();
+    const hipStream_t main = stream ? stream : HipBackend::default_stream(dev_->handle());
+    bool two = aux_ != nullptr;
+    if (two) {
+        // Under stream capture the plan stays on the captured stream.
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        HipBackend::bind(dev_->handle());
+        hip_check(hipStreamIsCapturing(main, &st), "hipStreamIsCapturing");
+        two = st == hipStreamCaptureStatusNone;
+    }
+    if (two) {
+        hip_check(hipEventRecord(aux_->fork, main), "hipEventRecord");
+        hip_check(hipStreamWaitEvent(aux_->stream, aux_->fork, 0), "hipStreamWaitEvent");
+    }
     size_t launch = 0;
-    for (uint64_t u0 = 0; u0 < batch_; u0 += chunk_) {
+    size_t chunk = 0;
+    for (uint64_t u0 = 0; u0 < batch_; u0 += chunk_, ++chunk) {
         const uint64_t units = std::min<uint64_t>(chunk_, batch_ - u0);
-        // The caller's arrays are offset to the chunk; the workspace holds one chunk.
+        const bool odd = two && (chunk & 1);
+        const hipStream_t cs = odd ? aux_->stream : main;
+        // The caller's arrays are offset to the chunk; a workspace holds one chunk.
         auto bind = [&](Buf b) -> void* {
             switch (b) {
                 case Buf::In: return const_cast<Cf32*>(static_cast<const Cf32*>(in)) + u0 * unit;
                 case Buf::Out: return static_cast<Cf32*>(out) + u0 * unit;
-                default: return work_.data();
+                default: return odd ? work2_.data() : work_.data();
             }
         };
         for (size_t i = 0; i < steps_.size(); ++i) {
@@ -577,18 +627,18 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
                 void* args[] = {&src, &dst, (void*)&tw, (void*)&twc, &count, &sc, &flags};
                 const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
                 if (events)
-                    HipBackend::launch_stamped(dev_->handle(), stream, s.fn, grid, s.block, 0, args, events[launch]);
+                    HipBackend::launch_stamped(dev_->handle(), cs, s.fn, grid, s.block, 0, args, events[launch]);
                 else
-                    HipBackend::launch(dev_->handle(), stream, s.fn, grid, s.block, 0, args);
+                    HipBackend::launch(dev_->handle(), cs, s.fn, grid, s.block, 0, args);
             } else if (!s.tile) {
                 uint64_t count = s.per_unit * units;
                 float sc = scale;
                 void* args[] = {&src, &dst, (void*)&tw, &count, &sc, &flags};
                 const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
                 if (events)
-                    HipBackend::launch_stamped(dev_->handle(), stream, s.fn, grid, s.block, 0, args, events[launch]);
+                    HipBackend::launch_stamped(dev_->handle(), cs, s.fn, grid, s.block, 0, args, events[launch]);
                 else
-                    HipBackend::launch(dev_->handle(), stream, s.fn, grid, s.block, 0, args);
+                    HipBackend::launch(dev_->handle(), cs, s.fn, grid, s.block, 0, args);
             } else {
                 TileGeom g = s.geom;
                 g.flags = flags;
@@ -598,12 +648,16 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
                 void* args[] = {&src, &dst, (void*)&tw, (void*)&big, &g};
                 const Dim3 grid((uint32_t)(s.per_unit * units));
                 if (events)
-                    HipBackend::launch_stamped(dev_->handle(), stream, s.fn, grid, s.block, 0, args, events[launch]);
+                    HipBackend::launch_stamped(dev_->handle(), cs, s.fn, grid, s.block, 0, args, events[launch]);
                 else
-                    HipBackend::launch(dev_->handle(), stream, s.fn, grid, s.block, 0, args);
+                    HipBackend::launch(dev_->handle(), cs, s.fn, grid, s.block, 0, args);
             }
             ++launch;
         }
+    }
+    if (two) {
+        hip_check(hipEventRecord(aux_->join, aux_->stream), "hipEventRecord");
+        hip_check(hipStreamWaitEvent(main, aux_->join, 0), "hipStreamWaitEvent");
     }
 }
 

@@ -54,11 +54,18 @@ public:
     // Forward or inverse transform of batch transforms from in to out (may alias).
     // Multi-launch plans run chunk by chunk: every pass over chunk_units()
     // transforms (images) before the next chunk, so a chunk's intermediate
-    // array stays in the Infinity Cache (chunk_bytes()).
-    // With `events` (launches() of them), events[i] is recorded on the stream
-    // right after launch i.
+    // array stays in the Infinity Cache (chunk_bytes()).  Plans with
+    // streams() == 2 run the odd chunks on a second stream of their own, with
+    // a second workspace, forked from `stream` at the start and joined back
+    // at the end (on a capturing stream: every chunk on `stream`).
+    // With `events` (launches() of them), events[i] is recorded right after
+    // launch i on the stream launch i runs on (chunk_stream()).
     void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
               hipEvent_t* events = nullptr) const;
+    // 1, or 2 for multi-pass 1D plans of two or more chunks.
+    int streams() const { return aux_ ? 2 : 1; }
+    // The stream a chunk's launches run on: 0 the caller's, 1 the plan's own.
+    int chunk_stream(size_t chunk) const { return aux_ ? (int)(chunk & 1) : 0; }
     // exec() on the split layout: real and imaginary parts in separate f32
     // arrays of batch * elems() each (the reference's *_split kernels,
     // kernels_body.rs:509-626).  Single-pass plans read and write the split
@@ -93,7 +100,7 @@ public:
     // Whether intermediate arrays are kept cached (chunk fits the cache limit).
     bool cache_resident() const { return cached_; }
     const std::string& main_kernel() const { return main_kernel_; }
-    size_t workspace_bytes() const { return work_.bytes(); }
+    size_t workspace_bytes() const { return work_.bytes() + work2_.bytes(); }
     // Kernel names in launch order.
     std::vector<std::string> kernel_names() const;
 
@@ -117,6 +124,18 @@ private:
         uint32_t tile_order = 0;                // tile: TileGeom::remap (FG_TILE_ORDER_*) when the grid
         uint32_t order_unit = 1;                // is a multiple of order_unit, else the natural order
         TileGeom geom{};                        // tile: addressing (flags/scale/remap set at exec)
+    };
+
+    // The second stream of a two-stream plan and its fork / join events,
+    // released with the plan (after the stream's work is done).
+    struct ChunkStream {
+        explicit ChunkStream(const HipBackend::DeviceHandle& dev);
+        ~ChunkStream();
+        ChunkStream(const ChunkStream&) = delete;
+        ChunkStream& operator=(const ChunkStream&) = delete;
+        HipBackend::DeviceHandle dev;
+        hipStream_t stream = nullptr;
+        hipEvent_t fork = nullptr, join = nullptr;
     };
 
     FftPlan(HipDevice& dev, Kind kind, uint32_t log_n, uint32_t log_rows, size_t batch)
@@ -155,6 +174,8 @@ private:
     std::vector<std::pair<uint32_t, Buffer<Cf32, HipBackend>>> stage_tables_;
     Buffer<Cf32, HipBackend> big_;
     Buffer<Cf32, HipBackend> work_;
+    Buffer<Cf32, HipBackend> work2_;         // the odd chunks' workspace (two-stream plans)
+    std::unique_ptr<ChunkStream> aux_;       // two-stream plans: the odd chunks' stream
     std::string main_kernel_;
     HipBackend::KernelHandle split_fn_ = nullptr;  // single-pass plans: the split-layout twin
     Pointwise pw_;

@@ -278,9 +278,11 @@ class _Plan:
         passes, units, chunks, cached = ctypes.c_int(), ctypes.c_size_t(), ctypes.c_int(), ctypes.c_int()
         _n.check(_n.lib.fg_fft_plan_chunking(self._p, ctypes.byref(passes), ctypes.byref(units),
                                              ctypes.byref(chunks), ctypes.byref(cached)))
+        streams = ctypes.c_int()
+        _n.check(_n.lib.fg_fft_plan_streams(self._p, ctypes.byref(streams)))
         return {"launches": launches.value, "main_kernel": name.value.decode(), "workspace_bytes": ws.value,
                 "passes": passes.value, "units_per_chunk": units.value, "chunks": chunks.value,
-                "cache_resident": bool(cached.value)}
+                "cache_resident": bool(cached.value), "streams": streams.value}
 
     def destroy(self) -> None:
         """Free the plan; refused (FerrumGpuError) while graphs of it exist."""

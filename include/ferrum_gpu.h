@@ -151,15 +151,18 @@ FG_API int fg_fft_plan_destroy(fg_fft_plan_t plan);
  * they may be equal (in place) but must not otherwise overlap.
  * direction: FG_FORWARD or FG_INVERSE.  stream NULL = device default stream.
  * A multi-launch plan (1D N > 32768, 2D images above 16384 points) keeps one
- * workspace (and one split-layout staging buffer): executions of one plan
- * must be ordered, one stream at a time; run concurrent work on separate
- * plans. */
+ * workspace (two for two-stream plans, fg_fft_plan_streams) and one
+ * split-layout staging buffer: executions of one plan must be ordered, one
+ * stream at a time; run concurrent work on separate plans. */
 FG_API int fg_fft_exec(fg_fft_plan_t plan, const void *d_in, void *d_out, int direction, int normalize,
                 fg_stream_t stream);
-/* fg_fft_exec that also records events[i] on the stream right after launch i
- * (nevents must equal the plan's launch count); no synchronisation.  Launch
- * i's duration is the time from the previous event on the stream (the
- * caller's start event, or events[i-1]) to events[i].  For per-kernel timing
+/* fg_fft_exec that also records events[i] right after launch i (nevents must
+ * equal the plan's launch count); no synchronisation.  Launch i's duration is
+ * the time from the previous event on its stream (the caller's start event,
+ * or events[i-1]) to events[i]; on a two-stream plan (fg_fft_plan_streams)
+ * the launches of odd chunks run, and stamp their events, on the plan's
+ * second stream, whose first launch starts when the caller's stream reaches
+ * the call.  For per-kernel timing
  * in benchmarks: the reference's bench brackets its single launch with an
  * event pair (crates/ferrum-gpu-bench/src/lib.rs:163-198); here each event is
  * stamped by its launch's dispatch (no marker packet between back-to-back
@@ -216,6 +219,15 @@ FG_API int fg_fft_get_chunk_bytes(size_t *bytes);
  * are kept cached (1) or every pass streams (0). */
 FG_API int fg_fft_plan_chunking(fg_fft_plan_t plan, int *passes, size_t *units_per_chunk, int *chunks,
                                 int *cached);
+/* Streams an execution runs on: 1, or 2 for multi-pass 1D plans of two or
+ * more chunks, which run the odd chunks (launches passes*c .. passes*c +
+ * passes - 1 of chunk c) on a second stream of their own with a second
+ * workspace, forked from the caller's stream when the execution starts and
+ * joined back to it when it ends (so work enqueued on the caller's stream
+ * afterwards sees the whole output).  On a capturing stream every chunk runs
+ * on the captured stream.  No counterpart in the reference (one stream per
+ * call, crates/ferrum-gpu-py/src/lib.rs:142-233). */
+FG_API int fg_fft_plan_streams(fg_fft_plan_t plan, int *streams);
 /* Kernel name of launch `index` of an execution. */
 FG_API int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char *name, size_t cap);
 /* Number of kernel launches per execution and the name of the kernel that

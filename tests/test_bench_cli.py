@@ -83,3 +83,50 @@ def test_single_pass_workloads():
     for name, log_n, batch in (("1d_8192", 13, 8192), ("1d_16384", 14, 4096), ("1d_32768", 15, 2048)):
         dims, ln, b, *_ = bench.FFT_WORKLOADS[name]
         assert (dims, ln, b) == (1, log_n, batch) and b << ln == 1 << 26   # 512 MiB
+
+
+class _Ev:
+    """A stand-in for hip.Event: a time stamp in ms."""
+
+    def __init__(self, t):
+        self.t = t
+
+    def elapsed_ms(self, end):
+        return end.t - self.t
+
+
+class _Wl:
+    def __init__(self, streams, keys, execs):
+        self.launch_streams, self.launch_keys, self.exec_bounds = streams, keys, execs
+
+
+def test_launch_durations_one_stream_are_event_gaps():
+    import bench
+
+    wl = _Wl([0, 0, 0], ["0:a", "1:b", "2:c"], [(0, 3)])
+    evs = [[_Ev(1), _Ev(2), _Ev(4)], [_Ev(5), _Ev(7), _Ev(8)]]
+    got = bench.launch_durations(_Ev(0), evs, wl)
+    assert got == {"0:a": [1, 1], "1:b": [1, 2], "2:c": [2, 1]}
+
+
+def test_launch_durations_two_streams_use_each_streams_previous_event():
+    # four chunks of one pass, odd chunks on the second stream: each launch
+    # runs from the previous event of its stream, the first ones from the
+    # end of the previous execution (where the plan forks)
+    import bench
+
+    wl = _Wl([0, 1, 0, 1], ["0:k"] * 4, [(0, 4)])
+    evs = [[_Ev(3), _Ev(4), _Ev(6), _Ev(7)], [_Ev(10), _Ev(11), _Ev(13), _Ev(14)]]
+    got = bench.launch_durations(_Ev(0), evs, wl)
+    assert got == {"0:k": [3, 4, 3, 3, 3, 4, 3, 3]}
+
+
+def test_launch_durations_two_executions_per_step():
+    # forward then inverse per step (config 2's shape): the inverse starts
+    # where the forward's last event is
+    import bench
+
+    wl = _Wl([0, 0], ["0:f", "0:i"], [(0, 1), (1, 2)])
+    evs = [[_Ev(2), _Ev(5)], [_Ev(6), _Ev(9)]]
+    got = bench.launch_durations(_Ev(0), evs, wl)
+    assert got == {"0:f": [2, 1], "0:i": [3, 3]}

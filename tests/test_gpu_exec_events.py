@@ -73,14 +73,19 @@ def test_recorded_execution_equals_plain(gpu_device, chunk_limit, two_d, log_n, 
         want = oracle.fft_1d(x, log_n)
     assert rel_l2(rec, want) < 1e-4
 
-    # launch order: every launch took a non-negative time after the previous stamp
-    prev, total = start, 0.0
-    for e in evs:
-        dt = prev.elapsed_ms(e)
-        assert dt >= 0.0
-        total += dt
-        prev = e
-    assert start.elapsed_ms(evs[-1]) == pytest.approx(total, rel=1e-3, abs=1e-3)
+    # launch order: every launch took a non-negative time after the previous
+    # stamp on its stream (two-stream plans: odd chunks on the plan's own)
+    d = plan.describe()
+    streams, passes = d["streams"], d["passes"]
+    for s in range(streams):
+        mine = [e for i, e in enumerate(evs) if streams == 1 or (i // passes) % 2 == s]
+        prev, total = start, 0.0
+        for e in mine:
+            dt = prev.elapsed_ms(e)
+            assert dt >= 0.0
+            total += dt
+            prev = e
+        assert start.elapsed_ms(mine[-1]) == pytest.approx(total, rel=1e-3, abs=1e-3)
     plan.destroy()
 
 

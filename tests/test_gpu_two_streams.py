@@ -1,0 +1,211 @@
+"""Two-stream execution of multi-pass 1D plans (fg_fft_plan_streams == 2).
+
+A multi-pass 1D plan of two or more chunks runs its odd chunks on a second
+stream of its own, with a second workspace, forked from the caller's stream
+when an execution starts and joined back when it ends.  Which stream runs a
+chunk changes nothing in the arithmetic, so the output must be bit-identical
+to the same plan run as one chunk on one stream, and the oracle's (the
+reference's Stockham, cpu.rs:90-124) within 1e-4; work enqueued afterwards
+on the caller's stream must see the whole output; events must be stamped on
+each launch's own stream; and under graph capture the plan runs on the
+captured stream alone.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import normal_c64, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture
+def chunk_limit():
+    import ferrum_gpu
+
+    saved = ferrum_gpu.fft.get_chunk_bytes()
+    yield ferrum_gpu.fft.set_chunk_bytes
+    ferrum_gpu.fft.set_chunk_bytes(saved)
+
+
+def _run(dev, x, log_n, batch, direction="forward", normalize=False):
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer
+
+    plan = ferrum_gpu.fft.Plan1D(log_n, batch, dev)
+    d = plan.describe()
+    a, b = DeviceBuffer(dev, plan.nbytes), DeviceBuffer(dev, plan.nbytes)
+    a.copy_from_host(x)
+    plan.execute(a, b, direction, normalize)
+    dev.sync()
+    out = np.empty_like(x)
+    b.copy_to_host(out)
+    plan.destroy()
+    a.free()
+    b.free()
+    return out, d
+
+
+def _lanes(out, x, log_n, batch, direction="forward", normalize=False):
+    n = 1 << log_n
+    err = 0.0
+    for lane in sorted({0, batch // 2, batch - 1}):
+        got = out[lane * n:(lane + 1) * n]
+        want = oracle.fft_1d(x[lane * n:(lane + 1) * n], log_n, direction, normalize, threads=8)
+        err = max(err, rel_l2(got, want))
+    return err
+
+
+# (log_n, batch, transforms per chunk): an even and an odd number of chunks,
+# a ragged last chunk, and config 4's shape
+CASES = [(16, 7, 2), (17, 4, 1), (20, 3, 1), (22, 5, 2), (24, 2, 1)]
+
+
+@pytest.mark.parametrize("log_n,batch,per_chunk", CASES)
+def test_two_streams_match_one_stream_bits(gpu_device, chunk_limit, log_n, batch, per_chunk):
+    n = 1 << log_n
+    rng = np.random.default_rng(log_n * 31 + batch)
+    x = normal_c64(rng, batch * n)
+    print(f"[case] two streams log_n={log_n} batch={batch} chunk={per_chunk}", flush=True)
+    chunk_limit(per_chunk * n * 8)
+    two, d2 = _run(gpu_device, x, log_n, batch)
+    assert d2["streams"] == 2 and d2["chunks"] == -(-batch // per_chunk)
+    chunk_limit(batch * n * 8)
+    one, d1 = _run(gpu_device, x, log_n, batch)
+    assert d1["streams"] == 1 and d1["chunks"] == 1
+    assert np.array_equal(two.view(np.uint32), one.view(np.uint32))
+    assert _lanes(two, x, log_n, batch) <= TOL
+
+
+def test_two_stream_output_is_ordered_on_the_callers_stream(gpu_device, chunk_limit):
+    # forward then normalised inverse back to back on a user stream, no
+    # synchronisation between them: the inverse must read the whole forward
+    # output, and the copy after it the whole inverse output
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer, Stream
+
+    log_n, batch = 20, 5
+    n = 1 << log_n
+    chunk_limit(n * 8)
+    x = normal_c64(np.random.default_rng(12), batch * n)
+    plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
+    assert plan.describe()["streams"] == 2
+    s = Stream(gpu_device)
+    a, b, c = (DeviceBuffer(gpu_device, plan.nbytes) for _ in range(3))
+    a.copy_from_host(x)
+    for _ in range(3):
+        plan.execute(a, b, "forward", False, stream=s.handle)
+        plan.execute(b, c, "inverse", True, stream=s.handle)
+        plan.execute(c, a, "forward", False, stream=s.handle)
+        plan.execute(a, c, "inverse", True, stream=s.handle)
+        plan.execute(c, a, "forward", False, stream=s.handle)
+        plan.execute(a, a, "inverse", True, stream=s.handle)   # in place
+    s.sync()
+    back = np.empty_like(x)
+    a.copy_to_host(back)
+    assert rel_l2(back, x) <= 1e-5
+    s.destroy()
+    plan.destroy()
+
+
+def test_two_stream_events_on_each_launchs_stream(gpu_device, chunk_limit):
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer, Event
+
+    log_n, batch = 16, 8
+    n = 1 << log_n
+    chunk_limit(2 * n * 8)
+    x = normal_c64(np.random.default_rng(5), batch * n)
+    plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
+    d = plan.describe()
+    assert d["streams"] == 2 and d["chunks"] == 4 and d["launches"] == 8
+    a, b = DeviceBuffer(gpu_device, plan.nbytes), DeviceBuffer(gpu_device, plan.nbytes)
+    a.copy_from_host(x)
+    start = Event(gpu_device)
+    evs = [Event(gpu_device) for _ in range(d["launches"])]
+    start.record()
+    plan.execute_recording(a, b, evs)
+    gpu_device.sync()
+    t = [start.elapsed_ms(e) for e in evs]
+    passes = d["passes"]
+    # within a stream, a chunk's passes and the chunks follow one another
+    for s in (0, 1):
+        mine = [t[i] for i in range(len(t)) if (i // passes) % 2 == s]
+        assert all(v > 0 for v in mine) and mine == sorted(mine), (s, t)
+    out = np.empty_like(x)
+    b.copy_to_host(out)
+    ref, _ = _run(gpu_device, x, log_n, batch)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    plan.destroy()
+
+
+def test_two_stream_plan_in_a_graph_runs_on_the_captured_stream(gpu_device, chunk_limit):
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer
+
+    log_n, batch = 20, 6
+    n = 1 << log_n
+    chunk_limit(2 * n * 8)
+    x = normal_c64(np.random.default_rng(8), batch * n)
+    plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
+    assert plan.describe()["streams"] == 2
+    a, b = DeviceBuffer(gpu_device, plan.nbytes), DeviceBuffer(gpu_device, plan.nbytes)
+    a.copy_from_host(x)
+    plan.execute(a, b)
+    gpu_device.sync()
+    eager = np.empty_like(x)
+    b.copy_to_host(eager)
+    g = plan.capture_graph(a, b, reps=2)
+    for _ in range(3):
+        b.copy_from_host(np.zeros_like(x))
+        g.launch()
+        gpu_device.sync()
+        got = np.empty_like(x)
+        b.copy_to_host(got)
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
+    g.destroy()
+    plan.destroy()
+
+
+def test_two_stream_split_layout(gpu_device, chunk_limit):
+    # the split path interleaves on the caller's stream, runs the two-stream
+    # execution in place and deinterleaves after the join
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer
+
+    log_n, batch = 17, 5
+    n = 1 << log_n
+    chunk_limit(n * 8)
+    x = normal_c64(np.random.default_rng(21), batch * n)
+    plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
+    assert plan.describe()["streams"] == 2
+    bufs = [DeviceBuffer(gpu_device, 4 * batch * n) for _ in range(4)]
+    bufs[0].copy_from_host(np.ascontiguousarray(x.real))
+    bufs[1].copy_from_host(np.ascontiguousarray(x.imag))
+    plan.execute_split(*bufs, "forward", False)
+    gpu_device.sync()
+    re, im = np.empty(batch * n, np.float32), np.empty(batch * n, np.float32)
+    bufs[2].copy_to_host(re)
+    bufs[3].copy_to_host(im)
+    ref, _ = _run(gpu_device, x, log_n, batch)
+    assert np.array_equal(re.view(np.uint32), np.ascontiguousarray(ref.real).view(np.uint32))
+    assert np.array_equal(im.view(np.uint32), np.ascontiguousarray(ref.imag).view(np.uint32))
+    plan.destroy()
+
+
+def test_which_plans_take_two_streams(gpu_device, chunk_limit):
+    import ferrum_gpu
+
+    chunk_limit(128 << 20)
+    assert ferrum_gpu.fft.Plan1D(24, 4, gpu_device).describe()["streams"] == 2   # config 4: four chunks
+    assert ferrum_gpu.fft.Plan1D(24, 1, gpu_device).describe()["streams"] == 1   # one chunk
+    assert ferrum_gpu.fft.Plan1D(10, 65536, gpu_device).describe()["streams"] == 1   # single pass
+    assert ferrum_gpu.fft.Plan2D(12, 4, gpu_device).describe()["streams"] == 1   # 2D keeps one stream
+    # 2^18 = 512 x 512: the last pass stores 8-row tiles, one stream
+    assert ferrum_gpu.fft.Plan1D(18, 256, gpu_device).describe()["streams"] == 1
+    assert ferrum_gpu.fft.Plan1D(20, 64, gpu_device).describe()["streams"] == 2
