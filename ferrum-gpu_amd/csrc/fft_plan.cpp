@@ -429,7 +429,11 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
     {
         const uint32_t log_l = logs[P - 1];
         const uint64_t L = 1ull << log_l, n1 = 1ull << logs[0];
-        const uint32_t g = p->cached_ ? cached_tile_columns(log_l, true) : tile_columns(log_l);
+        uint32_t g = p->cached_ ? cached_tile_columns(log_l, true) : tile_columns(log_l);
+        // With two chunks in flight (below) the 16-row tile wins at 512
+        // points too: 2^18 / 2^19 at 512 MiB 397 / 406 us (8 rows, one
+        // stream) -> 370 / 376 us (16 rows, two streams).
+        if (p->cached_ && p->chunks() > 1 && g < 16) g = 16;
         if (n1 < g) fail(FG_ERR_INTERNAL, "digit split leaves fewer rows than a tile");
         TileGeom t{};
         t.t0n = (uint32_t)(n1 / g);
@@ -445,16 +449,16 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         t.ocs = 1;
         t.oes = N / L;
         p->add_tile(mod, log_l, g, true, t, (uint64_t)t.t0n * t.t1n, Buf::Work, Buf::Out, p->policy(P - 1, P));
-        if (p->chunks() > 1 && g >= 16) {
+        if (p->chunks() > 1) {
             // Two chunks in flight, one per stream: their passes overlap, so
             // one chunk's transform phases fill the other's memory phases.
             // Measured on gfx950 at 512 MiB in chunks of 128 MiB (us per
             // execution, one stream -> two): 2^16 347 -> 328, 2^17 380 -> 348,
-            // 2^20 446 -> 403, 2^21 .. 2^24 510 .. 519 -> 481 .. 485.  Not
-            // when the last pass stores 8-row tiles (512-point rows: 2^18,
-            // 2^19 went 397 / 405 -> 502 / 515), nor for 2D plans (four
-            // 4096 x 4096 images 425 -> 466): narrow pieces of one line meet
-            // in an XCD's L2 only while a single chunk streams through it.
+            // 2^20 446 -> 403, 2^21 .. 2^24 510 .. 519 -> 481 .. 485.  With
+            // the last pass in 8-row tiles 2^18 / 2^19 lost (397 / 405 ->
+            // 502 / 515), and 2D plans lose (four 4096 x 4096 images 425 ->
+            // 466): narrow pieces of one line meet in an XCD's L2 only while
+            // a single chunk streams through it.
             p->work2_ = dev.alloc<Cf32>(N * p->chunk_);
             p->aux_.reset(new ChunkStream(dev.handle()));
         }

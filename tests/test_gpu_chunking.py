@@ -90,7 +90,7 @@ def test_every_chunking_gives_the_same_bits(gpu_device, chunk_limit, two_d, log_
             # first pass streams in, last streams out, middle passes stay
             # cached; narrow tiles always cached (the model's names per pass)
             assert names[0].endswith("_sc")
-            assert names[:d["passes"]] == plan_kernel_names(two_d, log_n, cached=True)
+            assert names[:d["passes"]] == plan_kernel_names(two_d, log_n, cached=True, chunks=d["chunks"])
         assert d["launches"] == d["passes"] * d["chunks"] == len(names)
         outs[limit] = got
     for limit, got in outs.items():

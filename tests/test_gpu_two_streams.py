@@ -63,7 +63,7 @@ def _lanes(out, x, log_n, batch, direction="forward", normalize=False):
 
 # (log_n, batch, transforms per chunk): an even and an odd number of chunks,
 # a ragged last chunk, and config 4's shape
-CASES = [(16, 7, 2), (17, 4, 1), (20, 3, 1), (22, 5, 2), (24, 2, 1)]
+CASES = [(16, 7, 2), (17, 4, 1), (18, 3, 1), (20, 3, 1), (22, 5, 2), (24, 2, 1)]
 
 
 @pytest.mark.parametrize("log_n,batch,per_chunk", CASES)
@@ -206,6 +206,9 @@ def test_which_plans_take_two_streams(gpu_device, chunk_limit):
     assert ferrum_gpu.fft.Plan1D(24, 1, gpu_device).describe()["streams"] == 1   # one chunk
     assert ferrum_gpu.fft.Plan1D(10, 65536, gpu_device).describe()["streams"] == 1   # single pass
     assert ferrum_gpu.fft.Plan2D(12, 4, gpu_device).describe()["streams"] == 1   # 2D keeps one stream
-    # 2^18 = 512 x 512: the last pass stores 8-row tiles, one stream
-    assert ferrum_gpu.fft.Plan1D(18, 256, gpu_device).describe()["streams"] == 1
-    assert ferrum_gpu.fft.Plan1D(20, 64, gpu_device).describe()["streams"] == 2
+    # 2^18 = 512 x 512: one chunk keeps the 8-row last pass on one stream,
+    # two or more take 16-row tiles and two streams
+    one = ferrum_gpu.fft.Plan1D(18, 1, gpu_device)
+    assert one.describe()["streams"] == 1 and one.kernel_names()[-1] == "fg_tile_l9_g8_r_cc"
+    many = ferrum_gpu.fft.Plan1D(18, 256, gpu_device)
+    assert many.describe()["streams"] == 2 and many.kernel_names()[-1] == "fg_tile_l9_g16_r_cs"

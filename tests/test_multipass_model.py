@@ -52,9 +52,11 @@ def split_1d(log_n):
     return [base + (1 if rest > 0 else 0), base + (1 if rest > 1 else 0), base]
 
 
-def tile_geometry_1d(log_n, batch, cached=True):
+def tile_geometry_1d(log_n, batch, cached=True, chunks=1):
     """Per-pass geometry dicts (TileGeom), built as FftPlan::make_1d builds them;
-    ``cached``: the plan is chunked, so passes after the first read the caches."""
+    ``cached``: the plan is chunked, so passes after the first read the caches;
+    ``chunks``: how many chunks the batch takes (two or more: the last pass
+    takes at least 16 rows, for the plan's two chunks in flight)."""
     logs = split_1d(log_n)
     P = len(logs)
     N = 1 << log_n
@@ -79,6 +81,8 @@ def tile_geometry_1d(log_n, batch, cached=True):
     L = sizes[-1]
     n1 = sizes[0]
     gp = cached_tile_columns(logs[-1], True) if cached else tile_columns(logs[-1])
+    if cached and chunks > 1:
+        gp = max(gp, 16)
     assert n1 >= gp
     inner = N // (n1 * L)             # values of k_2..k_{P-1}
     # the row for (k_1, kmid) starts at k_1*S_1 + sum k_j S_j = k_1*S_1 + kmid*L
@@ -127,7 +131,7 @@ def use_halves_tile(log_l, g, rowwise, reads_input):
     return log_l == 10 and g == 8
 
 
-def plan_kernel_names(two_d, log_n, cached=True, log_cols=None):
+def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, chunks=1):
     """The kernel of every pass of a plan of 1D length 2^log_n (one pass up to
     16384 points, several beyond) or of 2D images with 2^log_n rows and
     2^log_cols columns, in launch order."""
@@ -141,7 +145,7 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None):
             # single pass: the Stockham kernel (fg_fft_n13 / n14 / n15: 32
             # elements per thread, exchanges in halves; test_tile_halves_model)
             return [f"fg_fft_n{log_n}"]
-        passes = tile_geometry_1d(log_n, 1, cached)
+        passes = tile_geometry_1d(log_n, 1, cached, chunks)
         return [tile(p, pass_policy(i, len(passes), cached, p["g"]), reads_input=(i == 0))
                 for i, p in enumerate(passes)]
     lc = log_n if log_cols is None else log_cols

@@ -107,6 +107,7 @@ def planned_kernels():
     for cached in (False, True):
         for log_n in range(13, 25):
             names |= set(plan_kernel_names(False, log_n, cached))
+            names |= set(plan_kernel_names(False, log_n, cached, chunks=2))
         for lr in range(4, 13):
             for lc in range(4, 13):
                 names |= set(plan_kernel_names(True, lr, cached, lc))
