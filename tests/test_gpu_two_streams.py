@@ -212,3 +212,18 @@ def test_which_plans_take_two_streams(gpu_device, chunk_limit):
     assert one.describe()["streams"] == 1 and one.kernel_names()[-1] == "fg_tile_l9_g8_r_cc"
     many = ferrum_gpu.fft.Plan1D(18, 256, gpu_device)
     assert many.describe()["streams"] == 2 and many.kernel_names()[-1] == "fg_tile_l9_g16_r_cs"
+
+
+def test_two_stream_plan_behind_the_host_array_path(gpu_device, chunk_limit):
+    # fft_1d_c2c_pow2 on host arrays: staging copies on the device stream
+    # around a plan whose chunks alternate over two streams
+    import ferrum_gpu
+
+    log_n, batch = 16, 9
+    n = 1 << log_n
+    chunk_limit(n * 8)
+    x = normal_c64(np.random.default_rng(99), batch * n)
+    for direction, normalize in (("forward", False), ("inverse", True)):
+        got = ferrum_gpu.fft.fft_1d_c2c_pow2(x, log_n, direction, normalize, device=gpu_device)
+        want = oracle.fft_1d(x, log_n, direction, normalize, threads=8)
+        assert rel_l2(got, want) <= TOL
