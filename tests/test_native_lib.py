@@ -291,6 +291,9 @@ def test_c_abi_validation_without_device():
     assert rc == N.FG_ERR_INVALID_ARGUMENT and "plan is null" in N.last_error()
     rc = N.lib.fg_fft_plan_1d(None, 10, 1, ctypes.byref(ctypes.c_void_p()))
     assert rc == N.FG_ERR_INVALID_ARGUMENT
+    streams = ctypes.c_int(-1)
+    rc = N.lib.fg_fft_plan_streams(None, ctypes.byref(streams))
+    assert rc == N.FG_ERR_INVALID_ARGUMENT and "plan is null" in N.last_error() and streams.value == -1
 
 
 def test_split_and_pointwise_validation_without_device():
