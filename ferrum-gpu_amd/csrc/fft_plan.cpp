@@ -508,8 +508,19 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     p->add_stockham(mod, log_cols, R, Buf::In, split ? Buf::Work : Buf::Out, p->policy(0, npass));
     if (!split) {
         // Column pass, in place: G adjacent columns of length R per tile.
+        // Plans of 32 .. 512 rows of at least 128 columns in two or more
+        // chunks run two chunks at a time (the odd ones on the plan's own
+        // stream, as the 1D plans) with the wide tiles of the HBM passes:
+        // measured on gfx950 at 512 MiB, us per execution against one stream
+        // with the 8-column tiles, 32 x 1024 .. 512 x 4096: 1.4 .. 10 %
+        // faster (256 x 256 337 -> 328, 128 x 2048 366 -> 330, 512 x 4096
+        // 373 -> 353); 16-row images lost 5 % and 512 x 64 7 %, and the
+        // narrow column tiles of 1024 .. 4096 rows lose with two streams
+        // (4096 x 4096 x 4: 425 -> 466).
+        const bool two = p->cached_ && p->chunks() > 1 && log_rows >= 5 && log_rows <= 9 && log_cols >= 7;
         const uint32_t g = (uint32_t)std::min<uint64_t>(
-            p->cached_ ? cached_tile_columns(log_rows, false) : tile_columns(log_rows), C);
+            (p->cached_ && !two) ? cached_tile_columns(log_rows, false) : tile_columns(log_rows), C);
+        if (two) p->aux_.reset(new ChunkStream(dev.handle()));
         TileGeom t{};
         t.t0n = (uint32_t)(C / g);
         t.t1n = 1;

@@ -55,14 +55,15 @@ public:
     // Multi-launch plans run chunk by chunk: every pass over chunk_units()
     // transforms (images) before the next chunk, so a chunk's intermediate
     // array stays in the Infinity Cache (chunk_bytes()).  Plans with
-    // streams() == 2 run the odd chunks on a second stream of their own, with
-    // a second workspace, forked from `stream` at the start and joined back
-    // at the end (on a capturing stream: every chunk on `stream`).
+    // streams() == 2 run the odd chunks on a second stream of their own (1D:
+    // with a second workspace), forked from `stream` at the start and joined
+    // back at the end (on a capturing stream: every chunk on `stream`).
     // With `events` (launches() of them), events[i] is recorded right after
     // launch i on the stream launch i runs on (chunk_stream()).
     void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
               hipEvent_t* events = nullptr) const;
-    // 1, or 2 for multi-pass 1D plans of two or more chunks.
+    // 1, or 2 for multi-pass plans of two or more chunks: 1D, and 2D of
+    // 32 .. 512 rows of at least 128 columns.
     int streams() const { return aux_ ? 2 : 1; }
     // The stream a chunk's launches run on: 0 the caller's, 1 the plan's own.
     int chunk_stream(size_t chunk) const { return aux_ ? (int)(chunk & 1) : 0; }
@@ -174,7 +175,7 @@ private:
     std::vector<std::pair<uint32_t, Buffer<Cf32, HipBackend>>> stage_tables_;
     Buffer<Cf32, HipBackend> big_;
     Buffer<Cf32, HipBackend> work_;
-    Buffer<Cf32, HipBackend> work2_;         // the odd chunks' workspace (two-stream plans)
+    Buffer<Cf32, HipBackend> work2_;         // the odd chunks' workspace (two-stream 1D plans)
     std::unique_ptr<ChunkStream> aux_;       // two-stream plans: the odd chunks' stream
     std::string main_kernel_;
     HipBackend::KernelHandle split_fn_ = nullptr;  // single-pass plans: the split-layout twin

@@ -205,7 +205,12 @@ def test_which_plans_take_two_streams(gpu_device, chunk_limit):
     assert ferrum_gpu.fft.Plan1D(24, 4, gpu_device).describe()["streams"] == 2   # config 4: four chunks
     assert ferrum_gpu.fft.Plan1D(24, 1, gpu_device).describe()["streams"] == 1   # one chunk
     assert ferrum_gpu.fft.Plan1D(10, 65536, gpu_device).describe()["streams"] == 1   # single pass
-    assert ferrum_gpu.fft.Plan2D(12, 4, gpu_device).describe()["streams"] == 1   # 2D keeps one stream
+    assert ferrum_gpu.fft.Plan2D(12, 4, gpu_device).describe()["streams"] == 1   # narrow column tiles
+    # 32 .. 512 rows of at least 128 columns: two streams, wide column tiles
+    p2 = ferrum_gpu.fft.Plan2D(8, 1024, gpu_device)
+    assert p2.describe()["streams"] == 2 and p2.kernel_names()[1] == "fg_tile_l8_g32_c_cs"
+    assert ferrum_gpu.fft.Plan2D(9, 2048, gpu_device, log_cols=6).describe()["streams"] == 1
+    assert ferrum_gpu.fft.Plan2D(4, 2048, gpu_device, log_cols=11).describe()["streams"] == 1
     # 2^18 = 512 x 512: one chunk keeps the 8-row last pass on one stream,
     # two or more take 16-row tiles and two streams
     one = ferrum_gpu.fft.Plan1D(18, 1, gpu_device)
@@ -227,3 +232,38 @@ def test_two_stream_plan_behind_the_host_array_path(gpu_device, chunk_limit):
         got = ferrum_gpu.fft.fft_1d_c2c_pow2(x, log_n, direction, normalize, device=gpu_device)
         want = oracle.fft_1d(x, log_n, direction, normalize, threads=8)
         assert rel_l2(got, want) <= TOL
+
+
+# 2D (log rows, log cols, batch, images per chunk): two-stream plans take the
+# wide column tiles; one chunk takes the 8-column ones -- the same bits
+CASES_2D = [(8, 8, 7, 2), (5, 10, 5, 2), (9, 7, 3, 1), (7, 12, 2, 1)]
+
+
+@pytest.mark.parametrize("lr,lc,batch,per_chunk", CASES_2D)
+def test_two_stream_2d_plans_match_one_stream_bits(gpu_device, chunk_limit, lr, lc, batch, per_chunk):
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer
+    from test_gpu_extras import oracle_2d_rect
+
+    image = 8 << (lr + lc)
+    x = normal_c64(np.random.default_rng(lr * 16 + lc), batch * (image // 8)).reshape(batch, 1 << lr, 1 << lc)
+    outs = []
+    for limit, streams in ((per_chunk * image, 2), (batch * image, 1)):
+        chunk_limit(limit)
+        print(f"[case] 2d {1 << lr}x{1 << lc} batch={batch} chunk limit={limit}", flush=True)
+        plan = ferrum_gpu.fft.Plan2D(lr, batch, gpu_device, log_cols=lc)
+        assert plan.describe()["streams"] == streams
+        a, b = DeviceBuffer(gpu_device, plan.nbytes), DeviceBuffer(gpu_device, plan.nbytes)
+        a.copy_from_host(x)
+        plan.execute(a, b, "forward")
+        plan.execute(b, a, "inverse", True)
+        gpu_device.sync()
+        fwd, back = np.empty_like(x), np.empty_like(x)
+        b.copy_to_host(fwd)
+        a.copy_to_host(back)
+        outs.append((fwd, back))
+        plan.destroy()
+    assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32))
+    assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
+    assert rel_l2(outs[0][0], oracle_2d_rect(x, lr, lc)) <= TOL
+    assert rel_l2(outs[0][1], x) <= TOL

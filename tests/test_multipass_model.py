@@ -94,14 +94,22 @@ def tile_geometry_1d(log_n, batch, cached=True, chunks=1):
     return passes
 
 
-def tile_geometry_2d(log_n, batch, log_cols=None, cached=True):
+def two_stream_2d(log_rows, log_cols, cached, chunks):
+    """FftPlan::make_2d: plans of 32 .. 512 rows of at least 128 columns in two
+    or more chunks run two chunks at a time, with the wide column tiles."""
+    return cached and chunks > 1 and 5 <= log_rows <= 9 and log_cols >= 7
+
+
+def tile_geometry_2d(log_n, batch, log_cols=None, cached=True, chunks=1):
     """Column FFT of each R x C image after the row pass, as FftPlan::make_2d builds it
     (R = 2^log_n rows, C = 2^log_cols columns, square by default): one tile pass over
     min(width, C) adjacent columns of length R, in place; the width is the
-    cache-resident one when the plan is chunked."""
+    cache-resident one when the plan is chunked (the HBM one for two-stream plans)."""
     R = 1 << log_n
     C = R if log_cols is None else 1 << log_cols
-    g = min(cached_tile_columns(log_n, False) if cached else tile_columns(log_n), C)
+    lc = log_n if log_cols is None else log_cols
+    wide = two_stream_2d(log_n, lc, cached, chunks)
+    g = min(cached_tile_columns(log_n, False) if (cached and not wide) else tile_columns(log_n), C)
     return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
                  is0=g, is1=0, is2=R * C, ics=1, ies=C,
                  os0=g, os1=0, os2=R * C, ocs=1, oes=C,
@@ -134,7 +142,8 @@ def use_halves_tile(log_l, g, rowwise, reads_input):
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, chunks=1):
     """The kernel of every pass of a plan of 1D length 2^log_n (one pass up to
     16384 points, several beyond) or of 2D images with 2^log_n rows and
-    2^log_cols columns, in launch order."""
+    2^log_cols columns, in launch order; ``chunks``: how many chunks the batch
+    takes (two or more: the two-stream widths)."""
     def tile(p, pol, reads_input=False):
         kind = "h" if use_halves_tile(p["log_l"], p["g"], p["rowwise"], reads_input) else \
             ("r" if p["rowwise"] else "c")
@@ -152,7 +161,7 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, chunks=1):
     if log_n + lc <= 14:
         # images of up to 16384 points: one pass (fg_fft2d_*, test_fft2d_small_model)
         return [f"fg_fft2d_l{log_n}_{lc}"]
-    passes = tile_geometry_2d(log_n, 1, lc, cached)
+    passes = tile_geometry_2d(log_n, 1, lc, cached, chunks)
     n = len(passes) + 1
     return [f"fg_fft_n{lc}" + ("_sc" if cached else "")] + \
         [tile(p, pass_policy(i + 1, n, cached, p["g"])) for i, p in enumerate(passes)]
