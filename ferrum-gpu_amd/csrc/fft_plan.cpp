@@ -197,11 +197,14 @@ bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise, bool reads_input)
     // 4096 points always exchange in halves (twice the columns per tile in
     // the same LDS; add_tile gives the timings); 1024 points too, 46.6 ..
     // 52.5 -> 44.7 .. 48.5 us per 128 MiB pass at 64 .. 4096 columns; 512
-    // points lose (41.5 .. 46.7 -> 45.8 .. 47.3).
+    // points lose (41.5 .. 46.7 -> 45.8 .. 47.3).  The 16-column passes of
+    // 1024 points (two-stream and unchunked 2D plans) take the halves tile
+    // too: with two streams 2 .. 7 % faster per plan than with the 16-element
+    // tile.
     if (rowwise) return false;
     if (log_l > 10) return true;
     if (reads_input) return log_l >= 7 && g == tile_columns(log_l);
-    return log_l == 10 && g == 8;
+    return log_l == 10 && (g == 8 || g == 16);
 }
 
 bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }
@@ -508,16 +511,17 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     p->add_stockham(mod, log_cols, R, Buf::In, split ? Buf::Work : Buf::Out, p->policy(0, npass));
     if (!split) {
         // Column pass, in place: G adjacent columns of length R per tile.
-        // Plans of 32 .. 512 rows of at least 128 columns in two or more
+        // Plans of 32 .. 1024 rows of at least 128 columns in two or more
         // chunks run two chunks at a time (the odd ones on the plan's own
         // stream, as the 1D plans) with the wide tiles of the HBM passes:
         // measured on gfx950 at 512 MiB, us per execution against one stream
         // with the 8-column tiles, 32 x 1024 .. 512 x 4096: 1.4 .. 10 %
         // faster (256 x 256 337 -> 328, 128 x 2048 366 -> 330, 512 x 4096
-        // 373 -> 353); 16-row images lost 5 % and 512 x 64 7 %, and the
-        // narrow column tiles of 1024 .. 4096 rows lose with two streams
+        // 373 -> 353); 1024 rows (16 columns in halves) 1.5 .. 3 % (1024 x
+        // 4096 384 -> 372).  16-row images lost 5 % and 512 x 64 7 %, and
+        // the narrow column tiles of 2048 / 4096 rows lose with two streams
         // (4096 x 4096 x 4: 425 -> 466).
-        const bool two = p->cached_ && p->chunks() > 1 && log_rows >= 5 && log_rows <= 9 && log_cols >= 7;
+        const bool two = p->cached_ && p->chunks() > 1 && log_rows >= 5 && log_rows <= 10 && log_cols >= 7;
         const uint32_t g = (uint32_t)std::min<uint64_t>(
             (p->cached_ && !two) ? cached_tile_columns(log_rows, false) : tile_columns(log_rows), C);
         if (two) p->aux_.reset(new ChunkStream(dev.handle()));

@@ -63,7 +63,7 @@ public:
     void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
               hipEvent_t* events = nullptr) const;
     // 1, or 2 for multi-pass plans of two or more chunks: 1D, and 2D of
-    // 32 .. 512 rows of at least 128 columns.
+    // 32 .. 1024 rows of at least 128 columns.
     int streams() const { return aux_ ? 2 : 1; }
     // The stream a chunk's launches run on: 0 the caller's, 1 the plan's own.
     int chunk_stream(size_t chunk) const { return aux_ ? (int)(chunk & 1) : 0; }

@@ -220,7 +220,7 @@ FG_API int fg_fft_get_chunk_bytes(size_t *bytes);
 FG_API int fg_fft_plan_chunking(fg_fft_plan_t plan, int *passes, size_t *units_per_chunk, int *chunks,
                                 int *cached);
 /* Streams an execution runs on: 1, or 2 for multi-pass plans of two or more
- * chunks (1D; 2D of 2^5 .. 2^9 rows of at least 2^7 columns), which run the
+ * chunks (1D; 2D of 2^5 .. 2^10 rows of at least 2^7 columns), which run the
  * odd chunks (launches passes*c .. passes*c + passes - 1 of chunk c) on a
  * second stream of their own (1D: with a second workspace), forked from the
  * caller's stream when the execution starts and

@@ -17,6 +17,7 @@ import pytest
 
 from conftest import rel_l2, uniform_c64
 from test_gpu_extras import oracle_2d_rect
+from test_multipass_model import two_stream_2d
 
 pytestmark = pytest.mark.gpu
 
@@ -56,7 +57,7 @@ def _exec(dev, x, lr, lc, direction, normalize):
 # (smaller ones take the one-pass kernels); tiles per image = C / 8
 CASES = [
     (10, 5, 11, 4),     # chunks of 16 tiles (line groups), the last of 12 (natural)
-    (10, 9, 5, 2),      # 64 tiles per image: every chunk in line groups
+    (10, 9, 5, 2),      # 512 columns in three chunks: 16-column tiles, two streams
     (11, 4, 9, 3),      # 6 tiles per chunk: natural order throughout
     (11, 7, 5, 2),
     (11, 12, 2, 1),
@@ -74,7 +75,11 @@ def test_halves_column_pass_chunked(gpu_device, chunk_limit, lr, lc, batch, per_
     chunk_limit(per_chunk * image)
     print(f"[case] 2d {1 << lr}x{1 << lc} batch={batch} chunk={per_chunk} images", flush=True)
     fwd, d, names = _exec(gpu_device, x, lr, lc, "forward", False)
-    assert names[-1] == f"fg_tile_l{lr}_g8_h_cc", names
+    # 1024 rows of at least 128 columns in several chunks: two chunks in
+    # flight with 16-column halves tiles (two_stream_2d), else 8 columns
+    wide = two_stream_2d(lr, lc, True, d["chunks"])
+    assert names[-1] == (f"fg_tile_l{lr}_g16_h_cs" if wide else f"fg_tile_l{lr}_g8_h_cc"), names
+    assert d["streams"] == (2 if wide else 1)
     assert d["units_per_chunk"] == per_chunk and d["chunks"] == -(-batch // per_chunk)
     assert rel_l2(fwd, oracle_2d_rect(x, lr, lc)) <= TOL
     inv, _, _ = _exec(gpu_device, fwd, lr, lc, "inverse", True)

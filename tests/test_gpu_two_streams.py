@@ -236,7 +236,7 @@ def test_two_stream_plan_behind_the_host_array_path(gpu_device, chunk_limit):
 
 # 2D (log rows, log cols, batch, images per chunk): two-stream plans take the
 # wide column tiles; one chunk takes the 8-column ones -- the same bits
-CASES_2D = [(8, 8, 7, 2), (5, 10, 5, 2), (9, 7, 3, 1), (7, 12, 2, 1)]
+CASES_2D = [(8, 8, 7, 2), (5, 10, 5, 2), (9, 7, 3, 1), (7, 12, 2, 1), (10, 8, 5, 2), (10, 12, 3, 1)]
 
 
 @pytest.mark.parametrize("lr,lc,batch,per_chunk", CASES_2D)

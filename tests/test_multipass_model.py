@@ -95,9 +95,9 @@ def tile_geometry_1d(log_n, batch, cached=True, chunks=1):
 
 
 def two_stream_2d(log_rows, log_cols, cached, chunks):
-    """FftPlan::make_2d: plans of 32 .. 512 rows of at least 128 columns in two
+    """FftPlan::make_2d: plans of 32 .. 1024 rows of at least 128 columns in two
     or more chunks run two chunks at a time, with the wide column tiles."""
-    return cached and chunks > 1 and 5 <= log_rows <= 9 and log_cols >= 7
+    return cached and chunks > 1 and 5 <= log_rows <= 10 and log_cols >= 7
 
 
 def tile_geometry_2d(log_n, batch, log_cols=None, cached=True, chunks=1):
@@ -136,7 +136,7 @@ def use_halves_tile(log_l, g, rowwise, reads_input):
         return True
     if reads_input:
         return 7 <= log_l and g == tile_columns(log_l)
-    return log_l == 10 and g == 8
+    return log_l == 10 and g in (8, 16)
 
 
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, chunks=1):

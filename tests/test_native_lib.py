@@ -91,6 +91,9 @@ def instantiated_kernels():
     # first-pass tiles with the exchanges in halves: unchunked and _sc
     for m in re.finditer(r"^FG_TILE_HALVES\((\d+), (\d+)\)", src, flags=re.M):
         names |= {f"fg_tile_l{m.group(1)}_g{m.group(2)}_h{pol}" for pol in ("", "_sc")}
+    # the 1024-point column pass in 16-column halves tiles, streamed out
+    for m in re.finditer(r"^FG_TILE_HALVES_P\((\d+), (\d+), _cs, true, false\)", src, flags=re.M):
+        names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_h_cs")
     # narrow tiles in halves (2D columns of 2048 / 4096 points): _cc alone
     for m in re.finditer(r"^FG_TILE_HALVES_NARROW\((\d+), (\d+)\)", src, flags=re.M):
         names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_h_cc")
