@@ -569,6 +569,40 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         b.oes = R1 * C;
         p->add_tile(mod, l2, g, false, b, (uint64_t)b.t0n * b.t1n, Buf::Work, Buf::Out, p->policy(2, npass));
     }
+    if (log_rows == 12 && log_cols >= 11) {
+        // 4096 rows of 2048 / 4096 points, out of place: the column DFT split
+        // radix-2 over the row index.  The row pass transforms rows r and
+        // r + 2048 of an image in one workgroup and stores A + B and
+        // (A - B) W_4096^r to output rows 2r and 2r + 1
+        // (kernels/fft_2d_rowpair.hpp); the column pass takes 2048-point DFTs
+        // over the rows of each parity in place, 8 columns per tile in halves
+        // (68 KB: two workgroups per CU where a 4096-row tile takes the CU's
+        // LDS).  In-place executions keep the two passes above.
+        p->steps_in_place_ = std::move(p->steps_);
+        p->steps_.clear();
+        Step s;
+        s.rowpair = true;
+        s.log_rows = log_rows;
+        s.name = "fg_fft2d_rowpair_n" + std::to_string(log_cols);
+        s.fn = HipBackend::get_kernel(mod, s.name.c_str());
+        s.block = Dim3(1u << (log_cols - 3));
+        s.src = Buf::In;
+        s.dst = Buf::Out;
+        s.tw = p->stage_table(log_cols, 4);
+        s.per_unit = R / 2;
+        p->big_table();
+        p->steps_.push_back(s);
+        TileGeom t{};
+        t.t0n = (uint32_t)(C / 8);
+        t.t1n = 2;  // row parity
+        t.is0 = t.os0 = 8;
+        t.is1 = t.os1 = C;
+        t.is2 = t.os2 = RC;
+        t.ics = t.ocs = 1;
+        t.ies = t.oes = 2 * C;
+        p->add_tile(mod, log_rows - 1, 8, false, t, (uint64_t)t.t0n * t.t1n, Buf::Out, Buf::Out,
+                    p->policy(1, npass));
+    }
     p->main_kernel_ = p->steps_.back().name;
     p->pw_ = Pointwise(mod);
     return p;
@@ -605,6 +639,7 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
     const void* big = big_.data();
     const uint64_t unit = elems();
     const hipStream_t main = stream ? stream : HipBackend::default_stream(dev_->handle());
+    const std::vector<Step>& steps = (in == out && !steps_in_place_.empty()) ? steps_in_place_ : steps_;
     bool two = aux_ != nullptr;
     if (two) {
         // Under stream capture the plan stays on the captured stream.
@@ -631,15 +666,24 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
                 default: return odd ? work2_.data() : work_.data();
             }
         };
-        for (size_t i = 0; i < steps_.size(); ++i) {
-            const Step& s = steps_[i];
+        for (size_t i = 0; i < steps.size(); ++i) {
+            const Step& s = steps[i];
             uint32_t flags = 0;
             if (inverse && i == 0) flags |= FG_PASS_CONJ_IN;
-            if (inverse && i + 1 == steps_.size()) flags |= FG_PASS_CONJ_SCALE_OUT;
+            if (inverse && i + 1 == steps.size()) flags |= FG_PASS_CONJ_SCALE_OUT;
             void* src = bind(s.src);
             void* dst = bind(s.dst);
             const void* tw = s.tw;
-            if (s.small2d) {
+            if (s.rowpair) {
+                uint64_t pairs = s.per_unit * units;
+                uint32_t lr = s.log_rows;
+                void* args[] = {&src, &dst, (void*)&tw, (void*)&big, &pairs, &lr, &flags};
+                const Dim3 grid((uint32_t)pairs);
+                if (events)
+                    HipBackend::launch_stamped(dev_->handle(), cs, s.fn, grid, s.block, 0, args, events[launch]);
+                else
+                    HipBackend::launch(dev_->handle(), cs, s.fn, grid, s.block, 0, args);
+            } else if (s.small2d) {
                 uint64_t count = s.per_unit * units;
                 float sc = scale;
                 const void* twc = s.tw_cols;

@@ -102,7 +102,7 @@ public:
     bool cache_resident() const { return cached_; }
     const std::string& main_kernel() const { return main_kernel_; }
     size_t workspace_bytes() const { return work_.bytes() + work2_.bytes(); }
-    // Kernel names in launch order.
+    // Kernel names in launch order (out of place; steps_in_place_ has as many passes).
     std::vector<std::string> kernel_names() const;
 
 private:
@@ -112,6 +112,8 @@ private:
     struct Step {
         bool tile = false;                      // tile pass (else single-pass Stockham)
         bool small2d = false;                   // one-pass 2D of small images (fg_fft2d_*)
+        bool rowpair = false;                   // 2D row pass over row pairs (fg_fft2d_rowpair_*)
+        uint32_t log_rows = 0;                  // rowpair: log2 of the image's rows
         const void* tw_cols = nullptr;          // small2d: the column stage table
         std::string name;
         HipBackend::KernelHandle fn = nullptr;
@@ -172,6 +174,7 @@ private:
     size_t chunk_;         // units per chunk (batch_ when not chunked)
     bool cached_ = false;  // intermediates kept cached (else every pass streams)
     std::vector<Step> steps_;
+    std::vector<Step> steps_in_place_;  // when not empty: the passes of in-place executions (in == out)
     std::vector<std::pair<uint32_t, Buffer<Cf32, HipBackend>>> stage_tables_;
     Buffer<Cf32, HipBackend> big_;
     Buffer<Cf32, HipBackend> work_;

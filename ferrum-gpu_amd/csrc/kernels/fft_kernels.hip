@@ -311,6 +311,19 @@ FG_FFT2D_HALVES(9, 4)
 FG_FFT2D_HALVES(9, 5)
 FG_FFT2D_HALVES(10, 4)
 
+// Row pass of 2D plans of 4096 rows of 2048 / 4096 points: rows r and
+// r + 2048 per workgroup of 2T threads, combined radix-2 over the row index
+// (fft_2d_rowpair.hpp), so the column pass runs 2048-row tiles.
+#include "fft_2d_rowpair.hpp"
+#define FG_FFT2D_ROWPAIR(LOGN)                                                                        \
+    extern "C" __global__ __launch_bounds__(1 << ((LOGN) - 3)) void fg_fft2d_rowpair_n##LOGN(       \
+        const float2* __restrict__ in, float2* __restrict__ out, const float2* __restrict__ tw,      \
+        const float2* __restrict__ big, uint64_t pairs, uint32_t log_rows, uint32_t flags) {         \
+        fft2d_rowpair_body<LOGN>(in, out, tw, big, pairs, log_rows, flags);                          \
+    }
+FG_FFT2D_ROWPAIR(11)
+FG_FFT2D_ROWPAIR(12)
+
 // ------------------------------------------------------- multi-pass tiles
 //
 // fg_tile_l<LOGL>_g<G>_<c|r|h>[_<policy>]: one pass over G columns of length

@@ -229,7 +229,9 @@ FG_API int fg_fft_plan_chunking(fg_fft_plan_t plan, int *passes, size_t *units_p
  * on the captured stream.  No counterpart in the reference (one stream per
  * call, crates/ferrum-gpu-py/src/lib.rs:142-233). */
 FG_API int fg_fft_plan_streams(fg_fft_plan_t plan, int *streams);
-/* Kernel name of launch `index` of an execution. */
+/* Kernel name of launch `index` of an execution out of place (d_in != d_out).
+ * 2D plans of 4096 rows of 2048 or 4096 columns run other kernels in place
+ * (fg_fft_n<log_cols> rows, then 4096-row column tiles), as many launches. */
 FG_API int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char *name, size_t cap);
 /* Number of kernel launches per execution and the name of the kernel that
  * moves the most bytes (what the bench times and profiles). */

@@ -18,6 +18,7 @@ import pytest
 
 import oracle
 from conftest import rel_l2, uniform_c64
+from test_multipass_model import rowpair_2d
 
 pytestmark = pytest.mark.gpu
 
@@ -99,7 +100,12 @@ def test_split_2d_equals_interleaved(gpu_device, lr, lc):
     x = uniform_c64(np.random.default_rng(lr + lc), batch << (lr + lc))
     plan = ferrum_gpu.fft.Plan2D(lr, batch, gpu_device, log_cols=lc)
     inter, split = _run_both(gpu_device, plan, x)
-    assert np.array_equal(inter, split)
+    if rowpair_2d(lr, lc):
+        # the split layout stages and runs in place: the row and column passes,
+        # where out of place the plan pairs rows (another rounding)
+        assert rel_l2(split, inter) <= TOL
+    else:
+        assert np.array_equal(inter, split)
     exp = np.fft.fft2(x.reshape(batch, 1 << lr, 1 << lc).astype(np.complex128)).reshape(-1)
     assert rel_l2(split, exp) <= TOL
 

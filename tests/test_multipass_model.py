@@ -94,6 +94,31 @@ def tile_geometry_1d(log_n, batch, cached=True, chunks=1):
     return passes
 
 
+def rowpair_2d(log_rows, log_cols):
+    """FftPlan::make_2d: images of 4096 rows of 2048 / 4096 points split their
+    column DFT radix-2 over the row index (kernels/fft_2d_rowpair.hpp) when
+    run out of place; in place they keep the row pass + 4096-row columns."""
+    return log_rows == 12 and log_cols >= 11
+
+
+def rowpair_model(x):
+    """numpy model of the split: x (B, R, C) -> the 2D DFT.  Row DFTs; rows r
+    and r + R/2 combined as A + B to row 2r and (A - B) W_R^r to row 2r + 1;
+    then, in place, R/2-point DFTs down the rows of each parity h (a strided
+    tile geometry: is1 = os1 = C, ies = oes = 2 C), X[2k + h] at row 2k + h."""
+    b, R, C = x.shape
+    half = R // 2
+    rows = np.fft.fft(x.astype(np.complex128), axis=2)
+    a, bb = rows[:, :half, :], rows[:, half:, :]
+    w = np.exp(-2j * np.pi * np.arange(half) / R)[None, :, None]
+    out = np.empty_like(rows)
+    out[:, 0::2, :] = a + bb              # the row pass's output, rows as stored
+    out[:, 1::2, :] = (a - bb) * w
+    for h in range(2):
+        out[:, h::2, :] = np.fft.fft(out[:, h::2, :], axis=1)
+    return out
+
+
 def two_stream_2d(log_rows, log_cols, cached, chunks):
     """FftPlan::make_2d: plans of 32 .. 1024 rows of at least 128 columns in two
     or more chunks run two chunks at a time, with the wide column tiles."""
@@ -161,6 +186,9 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, chunks=1):
     if log_n + lc <= 14:
         # images of up to 16384 points: one pass (fg_fft2d_*, test_fft2d_small_model)
         return [f"fg_fft2d_l{log_n}_{lc}"]
+    if rowpair_2d(log_n, lc):
+        # 4096 rows of 2048 / 4096 points: row pairs, then 2048-row halves
+        return [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l11_g8_h_cc"]
     passes = tile_geometry_2d(log_n, 1, lc, cached, chunks)
     n = len(passes) + 1
     return [f"fg_fft_n{lc}" + ("_sc" if cached else "")] + \
@@ -351,3 +379,30 @@ def test_split_sizes_fit_the_tile_kernel():
         logs = split_1d(log_n)
         assert sum(logs) == log_n
         assert all(4 <= l <= 10 for l in logs), (log_n, logs)   # wide tiles only
+
+
+@pytest.mark.parametrize("R,C", [(4096, 16), (64, 32), (16, 8)])
+def test_rowpair_split_matches_fft2(R, C):
+    # the radix-2 split of the column DFT reproduces the 2D DFT (any R; the
+    # plan uses it at 4096 rows)
+    rng = np.random.default_rng(R + C)
+    x = uniform_c64(rng, 2 * R * C).reshape(2, R, C)
+    assert rel_l2(rowpair_model(x), np.fft.fft2(x.astype(np.complex128))) < 1e-12
+
+
+def test_rowpair_geometry_stays_in_bounds():
+    # the column pass's tiles (8 columns, the rows of one parity) read and
+    # write the image's elements, each exactly once and each in its own tile
+    # (so the pass runs in place); the row pass's workgroups write rows 2r and
+    # 2r + 1 of what they read from rows r and r + R/2, every row once
+    for R, C in ((4096, 4096), (4096, 2048)):
+        t0n, t1n, g, L = C // 8, 2, 8, R // 2
+        t0 = np.arange(t0n)[:, None, None, None]
+        t1 = np.arange(t1n)[None, :, None, None]
+        c = np.arange(g)[None, None, :, None]
+        k = np.arange(L)[None, None, None, :]
+        idx = t0 * 8 + t1 * C + c + k * (2 * C)
+        assert idx.min() == 0 and idx.max() == R * C - 1 and len(np.unique(idx)) == R * C
+        r = np.arange(R // 2)
+        assert sorted(np.concatenate([r, r + R // 2])) == list(range(R))
+        assert sorted(np.concatenate([2 * r, 2 * r + 1])) == list(range(R))
