@@ -585,7 +585,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         s.log_rows = log_rows;
         s.name = "fg_fft2d_rowpair_n" + std::to_string(log_cols);
         s.fn = HipBackend::get_kernel(mod, s.name.c_str());
-        s.block = Dim3(1u << (log_cols - 3));
+        s.block = Dim3(256);  // two rows of 128 threads (16 / 32 elements each at 2048 / 4096 points)
         s.src = Buf::In;
         s.dst = Buf::Out;
         s.tw = p->stage_table(log_cols, 4);

@@ -3,9 +3,9 @@
 //   X[2k]     = sum_{r < R/2} W_{R/2}^{r k} (A_r + B_r)
 //   X[2k + 1] = sum_{r < R/2} W_{R/2}^{r k} (A_r - B_r) W_R^r
 // with A_r, B_r the DFTs of rows r and r + R/2 (per column).  One workgroup
-// takes that pair of rows, one row per half of its threads (the 16-element
-// Stockham layout of fft_stockham.hpp, each half in its own LDS region), and
-// stores A + B to output row 2r and (A - B) W_R^r to output row 2r + 1.  The
+// takes that pair of rows, one row per half of its threads (a Stockham layout
+// of fft_stockham.hpp, each half in its own LDS region), and stores A + B to
+// output row 2r and (A - B) W_R^r to output row 2r + 1.  The
 // column pass then takes R/2-point DFTs over the rows of each parity in place
 // (element stride 2C), which leaves X[2k + h] at row 2k + h: an R/2-point
 // column tile holds twice the columns of an R-point one in the same LDS, so
@@ -17,30 +17,28 @@
 
 namespace fg {
 
-// Half S of the workgroup holds row S of the pair, positions T m + t.  It
-// hands the positions the other half combines (m in [8 (1 - S), 8 (1 - S) + 8))
-// to it through LDS region S.
-template <int LOGN, int S>
-__device__ __forceinline__ void rowpair_send(const float2 (&x)[16], int t, float2* region) {
-    constexpr int T = StockhamShape<LOGN, 4>::T;
+// Half S of the workgroup holds row S of the pair, positions T m + t (E
+// elements per thread, T threads per row).  It hands the positions the other
+// half combines (m in [(1 - S) E/2, (2 - S) E/2)) to it through LDS region S.
+template <int E, int T, int S>
+__device__ __forceinline__ void rowpair_send(const float2* x, int t, float2* region) {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) region[T * m + t] = x[8 * (1 - S) + m];
+    for (int m = 0; m < E / 2; ++m) region[T * m + t] = x[(E / 2) * (1 - S) + m];
 }
 
-// ... and combines positions T m + t, m in [8 S, 8 S + 8), with the other
-// row's values from LDS region 1 - S.
-template <int LOGN, int S, class IO>
-__device__ __forceinline__ void rowpair_combine(const float2 (&x)[16], int t, const float2* region, const IO& io,
-                                                uint64_t row_out, float2 w) {
-    using Sh = StockhamShape<LOGN, 4>;
+// ... and combines positions T m + t, m in [S E/2, (S + 1) E/2), with the
+// other row's values from LDS region 1 - S.
+template <int E, int T, int S, class IO>
+__device__ __forceinline__ void rowpair_combine(const float2* x, int t, const float2* region, const IO& io,
+                                                uint64_t row_out, uint64_t n, float2 w) {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const float2 o = region[Sh::T * m + t];
+    for (int m = 0; m < E / 2; ++m) {
+        const float2 o = region[T * m + t];
         const float2 a = S == 0 ? x[m] : o;
-        const float2 b = S == 0 ? o : x[8 + m];
-        const uint64_t pos = (uint64_t)Sh::T * (8 * S + m);
-        io.store_row(row_out * Sh::N + pos, t, make_float2(a.x + b.x, a.y + b.y));
-        io.store_row((row_out + 1) * Sh::N + pos, t, cmul(make_float2(a.x - b.x, a.y - b.y), w));
+        const float2 b = S == 0 ? o : x[E / 2 + m];
+        const uint64_t pos = (uint64_t)T * ((E / 2) * S + m);
+        io.store_row(row_out * n + pos, t, make_float2(a.x + b.x, a.y + b.y));
+        io.store_row((row_out + 1) * n + pos, t, cmul(make_float2(a.x - b.x, a.y - b.y), w));
     }
 }
 
@@ -74,13 +72,51 @@ __device__ __forceinline__ void fft2d_rowpair_body(const float2* __restrict__ in
     }
     StockhamStages<LOGN, 4, 0>::template run<false>(x, t, tw, lds[s]);
     __syncthreads();  // every read of the last exchange is done
-    if (s == 0) rowpair_send<LOGN, 0>(x, t, lds[0]);
-    else rowpair_send<LOGN, 1>(x, t, lds[1]);
+    if (s == 0) rowpair_send<Sh::E, Sh::T, 0>(x, t, lds[0]);
+    else rowpair_send<Sh::E, Sh::T, 1>(x, t, lds[1]);
     __syncthreads();
     const float2 w = big[r << (12 - log_rows)];
     const uint64_t row_out = first + 2 * r;
-    if (s == 0) rowpair_combine<LOGN, 0>(x, t, lds[1], io, row_out, w);
-    else rowpair_combine<LOGN, 1>(x, t, lds[0], io, row_out, w);
+    if (s == 0) rowpair_combine<Sh::E, Sh::T, 0>(x, t, lds[1], io, row_out, Sh::N, w);
+    else rowpair_combine<Sh::E, Sh::T, 1>(x, t, lds[0], io, row_out, Sh::N, w);
+}
+
+// The same pass with 32 elements per thread and each row's exchanges in
+// halves (fft_stockham.hpp, RowHalvesStages): 2T = N/16 threads and N/2 +
+// N/32 LDS positions per row, half the LDS of the 16-element layout.
+template <int LOGN>
+__device__ __forceinline__ void fft2d_rowpair_halves_body(const float2* __restrict__ in, float2* __restrict__ out,
+                                                          const float2* __restrict__ tw,
+                                                          const float2* __restrict__ big, uint64_t pairs,
+                                                          uint32_t log_rows, uint32_t flags) {
+    using H = HalvesShape<LOGN>;
+    static_assert(H::T % 64 == 0, "whole waves per row");
+    __shared__ float2 lds[2][H::HALF + H::HALF / 16];
+    const int s = threadIdx.x / H::T;  // the same for a whole wave
+    const int t = threadIdx.x - s * H::T;
+    const uint64_t p = blockIdx.x;
+    if (p >= pairs) return;  // uniform over the workgroup
+    const uint64_t half = 1ull << (log_rows - 1);
+    const uint64_t r = p & (half - 1);
+    const uint64_t first = (p >> (log_rows - 1)) << log_rows;
+    const InterleavedIOT<false, true> io{in, out};
+    const uint64_t row_in = first + r + (s ? half : 0);
+    float2 x[H::E], y[H::E];
+#pragma unroll
+    for (int m = 0; m < H::E; ++m) x[m] = io.load_row(row_in * H::N + H::T * m, t);
+    if (flags & FG_PASS_CONJ_IN) {
+#pragma unroll
+        for (int m = 0; m < H::E; ++m) x[m] = cconj(x[m]);
+    }
+    RowHalvesStages<LOGN, 0>::run(x, y, t, tw, lds[s]);
+    __syncthreads();  // every read of the last exchange is done
+    if (s == 0) rowpair_send<H::E, H::T, 0>(y, t, lds[0]);
+    else rowpair_send<H::E, H::T, 1>(y, t, lds[1]);
+    __syncthreads();
+    const float2 w = big[r << (12 - log_rows)];
+    const uint64_t row_out = first + 2 * r;
+    if (s == 0) rowpair_combine<H::E, H::T, 0>(y, t, lds[1], io, row_out, H::N, w);
+    else rowpair_combine<H::E, H::T, 1>(y, t, lds[0], io, row_out, H::N, w);
 }
 
 }  // namespace fg

@@ -95,8 +95,7 @@ def instantiated_kernels():
     for m in re.finditer(r"^FG_TILE_HALVES_P\((\d+), (\d+), _cs, true, false\)", src, flags=re.M):
         names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_h_cs")
     # row passes over row pairs (2D images of 4096 rows)
-    for m in re.finditer(r"^FG_FFT2D_ROWPAIR\((\d+)\)", src, flags=re.M):
-        names.add(f"fg_fft2d_rowpair_n{m.group(1)}")
+    names |= set(re.findall(r"void (fg_fft2d_rowpair_n\d+)\(", src))
     # narrow tiles in halves (2D columns of 2048 / 4096 points): _cc alone
     for m in re.finditer(r"^FG_TILE_HALVES_NARROW\((\d+), (\d+)\)", src, flags=re.M):
         names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_h_cc")
