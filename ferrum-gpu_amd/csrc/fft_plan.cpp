@@ -212,10 +212,17 @@ bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }
 namespace {
 
 size_t initial_chunk_limit() {
-    // 128 MiB: a chunk's intermediate array plus the streams in and out of it
-    // stay within the 256 MB Infinity Cache.  Measured on gfx950 with a copy
-    // over a working set of 2 x S: 8.4 TB/s at S = 128 MiB, 6.1 TB/s at 160.
-    size_t mib = 128;
+    // The bytes of a plan's chunks in flight at once: 256 MiB, the size of
+    // the Infinity Cache that keeps the intermediates between passes.  Plans
+    // that run two chunks at a time (FftPlan::choose_chunk) take chunks of
+    // half of it: 128 MiB each, measured on gfx950 with a copy over a working
+    // set of 2 x S: 8.4 TB/s at S = 128 MiB, 6.1 TB/s at 160.  Plans on one
+    // stream take chunks of all of it: measured at 512 MiB per execution, us,
+    // chunks of 128 -> 256 MiB, 2D 4096 x 4096 395 -> 380, 2048 x 2048 376
+    // -> 364, 4096 x 64 394 -> 386, 16 x 4096 342 -> 321, 512 x 64 343 ->
+    // 322, 4096 x 16 443 -> 413 (the two-chunk plans at 256 MiB per chunk:
+    // 1D 2^24 485 -> 638, 2D 256 x 256 324 -> 403).
+    size_t mib = 256;
     if (const char* e = getenv("FERRUM_GPU_CHUNK_MIB")) {
         char* end = nullptr;
         const unsigned long long v = strtoull(e, &end, 10);
@@ -243,7 +250,16 @@ size_t chunk_units_for(uint64_t unit_bytes, size_t batch, size_t limit, bool* ca
     return (size_t)std::min<uint64_t>(limit / unit_bytes, batch);
 }
 
-void FftPlan::choose_chunk() { chunk_ = chunk_units_for(8ull * elems(), batch_, chunk_limit_bytes(), &cached_); }
+bool FftPlan::choose_chunk(bool two_in_flight) {
+    const size_t limit = chunk_limit_bytes();
+    const uint64_t unit = 8ull * elems();
+    if (two_in_flight && unit <= limit / 2) {
+        chunk_ = chunk_units_for(unit, batch_, limit / 2, &cached_);
+        if (chunks() > 1) return true;
+    }
+    chunk_ = chunk_units_for(unit, batch_, limit, &cached_);
+    return false;
+}
 
 const char* FftPlan::policy(size_t i, size_t n) const {
     if (!cached_) return "";
@@ -398,7 +414,7 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
     S[0] = N;
     for (size_t i = 1; i <= P; ++i) S[i] = S[i - 1] >> logs[i - 1];
     if (N * batch > (1ull << 40)) invalid("transform too large");
-    p->choose_chunk();
+    const bool two = p->choose_chunk(true);
     p->work_ = dev.alloc<Cf32>(N * p->chunk_);
     const void* big = p->big_table();
     (void)big;
@@ -436,7 +452,7 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         // With two chunks in flight (below) the 16-row tile wins at 512
         // points too: 2^18 / 2^19 at 512 MiB 397 / 406 us (8 rows, one
         // stream) -> 370 / 376 us (16 rows, two streams).
-        if (p->cached_ && p->chunks() > 1 && g < 16) g = 16;
+        if (two && g < 16) g = 16;
         if (n1 < g) fail(FG_ERR_INTERNAL, "digit split leaves fewer rows than a tile");
         TileGeom t{};
         t.t0n = (uint32_t)(n1 / g);
@@ -452,7 +468,7 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         t.ocs = 1;
         t.oes = N / L;
         p->add_tile(mod, log_l, g, true, t, (uint64_t)t.t0n * t.t1n, Buf::Work, Buf::Out, p->policy(P - 1, P));
-        if (p->chunks() > 1) {
+        if (two) {
             // Two chunks in flight, one per stream: their passes overlap, so
             // one chunk's transform phases fill the other's memory phases.
             // Measured on gfx950 at 512 MiB in chunks of 128 MiB (us per
@@ -505,7 +521,9 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     }
     const bool split = split_2d_columns(log_rows);
     const size_t npass = split ? 3 : 2;
-    p->choose_chunk();
+    // Plans of 32 .. 1024 rows of at least 128 columns run two chunks at a
+    // time when they have two (the column pass below).
+    const bool two = p->choose_chunk(!split && log_rows >= 5 && log_rows <= 10 && log_cols >= 7);
     if (split) p->work_ = dev.alloc<Cf32>(RC * p->chunk_);
     // Row pass (the reference's K1 row FFT, py lib.rs:325-336): R rows of C per image.
     p->add_stockham(mod, log_cols, R, Buf::In, split ? Buf::Work : Buf::Out, p->policy(0, npass));
@@ -521,7 +539,6 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         // 4096 384 -> 372).  16-row images lost 5 % and 512 x 64 7 %, and
         // the narrow column tiles of 2048 / 4096 rows lose with two streams
         // (4096 x 4096 x 4: 425 -> 466).
-        const bool two = p->cached_ && p->chunks() > 1 && log_rows >= 5 && log_rows <= 10 && log_cols >= 7;
         const uint32_t g = (uint32_t)std::min<uint64_t>(
             (p->cached_ && !two) ? cached_tile_columns(log_rows, false) : tile_columns(log_rows), C);
         if (two) p->aux_.reset(new ChunkStream(dev.handle()));

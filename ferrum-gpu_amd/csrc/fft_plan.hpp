@@ -163,7 +163,10 @@ private:
                   uint64_t tiles_per_unit, Buf src, Buf dst, const char* policy);
     // Chunking of a multi-launch plan (sets chunk_ and cached_) and the cache
     // policy suffix of pass i of n.
-    void choose_chunk();
+    // chunk_ and cached_ for the chunk limit: chunks of half of it when the
+    // plan's shape runs two chunks at a time (two_in_flight) and the batch
+    // makes two or more of them (returns true), else of all of it.
+    bool choose_chunk(bool two_in_flight);
     const char* policy(size_t i, size_t n) const;
 
     HipDevice* dev_;

@@ -363,10 +363,12 @@ def transpose(device: Device, d_in, d_out, rows: int, cols: int, batch: int = 1,
 def set_chunk_bytes(nbytes: int) -> None:
     """Chunk limit, in bytes, for multi-launch plans (1D N > 32768, 2D) created
     from now on, process-wide.  Such a plan runs every pass over one chunk of
-    whole transforms (images) of at most ``nbytes`` before the next chunk, so
-    the chunk's intermediate array stays in the GPU's Infinity Cache.  0 turns
-    chunking off (one chunk, every pass streaming).  Default 128 MiB, or
-    FERRUM_GPU_CHUNK_MIB at library load."""
+    whole transforms (images) before the next chunk, so the chunk's
+    intermediate array stays in the GPU's Infinity Cache.  ``nbytes`` bounds
+    the chunks in flight: plans that run two chunks at a time (describe()
+    "streams" == 2) take chunks of at most nbytes / 2, the others of at most
+    ``nbytes``.  0 turns chunking off (one chunk, every pass streaming).
+    Default 256 MiB, or FERRUM_GPU_CHUNK_MIB at library load."""
     if int(nbytes) < 0:
         raise ValueError(f"chunk bytes must be >= 0, got {nbytes}")
     _n.check(_n.lib.fg_fft_set_chunk_bytes(int(nbytes)))

@@ -206,12 +206,15 @@ FG_API int fg_graph_destroy(fg_graph_t graph);
  * 16384 points).  No
  * counterpart in the reference, whose GPU path has no multi-pass plans
  * (crates/ferrum-gpu-fft/src/plan.rs:58).  Such a plan runs all of its passes
- * over one chunk of at most `bytes` (whole transforms or images) before the
- * next, keeping the chunk's intermediate array cached (in the 256 MB
- * Infinity Cache) instead of moving it through HBM.  The limit applies to
- * plans created afterwards, process-wide; 0 disables chunking (one chunk of
- * the whole batch, every pass streaming).  Default: FERRUM_GPU_CHUNK_MIB from
- * the environment when the library loads, else 128 MiB. */
+ * over one chunk (whole transforms or images) before the next, keeping the
+ * chunk's intermediate array cached (in the 256 MB Infinity Cache) instead of
+ * moving it through HBM.  `bytes` bounds the chunks in flight at once: plans
+ * that run two chunks at a time (fg_fft_plan_streams) take chunks of at most
+ * bytes / 2 when a transform fits that (else one chunk at a time, of at most
+ * `bytes`), the others chunks of at most `bytes`.  The limit applies to plans
+ * created afterwards, process-wide; 0 disables chunking (one chunk of the
+ * whole batch, every pass streaming).  Default: FERRUM_GPU_CHUNK_MIB from the
+ * environment when the library loads, else 256 MiB. */
 FG_API int fg_fft_set_chunk_bytes(size_t bytes);
 FG_API int fg_fft_get_chunk_bytes(size_t *bytes);
 /* How a plan executes: passes per chunk, transforms (2D: images) per chunk,

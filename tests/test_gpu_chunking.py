@@ -17,7 +17,7 @@ import pytest
 
 import oracle
 from conftest import normal_c64, rel_l2, uniform_c64
-from test_multipass_model import plan_kernel_names
+from test_multipass_model import choose_chunk, plan_kernel_names, two_in_flight_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -73,9 +73,10 @@ def test_every_chunking_gives_the_same_bits(gpu_device, chunk_limit, two_d, log_
     x = uniform_c64(rng, batch * elems)
     ref = oracle.fft_2d(x, log_n) if two_d else oracle.fft_1d(x, log_n, threads=8)
     outs = {}
-    # 0: one chunk, every pass streaming; one unit per chunk; a few units per
-    # chunk; the default 128 MiB.
-    for limit in (0, unit, 3 * unit, 128 * MIB):
+    # 0: one chunk, every pass streaming; one unit at a time; one and three
+    # units per chunk with two in flight; the default 256 MiB.
+    shape = two_in_flight_shape(two_d, log_n)
+    for limit in (0, unit, 2 * unit, 6 * unit, 256 * MIB):
         chunk_limit(limit)
         print(f"[case] two_d={two_d} log_n={log_n} batch={batch} chunk_limit={limit}", flush=True)
         got, d, names = _run(gpu_device, x, log_n, batch, two_d)
@@ -84,13 +85,13 @@ def test_every_chunking_gives_the_same_bits(gpu_device, chunk_limit, two_d, log_
             assert d["chunks"] == 1 and not d["cache_resident"] and d["units_per_chunk"] == batch
             assert not any(n.endswith(("_sc", "_cs")) for n in names)
         else:
-            per = min(batch, limit // unit)
+            per, _, two = choose_chunk(unit, batch, limit, shape)
             assert d["cache_resident"] and d["units_per_chunk"] == per
-            assert d["chunks"] == -(-batch // per)
+            assert d["chunks"] == -(-batch // per) and d["streams"] == (2 if two else 1)
             # first pass streams in, last streams out, middle passes stay
             # cached; narrow tiles always cached (the model's names per pass)
             assert names[0].endswith("_sc")
-            assert names[:d["passes"]] == plan_kernel_names(two_d, log_n, cached=True, chunks=d["chunks"])
+            assert names[:d["passes"]] == plan_kernel_names(two_d, log_n, cached=True, streams=d["streams"])
         assert d["launches"] == d["passes"] * d["chunks"] == len(names)
         outs[limit] = got
     for limit, got in outs.items():
@@ -101,7 +102,9 @@ def test_every_chunking_gives_the_same_bits(gpu_device, chunk_limit, two_d, log_
 @pytest.mark.parametrize("normalize", [False, True])
 def test_chunked_inverse_and_in_place(gpu_device, chunk_limit, two_d, log_n, batch, normalize):
     elems = 1 << (2 * log_n if two_d else log_n)
-    chunk_limit(2 * 8 * elems)  # two units per chunk: the last chunk is partial for odd batches
+    # two units per chunk (the last chunk partial for odd batches): two such
+    # chunks in flight for 1D
+    chunk_limit((4 if two_in_flight_shape(two_d, log_n) else 2) * 8 * elems)
     rng = np.random.default_rng(950 + log_n)
     x = normal_c64(rng, batch * elems)
     ref = (oracle.fft_2d(x, log_n, "inverse", normalize) if two_d
@@ -119,7 +122,7 @@ def test_chunked_split_layout(gpu_device, chunk_limit):
 
     log_n, batch = 16, 12
     n = batch << log_n
-    chunk_limit(4 * 8 << log_n)
+    chunk_limit(8 * 8 << log_n)  # two chunks of 4 in flight
     rng = np.random.default_rng(977)
     x = uniform_c64(rng, n)
     plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
@@ -139,8 +142,8 @@ def test_chunked_split_layout(gpu_device, chunk_limit):
 def test_chunk_limit_applies_to_new_plans_only(gpu_device, chunk_limit):
     import ferrum_gpu
 
-    chunk_limit(128 * MIB)
-    a = ferrum_gpu.fft.Plan1D(16, 512, gpu_device)  # 256 MiB: two chunks of 256 transforms
+    chunk_limit(256 * MIB)
+    a = ferrum_gpu.fft.Plan1D(16, 512, gpu_device)  # 256 MiB: two chunks of 256 transforms in flight
     chunk_limit(0)
     b = ferrum_gpu.fft.Plan1D(16, 512, gpu_device)
     assert a.describe()["chunks"] == 2 and a.describe()["units_per_chunk"] == 256

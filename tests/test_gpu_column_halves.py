@@ -17,7 +17,7 @@ import pytest
 
 from conftest import rel_l2, uniform_c64
 from test_gpu_extras import oracle_2d_rect
-from test_multipass_model import two_stream_2d
+from test_multipass_model import choose_chunk, two_in_flight_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -72,12 +72,16 @@ def test_halves_column_pass_chunked(gpu_device, chunk_limit, lr, lc, batch, per_
     image = 8 << (lr + lc)
     rng = np.random.default_rng(4000 + 16 * lr + lc)
     x = uniform_c64(rng, batch * (image // 8)).reshape(batch, 1 << lr, 1 << lc)
-    chunk_limit(per_chunk * image)
+    # the limit bounds the chunks in flight: twice the chunk for shapes that
+    # run two at a time
+    shape = two_in_flight_shape(True, lr, lc)
+    limit = per_chunk * image * (2 if shape else 1)
+    chunk_limit(limit)
     print(f"[case] 2d {1 << lr}x{1 << lc} batch={batch} chunk={per_chunk} images", flush=True)
     fwd, d, names = _exec(gpu_device, x, lr, lc, "forward", False)
     # 1024 rows of at least 128 columns in several chunks: two chunks in
     # flight with 16-column halves tiles (two_stream_2d), else 8 columns
-    wide = two_stream_2d(lr, lc, True, d["chunks"])
+    _, _, wide = choose_chunk(image, batch, limit, shape)
     assert names[-1] == (f"fg_tile_l{lr}_g16_h_cs" if wide else f"fg_tile_l{lr}_g8_h_cc"), names
     assert d["streams"] == (2 if wide else 1)
     assert d["units_per_chunk"] == per_chunk and d["chunks"] == -(-batch // per_chunk)
@@ -86,7 +90,7 @@ def test_halves_column_pass_chunked(gpu_device, chunk_limit, lr, lc, batch, per_
     assert rel_l2(inv, oracle_2d_rect(fwd, lr, lc, "inverse", True)) <= TOL
     assert rel_l2(inv, x) <= TOL
     # one chunk for the whole batch: other grids, other tile orders, same bits
-    chunk_limit(batch * image)
+    chunk_limit(2 * batch * image)
     one, d1, _ = _exec(gpu_device, x, lr, lc, "forward", False)
     assert d1["chunks"] == 1
     assert np.array_equal(one.view(np.uint32), fwd.view(np.uint32))

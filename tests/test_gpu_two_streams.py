@@ -72,10 +72,10 @@ def test_two_streams_match_one_stream_bits(gpu_device, chunk_limit, log_n, batch
     rng = np.random.default_rng(log_n * 31 + batch)
     x = normal_c64(rng, batch * n)
     print(f"[case] two streams log_n={log_n} batch={batch} chunk={per_chunk}", flush=True)
-    chunk_limit(per_chunk * n * 8)
+    chunk_limit(2 * per_chunk * n * 8)  # the limit bounds both chunks in flight
     two, d2 = _run(gpu_device, x, log_n, batch)
     assert d2["streams"] == 2 and d2["chunks"] == -(-batch // per_chunk)
-    chunk_limit(batch * n * 8)
+    chunk_limit(2 * batch * n * 8)
     one, d1 = _run(gpu_device, x, log_n, batch)
     assert d1["streams"] == 1 and d1["chunks"] == 1
     assert np.array_equal(two.view(np.uint32), one.view(np.uint32))
@@ -91,7 +91,7 @@ def test_two_stream_output_is_ordered_on_the_callers_stream(gpu_device, chunk_li
 
     log_n, batch = 20, 5
     n = 1 << log_n
-    chunk_limit(n * 8)
+    chunk_limit(2 * n * 8)
     x = normal_c64(np.random.default_rng(12), batch * n)
     plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
     assert plan.describe()["streams"] == 2
@@ -119,7 +119,7 @@ def test_two_stream_events_on_each_launchs_stream(gpu_device, chunk_limit):
 
     log_n, batch = 16, 8
     n = 1 << log_n
-    chunk_limit(2 * n * 8)
+    chunk_limit(4 * n * 8)
     x = normal_c64(np.random.default_rng(5), batch * n)
     plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
     d = plan.describe()
@@ -180,7 +180,7 @@ def test_two_stream_split_layout(gpu_device, chunk_limit):
 
     log_n, batch = 17, 5
     n = 1 << log_n
-    chunk_limit(n * 8)
+    chunk_limit(2 * n * 8)
     x = normal_c64(np.random.default_rng(21), batch * n)
     plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
     assert plan.describe()["streams"] == 2
@@ -201,7 +201,7 @@ def test_two_stream_split_layout(gpu_device, chunk_limit):
 def test_which_plans_take_two_streams(gpu_device, chunk_limit):
     import ferrum_gpu
 
-    chunk_limit(128 << 20)
+    chunk_limit(256 << 20)
     assert ferrum_gpu.fft.Plan1D(24, 4, gpu_device).describe()["streams"] == 2   # config 4: four chunks
     assert ferrum_gpu.fft.Plan1D(24, 1, gpu_device).describe()["streams"] == 1   # one chunk
     assert ferrum_gpu.fft.Plan1D(10, 65536, gpu_device).describe()["streams"] == 1   # single pass
@@ -226,7 +226,7 @@ def test_two_stream_plan_behind_the_host_array_path(gpu_device, chunk_limit):
 
     log_n, batch = 16, 9
     n = 1 << log_n
-    chunk_limit(n * 8)
+    chunk_limit(2 * n * 8)
     x = normal_c64(np.random.default_rng(99), batch * n)
     for direction, normalize in (("forward", False), ("inverse", True)):
         got = ferrum_gpu.fft.fft_1d_c2c_pow2(x, log_n, direction, normalize, device=gpu_device)
@@ -248,7 +248,7 @@ def test_two_stream_2d_plans_match_one_stream_bits(gpu_device, chunk_limit, lr, 
     image = 8 << (lr + lc)
     x = normal_c64(np.random.default_rng(lr * 16 + lc), batch * (image // 8)).reshape(batch, 1 << lr, 1 << lc)
     outs = []
-    for limit, streams in ((per_chunk * image, 2), (batch * image, 1)):
+    for limit, streams in ((2 * per_chunk * image, 2), (2 * batch * image, 1)):
         chunk_limit(limit)
         print(f"[case] 2d {1 << lr}x{1 << lc} batch={batch} chunk limit={limit}", flush=True)
         plan = ferrum_gpu.fft.Plan2D(lr, batch, gpu_device, log_cols=lc)

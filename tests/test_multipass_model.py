@@ -52,7 +52,7 @@ def split_1d(log_n):
     return [base + (1 if rest > 0 else 0), base + (1 if rest > 1 else 0), base]
 
 
-def tile_geometry_1d(log_n, batch, cached=True, chunks=1):
+def tile_geometry_1d(log_n, batch, cached=True, streams=1):
     """Per-pass geometry dicts (TileGeom), built as FftPlan::make_1d builds them;
     ``cached``: the plan is chunked, so passes after the first read the caches;
     ``chunks``: how many chunks the batch takes (two or more: the last pass
@@ -81,7 +81,7 @@ def tile_geometry_1d(log_n, batch, cached=True, chunks=1):
     L = sizes[-1]
     n1 = sizes[0]
     gp = cached_tile_columns(logs[-1], True) if cached else tile_columns(logs[-1])
-    if cached and chunks > 1:
+    if cached and streams == 2:
         gp = max(gp, 16)
     assert n1 >= gp
     inner = N // (n1 * L)             # values of k_2..k_{P-1}
@@ -119,13 +119,42 @@ def rowpair_model(x):
     return out
 
 
-def two_stream_2d(log_rows, log_cols, cached, chunks):
-    """FftPlan::make_2d: plans of 32 .. 1024 rows of at least 128 columns in two
-    or more chunks run two chunks at a time, with the wide column tiles."""
-    return cached and chunks > 1 and 5 <= log_rows <= 10 and log_cols >= 7
+def two_in_flight_shape(two_d, log_rows, log_cols=None):
+    """FftPlan::make_1d / make_2d: the multi-pass shapes that run two chunks at
+    a time when the batch makes two or more (1D; 2D of 32 .. 1024 rows of at
+    least 128 columns)."""
+    if not two_d:
+        return True
+    lc = log_rows if log_cols is None else log_cols
+    return 5 <= log_rows <= 10 and lc >= 7
 
 
-def tile_geometry_2d(log_n, batch, log_cols=None, cached=True, chunks=1):
+def choose_chunk(unit, batch, limit, two_in_flight):
+    """FftPlan::choose_chunk (fft_plan.cpp): (units per chunk, cached, two chunks
+    in flight).  The limit bounds the bytes in flight: chunks of limit / 2 for
+    shapes that run two at a time when a unit fits and the batch makes two or
+    more, else chunks of the limit; 0 or a unit above the limit: one
+    streaming chunk."""
+    def units_for(lim):
+        if lim == 0 or unit > lim:
+            return batch, False
+        return min(lim // unit, batch), True
+
+    if two_in_flight and unit <= limit // 2:
+        per, cached = units_for(limit // 2)
+        if -(-batch // per) > 1:
+            return per, cached, True
+    per, cached = units_for(limit)
+    return per, cached, False
+
+
+def two_stream_2d(log_rows, log_cols, cached, streams):
+    """FftPlan::make_2d: plans of 32 .. 1024 rows of at least 128 columns with
+    two chunks in flight (streams == 2) take the wide column tiles."""
+    return cached and streams == 2 and two_in_flight_shape(True, log_rows, log_cols)
+
+
+def tile_geometry_2d(log_n, batch, log_cols=None, cached=True, streams=1):
     """Column FFT of each R x C image after the row pass, as FftPlan::make_2d builds it
     (R = 2^log_n rows, C = 2^log_cols columns, square by default): one tile pass over
     min(width, C) adjacent columns of length R, in place; the width is the
@@ -133,7 +162,7 @@ def tile_geometry_2d(log_n, batch, log_cols=None, cached=True, chunks=1):
     R = 1 << log_n
     C = R if log_cols is None else 1 << log_cols
     lc = log_n if log_cols is None else log_cols
-    wide = two_stream_2d(log_n, lc, cached, chunks)
+    wide = two_stream_2d(log_n, lc, cached, streams)
     g = min(cached_tile_columns(log_n, False) if (cached and not wide) else tile_columns(log_n), C)
     return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
                  is0=g, is1=0, is2=R * C, ics=1, ies=C,
@@ -164,11 +193,11 @@ def use_halves_tile(log_l, g, rowwise, reads_input):
     return log_l == 10 and g in (8, 16)
 
 
-def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, chunks=1):
+def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
     """The kernel of every pass of a plan of 1D length 2^log_n (one pass up to
     16384 points, several beyond) or of 2D images with 2^log_n rows and
-    2^log_cols columns, in launch order; ``chunks``: how many chunks the batch
-    takes (two or more: the two-stream widths)."""
+    2^log_cols columns, in launch order; ``streams``: 2 for plans with two
+    chunks in flight (the two-stream widths)."""
     def tile(p, pol, reads_input=False):
         kind = "h" if use_halves_tile(p["log_l"], p["g"], p["rowwise"], reads_input) else \
             ("r" if p["rowwise"] else "c")
@@ -179,7 +208,7 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, chunks=1):
             # single pass: the Stockham kernel (fg_fft_n13 / n14 / n15: 32
             # elements per thread, exchanges in halves; test_tile_halves_model)
             return [f"fg_fft_n{log_n}"]
-        passes = tile_geometry_1d(log_n, 1, cached, chunks)
+        passes = tile_geometry_1d(log_n, 1, cached, streams)
         return [tile(p, pass_policy(i, len(passes), cached, p["g"]), reads_input=(i == 0))
                 for i, p in enumerate(passes)]
     lc = log_n if log_cols is None else log_cols
@@ -189,7 +218,7 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, chunks=1):
     if rowpair_2d(log_n, lc):
         # 4096 rows of 2048 / 4096 points: row pairs, then 2048-row halves
         return [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l11_g8_h_cc"]
-    passes = tile_geometry_2d(log_n, 1, lc, cached, chunks)
+    passes = tile_geometry_2d(log_n, 1, lc, cached, streams)
     n = len(passes) + 1
     return [f"fg_fft_n{lc}" + ("_sc" if cached else "")] + \
         [tile(p, pass_policy(i + 1, n, cached, p["g"])) for i, p in enumerate(passes)]
@@ -341,10 +370,12 @@ def test_tile_orders_of_the_2d_column_passes():
         for log_cols in range(4, 13):
             p = tile_geometry_2d(log_rows, 1, log_cols)[0]
             assert p["g"] == 8 and use_halves_tile(log_rows, 8, False, False)
-            # a full 128 MiB chunk: 2^21 / R tiles whatever C, so always line groups
-            units = (128 << 20) // (8 << (log_rows + log_cols))
+            # a full chunk at the default limit (128 MiB with two in flight,
+            # else 256): 2^21 / R or 2^22 / R tiles whatever C, so always line groups
+            unit = 8 << (log_rows + log_cols)
+            units, _, two = choose_chunk(unit, 1 << 20, 256 << 20, two_in_flight_shape(True, log_rows, log_cols))
             tiles = p["t0n"] * units
-            assert tiles == (1 << 21) >> log_rows
+            assert tiles == ((1 << 21) if two else (1 << 22)) >> log_rows
             assert tile_order(log_rows, 8, False, False, tiles) == 2
     # a short last chunk whose grid is no multiple of 16 keeps the natural order
     assert tile_order(12, 8, False, False, 2 * 3) == 0
@@ -406,3 +437,31 @@ def test_rowpair_geometry_stays_in_bounds():
         r = np.arange(R // 2)
         assert sorted(np.concatenate([r, r + R // 2])) == list(range(R))
         assert sorted(np.concatenate([2 * r, 2 * r + 1])) == list(range(R))
+
+
+def test_chunk_choice_bounds_the_bytes_in_flight():
+    MIB = 1 << 20
+    # config 4: four 128 MiB transforms, two chunks of one in flight
+    assert choose_chunk(128 * MIB, 4, 256 * MIB, True) == (1, True, True)
+    # config 5: two 128 MiB images on one stream, one chunk of both
+    assert choose_chunk(128 * MIB, 2, 256 * MIB, False) == (2, True, False)
+    # a batch that fits half the limit: one chunk, one stream
+    assert choose_chunk(MIB, 100, 256 * MIB, True) == (100, True, False)
+    # 512 MiB of 2D 256 x 256 images: 128 MiB chunks, two in flight
+    assert choose_chunk(512 * 1024, 1024, 256 * MIB, True) == (256, True, True)
+    # a unit above half the limit: one chunk at a time of the whole limit
+    assert choose_chunk(3 * MIB, 5, 4 * MIB, True) == (1, True, False)
+    # chunking off, or a unit above the limit: one streaming chunk
+    assert choose_chunk(MIB, 7, 0, True) == (7, False, False)
+    assert choose_chunk(8 * MIB, 7, 4 * MIB, False) == (7, False, False)
+    for unit in (1, 3, 64, 1000):
+        for batch in (1, 2, 5, 64):
+            for limit in (0, unit, 2 * unit, 3 * unit, 7 * unit, 1000 * unit):
+                for shape in (False, True):
+                    per, cached, two = choose_chunk(unit, batch, limit, shape)
+                    assert 1 <= per <= batch
+                    assert cached == (limit > 0 and unit <= limit)
+                    if two:  # two chunks in flight stay within the limit
+                        assert shape and 2 * per * unit <= limit and per < batch
+                    elif cached:
+                        assert per * unit <= limit

@@ -51,7 +51,7 @@ def test_chunk_limit_round_trip():
     # Process-wide; read by plans when they are created (no device needed).
     saved = ferrum_gpu.fft.get_chunk_bytes()
     try:
-        assert saved == 128 << 20 or os.environ.get("FERRUM_GPU_CHUNK_MIB")
+        assert saved == 256 << 20 or os.environ.get("FERRUM_GPU_CHUNK_MIB")
         for v in (0, 1, 64 << 20, 1 << 40):
             ferrum_gpu.fft.set_chunk_bytes(v)
             assert ferrum_gpu.fft.get_chunk_bytes() == v
@@ -112,11 +112,11 @@ def planned_kernels():
     for cached in (False, True):
         for log_n in range(13, 25):
             names |= set(plan_kernel_names(False, log_n, cached))
-            names |= set(plan_kernel_names(False, log_n, cached, chunks=2))
+            names |= set(plan_kernel_names(False, log_n, cached, streams=2))
         for lr in range(4, 13):
             for lc in range(4, 13):
                 names |= set(plan_kernel_names(True, lr, cached, lc))
-                names |= set(plan_kernel_names(True, lr, cached, lc, chunks=2))
+                names |= set(plan_kernel_names(True, lr, cached, lc, streams=2))
                 if lr + lc <= 14:   # one-pass images: exec_split's twin
                     names.add(f"fg_fft2d_l{lr}_{lc}_split")
     return names
