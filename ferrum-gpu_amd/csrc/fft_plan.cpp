@@ -197,10 +197,8 @@ bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise, bool reads_input)
     // 4096 points always exchange in halves (twice the columns per tile in
     // the same LDS; add_tile gives the timings); 1024 points too, 46.6 ..
     // 52.5 -> 44.7 .. 48.5 us per 128 MiB pass at 64 .. 4096 columns; 512
-    // points lose (41.5 .. 46.7 -> 45.8 .. 47.3).  The 16-column passes of
-    // 1024 points (two-stream and unchunked 2D plans) take the halves tile
-    // too: with two streams 2 .. 7 % faster per plan than with the 16-element
-    // tile.
+    // points lose (41.5 .. 46.7 -> 45.8 .. 47.3).  The 16-column pass of
+    // 1024 points (unchunked 2D plans) takes the halves tile too.
     if (rowwise) return false;
     if (log_l > 10) return true;
     if (reads_input) return log_l >= 7 && g == tile_columns(log_l);
@@ -521,27 +519,20 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     }
     const bool split = split_2d_columns(log_rows);
     const size_t npass = split ? 3 : 2;
-    // Plans of 32 .. 1024 rows of at least 128 columns run two chunks at a
-    // time when they have two (the column pass below).
-    const bool two = p->choose_chunk(!split && log_rows >= 5 && log_rows <= 10 && log_cols >= 7);
+    // One chunk at a time, of up to the whole chunk limit.  Measured on
+    // gfx950 at 512 MiB against two chunks of half of it in flight on two
+    // streams (with the wide column tiles), us per execution, 32 .. 1024 rows
+    // of 128 .. 4096 columns: 21 of 25 shapes faster by 0.6 .. 7.5 % (256 x
+    // 256 324 -> 315, 1024 x 2048 378 -> 350, 32 x 1024 336 -> 314), 128 x
+    // 2048 / 4096 and 512 x 4096 0.6 .. 1.3 % slower.
+    p->choose_chunk(false);
     if (split) p->work_ = dev.alloc<Cf32>(RC * p->chunk_);
     // Row pass (the reference's K1 row FFT, py lib.rs:325-336): R rows of C per image.
     p->add_stockham(mod, log_cols, R, Buf::In, split ? Buf::Work : Buf::Out, p->policy(0, npass));
     if (!split) {
         // Column pass, in place: G adjacent columns of length R per tile.
-        // Plans of 32 .. 1024 rows of at least 128 columns in two or more
-        // chunks run two chunks at a time (the odd ones on the plan's own
-        // stream, as the 1D plans) with the wide tiles of the HBM passes:
-        // measured on gfx950 at 512 MiB, us per execution against one stream
-        // with the 8-column tiles, 32 x 1024 .. 512 x 4096: 1.4 .. 10 %
-        // faster (256 x 256 337 -> 328, 128 x 2048 366 -> 330, 512 x 4096
-        // 373 -> 353); 1024 rows (16 columns in halves) 1.5 .. 3 % (1024 x
-        // 4096 384 -> 372).  16-row images lost 5 % and 512 x 64 7 %, and
-        // the narrow column tiles of 2048 / 4096 rows lose with two streams
-        // (4096 x 4096 x 4: 425 -> 466).
         const uint32_t g = (uint32_t)std::min<uint64_t>(
-            (p->cached_ && !two) ? cached_tile_columns(log_rows, false) : tile_columns(log_rows), C);
-        if (two) p->aux_.reset(new ChunkStream(dev.handle()));
+            p->cached_ ? cached_tile_columns(log_rows, false) : tile_columns(log_rows), C);
         TileGeom t{};
         t.t0n = (uint32_t)(C / g);
         t.t1n = 1;

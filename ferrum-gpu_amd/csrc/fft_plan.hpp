@@ -55,15 +55,14 @@ public:
     // Multi-launch plans run chunk by chunk: every pass over chunk_units()
     // transforms (images) before the next chunk, so a chunk's intermediate
     // array stays in the Infinity Cache (chunk_bytes()).  Plans with
-    // streams() == 2 run the odd chunks on a second stream of their own (1D:
-    // with a second workspace), forked from `stream` at the start and joined
+    // streams() == 2 run the odd chunks on a second stream of their own with
+    // a second workspace, forked from `stream` at the start and joined
     // back at the end (on a capturing stream: every chunk on `stream`).
     // With `events` (launches() of them), events[i] is recorded right after
     // launch i on the stream launch i runs on (chunk_stream()).
     void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
               hipEvent_t* events = nullptr) const;
-    // 1, or 2 for multi-pass plans of two or more chunks: 1D, and 2D of
-    // 32 .. 1024 rows of at least 128 columns.
+    // 1, or 2 for multi-pass 1D plans of two or more chunks.
     int streams() const { return aux_ ? 2 : 1; }
     // The stream a chunk's launches run on: 0 the caller's, 1 the plan's own.
     int chunk_stream(size_t chunk) const { return aux_ ? (int)(chunk & 1) : 0; }

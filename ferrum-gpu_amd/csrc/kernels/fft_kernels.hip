@@ -410,9 +410,6 @@ FG_TILE_HALVES(10, 16)
 FG_TILE_HALVES_NARROW(10, 8)
 FG_TILE_HALVES_NARROW(11, 8)
 FG_TILE_HALVES_NARROW(12, 8)
-// 2D column passes of 1024 rows in 16 columns (two chunks in flight, or
-// unchunked): cached in, streamed out.
-FG_TILE_HALVES_P(10, 16, _cs, true, false)
 // Row passes (last 1D digit: rows contiguous, transposed store): the widths
 // for HBM-resident input, then those for cache-resident input.
 FG_TILE(7, 64, true, r)

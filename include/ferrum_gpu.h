@@ -222,10 +222,10 @@ FG_API int fg_fft_get_chunk_bytes(size_t *bytes);
  * are kept cached (1) or every pass streams (0). */
 FG_API int fg_fft_plan_chunking(fg_fft_plan_t plan, int *passes, size_t *units_per_chunk, int *chunks,
                                 int *cached);
-/* Streams an execution runs on: 1, or 2 for multi-pass plans of two or more
- * chunks (1D; 2D of 2^5 .. 2^10 rows of at least 2^7 columns), which run the
- * odd chunks (launches passes*c .. passes*c + passes - 1 of chunk c) on a
- * second stream of their own (1D: with a second workspace), forked from the
+/* Streams an execution runs on: 1, or 2 for multi-pass 1D plans of two or
+ * more chunks, which run the odd chunks (launches passes*c .. passes*c +
+ * passes - 1 of chunk c) on a second stream of their own with a second
+ * workspace, forked from the
  * caller's stream when the execution starts and
  * joined back to it when it ends (so work enqueued on the caller's stream
  * afterwards sees the whole output).  On a capturing stream every chunk runs

@@ -57,7 +57,7 @@ def _exec(dev, x, lr, lc, direction, normalize):
 # (smaller ones take the one-pass kernels); tiles per image = C / 8
 CASES = [
     (10, 5, 11, 4),     # chunks of 16 tiles (line groups), the last of 12 (natural)
-    (10, 9, 5, 2),      # 512 columns in three chunks: 16-column tiles, two streams
+    (10, 9, 5, 2),      # 512 columns in three chunks
     (11, 4, 9, 3),      # 6 tiles per chunk: natural order throughout
     (11, 7, 5, 2),
     (11, 12, 2, 1),
@@ -72,25 +72,22 @@ def test_halves_column_pass_chunked(gpu_device, chunk_limit, lr, lc, batch, per_
     image = 8 << (lr + lc)
     rng = np.random.default_rng(4000 + 16 * lr + lc)
     x = uniform_c64(rng, batch * (image // 8)).reshape(batch, 1 << lr, 1 << lc)
-    # the limit bounds the chunks in flight: twice the chunk for shapes that
-    # run two at a time
-    shape = two_in_flight_shape(True, lr, lc)
-    limit = per_chunk * image * (2 if shape else 1)
+    # 2D plans run one chunk at a time, of up to the chunk limit
+    limit = per_chunk * image
     chunk_limit(limit)
     print(f"[case] 2d {1 << lr}x{1 << lc} batch={batch} chunk={per_chunk} images", flush=True)
     fwd, d, names = _exec(gpu_device, x, lr, lc, "forward", False)
-    # 1024 rows of at least 128 columns in several chunks: two chunks in
-    # flight with 16-column halves tiles (two_stream_2d), else 8 columns
-    _, _, wide = choose_chunk(image, batch, limit, shape)
-    assert names[-1] == (f"fg_tile_l{lr}_g16_h_cs" if wide else f"fg_tile_l{lr}_g8_h_cc"), names
-    assert d["streams"] == (2 if wide else 1)
+    per, _, two = choose_chunk(image, batch, limit, two_in_flight_shape(True, lr, lc))
+    assert per == per_chunk and not two
+    assert names[-1] == f"fg_tile_l{lr}_g8_h_cc", names
+    assert d["streams"] == 1
     assert d["units_per_chunk"] == per_chunk and d["chunks"] == -(-batch // per_chunk)
     assert rel_l2(fwd, oracle_2d_rect(x, lr, lc)) <= TOL
     inv, _, _ = _exec(gpu_device, fwd, lr, lc, "inverse", True)
     assert rel_l2(inv, oracle_2d_rect(fwd, lr, lc, "inverse", True)) <= TOL
     assert rel_l2(inv, x) <= TOL
     # one chunk for the whole batch: other grids, other tile orders, same bits
-    chunk_limit(2 * batch * image)
+    chunk_limit(batch * image)
     one, d1, _ = _exec(gpu_device, x, lr, lc, "forward", False)
     assert d1["chunks"] == 1
     assert np.array_equal(one.view(np.uint32), fwd.view(np.uint32))

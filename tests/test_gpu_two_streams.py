@@ -8,7 +8,7 @@ to the same plan run as one chunk on one stream, and the oracle's (the
 reference's Stockham, cpu.rs:90-124) within 1e-4; work enqueued afterwards
 on the caller's stream must see the whole output; events must be stamped on
 each launch's own stream; and under graph capture the plan runs on the
-captured stream alone.
+captured stream alone.  2D plans run one stream in every chunking.
 """
 
 from __future__ import annotations
@@ -206,9 +206,11 @@ def test_which_plans_take_two_streams(gpu_device, chunk_limit):
     assert ferrum_gpu.fft.Plan1D(24, 1, gpu_device).describe()["streams"] == 1   # one chunk
     assert ferrum_gpu.fft.Plan1D(10, 65536, gpu_device).describe()["streams"] == 1   # single pass
     assert ferrum_gpu.fft.Plan2D(12, 4, gpu_device).describe()["streams"] == 1   # narrow column tiles
-    # 32 .. 512 rows of at least 128 columns: two streams, wide column tiles
+    # every 2D plan runs one stream: 256 x 256 x 1024 (512 MiB) in two chunks
+    # of 256 MiB with the cache-resident 8-column tiles
     p2 = ferrum_gpu.fft.Plan2D(8, 1024, gpu_device)
-    assert p2.describe()["streams"] == 2 and p2.kernel_names()[1] == "fg_tile_l8_g32_c_cs"
+    d2 = p2.describe()
+    assert d2["streams"] == 1 and d2["chunks"] == 2 and p2.kernel_names()[1] == "fg_tile_l8_g8_c_cc"
     assert ferrum_gpu.fft.Plan2D(9, 2048, gpu_device, log_cols=6).describe()["streams"] == 1
     assert ferrum_gpu.fft.Plan2D(4, 2048, gpu_device, log_cols=11).describe()["streams"] == 1
     # 2^18 = 512 x 512: one chunk keeps the 8-row last pass on one stream,
@@ -234,13 +236,13 @@ def test_two_stream_plan_behind_the_host_array_path(gpu_device, chunk_limit):
         assert rel_l2(got, want) <= TOL
 
 
-# 2D (log rows, log cols, batch, images per chunk): two-stream plans take the
-# wide column tiles; one chunk takes the 8-column ones -- the same bits
+# 2D (log rows, log cols, batch, images per chunk): every 2D plan runs one
+# stream, in chunks of the whole limit; chunked and unchunked, the same bits
 CASES_2D = [(8, 8, 7, 2), (5, 10, 5, 2), (9, 7, 3, 1), (7, 12, 2, 1), (10, 8, 5, 2), (10, 12, 3, 1)]
 
 
 @pytest.mark.parametrize("lr,lc,batch,per_chunk", CASES_2D)
-def test_two_stream_2d_plans_match_one_stream_bits(gpu_device, chunk_limit, lr, lc, batch, per_chunk):
+def test_2d_plans_run_one_stream_in_every_chunking(gpu_device, chunk_limit, lr, lc, batch, per_chunk):
     import ferrum_gpu
     from ferrum_gpu.hip import DeviceBuffer
     from test_gpu_extras import oracle_2d_rect
@@ -248,11 +250,12 @@ def test_two_stream_2d_plans_match_one_stream_bits(gpu_device, chunk_limit, lr, 
     image = 8 << (lr + lc)
     x = normal_c64(np.random.default_rng(lr * 16 + lc), batch * (image // 8)).reshape(batch, 1 << lr, 1 << lc)
     outs = []
-    for limit, streams in ((2 * per_chunk * image, 2), (2 * batch * image, 1)):
+    for limit, chunks in ((per_chunk * image, -(-batch // per_chunk)), (batch * image, 1)):
         chunk_limit(limit)
         print(f"[case] 2d {1 << lr}x{1 << lc} batch={batch} chunk limit={limit}", flush=True)
         plan = ferrum_gpu.fft.Plan2D(lr, batch, gpu_device, log_cols=lc)
-        assert plan.describe()["streams"] == streams
+        d = plan.describe()
+        assert d["streams"] == 1 and d["chunks"] == chunks
         a, b = DeviceBuffer(gpu_device, plan.nbytes), DeviceBuffer(gpu_device, plan.nbytes)
         a.copy_from_host(x)
         plan.execute(a, b, "forward")

@@ -121,12 +121,8 @@ def rowpair_model(x):
 
 def two_in_flight_shape(two_d, log_rows, log_cols=None):
     """FftPlan::make_1d / make_2d: the multi-pass shapes that run two chunks at
-    a time when the batch makes two or more (1D; 2D of 32 .. 1024 rows of at
-    least 128 columns)."""
-    if not two_d:
-        return True
-    lc = log_rows if log_cols is None else log_cols
-    return 5 <= log_rows <= 10 and lc >= 7
+    a time when the batch makes two or more (1D; every 2D plan runs one)."""
+    return not two_d
 
 
 def choose_chunk(unit, batch, limit, two_in_flight):
@@ -148,22 +144,14 @@ def choose_chunk(unit, batch, limit, two_in_flight):
     return per, cached, False
 
 
-def two_stream_2d(log_rows, log_cols, cached, streams):
-    """FftPlan::make_2d: plans of 32 .. 1024 rows of at least 128 columns with
-    two chunks in flight (streams == 2) take the wide column tiles."""
-    return cached and streams == 2 and two_in_flight_shape(True, log_rows, log_cols)
-
-
-def tile_geometry_2d(log_n, batch, log_cols=None, cached=True, streams=1):
+def tile_geometry_2d(log_n, batch, log_cols=None, cached=True):
     """Column FFT of each R x C image after the row pass, as FftPlan::make_2d builds it
     (R = 2^log_n rows, C = 2^log_cols columns, square by default): one tile pass over
     min(width, C) adjacent columns of length R, in place; the width is the
-    cache-resident one when the plan is chunked (the HBM one for two-stream plans)."""
+    cache-resident one when the plan is chunked."""
     R = 1 << log_n
     C = R if log_cols is None else 1 << log_cols
-    lc = log_n if log_cols is None else log_cols
-    wide = two_stream_2d(log_n, lc, cached, streams)
-    g = min(cached_tile_columns(log_n, False) if (cached and not wide) else tile_columns(log_n), C)
+    g = min(cached_tile_columns(log_n, False) if cached else tile_columns(log_n), C)
     return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
                  is0=g, is1=0, is2=R * C, ics=1, ies=C,
                  os0=g, os1=0, os2=R * C, ocs=1, oes=C,
@@ -218,7 +206,7 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
     if rowpair_2d(log_n, lc):
         # 4096 rows of 2048 / 4096 points: row pairs, then 2048-row halves
         return [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l11_g8_h_cc"]
-    passes = tile_geometry_2d(log_n, 1, lc, cached, streams)
+    passes = tile_geometry_2d(log_n, 1, lc, cached)
     n = len(passes) + 1
     return [f"fg_fft_n{lc}" + ("_sc" if cached else "")] + \
         [tile(p, pass_policy(i + 1, n, cached, p["g"])) for i, p in enumerate(passes)]
@@ -370,12 +358,12 @@ def test_tile_orders_of_the_2d_column_passes():
         for log_cols in range(4, 13):
             p = tile_geometry_2d(log_rows, 1, log_cols)[0]
             assert p["g"] == 8 and use_halves_tile(log_rows, 8, False, False)
-            # a full chunk at the default limit (128 MiB with two in flight,
-            # else 256): 2^21 / R or 2^22 / R tiles whatever C, so always line groups
+            # a full 256 MiB chunk (the default limit, one chunk at a time):
+            # 2^22 / R tiles whatever C, so always line groups
             unit = 8 << (log_rows + log_cols)
             units, _, two = choose_chunk(unit, 1 << 20, 256 << 20, two_in_flight_shape(True, log_rows, log_cols))
             tiles = p["t0n"] * units
-            assert tiles == ((1 << 21) if two else (1 << 22)) >> log_rows
+            assert not two and tiles == (1 << 22) >> log_rows
             assert tile_order(log_rows, 8, False, False, tiles) == 2
     # a short last chunk whose grid is no multiple of 16 keeps the natural order
     assert tile_order(12, 8, False, False, 2 * 3) == 0

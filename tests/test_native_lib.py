@@ -116,7 +116,6 @@ def planned_kernels():
         for lr in range(4, 13):
             for lc in range(4, 13):
                 names |= set(plan_kernel_names(True, lr, cached, lc))
-                names |= set(plan_kernel_names(True, lr, cached, lc, streams=2))
                 if lr + lc <= 14:   # one-pass images: exec_split's twin
                     names.add(f"fg_fft2d_l{lr}_{lc}_split")
     return names
