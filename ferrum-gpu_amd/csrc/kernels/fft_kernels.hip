@@ -403,13 +403,14 @@ FG_TILE_HALVES(7, 64)
 FG_TILE_HALVES(8, 32)
 FG_TILE_HALVES(9, 16)
 FG_TILE_HALVES(10, 16)
-// 2D column passes of 1024 / 2048 / 4096 rows (cached in and out, like every
-// narrow tile): 8 columns per tile, 256 / 512 / 1024 threads, 34 / 68 / 136 KB
-// of LDS.
+// 2D column passes of 2048 / 4096 rows (cached in and out, like every narrow
+// tile): 8 columns per tile, 512 / 1024 threads, 68 / 136 KB of LDS.
 #define FG_TILE_HALVES_NARROW(LOGL, G) FG_TILE_HALVES_P(LOGL, G, _cc, true, true)
-FG_TILE_HALVES_NARROW(10, 8)
 FG_TILE_HALVES_NARROW(11, 8)
 FG_TILE_HALVES_NARROW(12, 8)
+// 2D column passes of 1024 rows of chunked plans: 16 columns, cached in,
+// streamed out.
+FG_TILE_HALVES_P(10, 16, _cs, true, false)
 // Row passes (last 1D digit: rows contiguous, transposed store): the widths
 // for HBM-resident input, then those for cache-resident input.
 FG_TILE(7, 64, true, r)

@@ -148,10 +148,12 @@ def tile_geometry_2d(log_n, batch, log_cols=None, cached=True):
     """Column FFT of each R x C image after the row pass, as FftPlan::make_2d builds it
     (R = 2^log_n rows, C = 2^log_cols columns, square by default): one tile pass over
     min(width, C) adjacent columns of length R, in place; the width is the
-    cache-resident one when the plan is chunked."""
+    cache-resident one for chunked plans of 512, 2048 and 4096 rows, else the
+    HBM one."""
     R = 1 << log_n
     C = R if log_cols is None else 1 << log_cols
-    g = min(cached_tile_columns(log_n, False) if cached else tile_columns(log_n), C)
+    narrow = cached and (log_n == 9 or log_n > 10)
+    g = min(cached_tile_columns(log_n, False) if narrow else tile_columns(log_n), C)
     return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
                  is0=g, is1=0, is2=R * C, ics=1, ies=C,
                  os0=g, os1=0, os2=R * C, ocs=1, oes=C,
@@ -178,7 +180,7 @@ def use_halves_tile(log_l, g, rowwise, reads_input):
         return True
     if reads_input:
         return 7 <= log_l and g == tile_columns(log_l)
-    return log_l == 10 and g in (8, 16)
+    return log_l == 10 and g == 16
 
 
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
@@ -354,7 +356,7 @@ def test_line_group_order_is_a_permutation_keeping_lines_on_one_xcd(grid, g):
 
 def test_tile_orders_of_the_2d_column_passes():
     # 4096 / 2048 rows: 8 columns in halves, line groups when the grid allows
-    for log_rows in (10, 11, 12):
+    for log_rows in (11, 12):
         for log_cols in range(4, 13):
             p = tile_geometry_2d(log_rows, 1, log_cols)[0]
             assert p["g"] == 8 and use_halves_tile(log_rows, 8, False, False)
@@ -367,9 +369,7 @@ def test_tile_orders_of_the_2d_column_passes():
             assert tile_order(log_rows, 8, False, False, tiles) == 2
     # a short last chunk whose grid is no multiple of 16 keeps the natural order
     assert tile_order(12, 8, False, False, 2 * 3) == 0
-    # 1024 rows: 8 columns in halves too; 512 rows: the 16-element narrow
-    # tile in XCD ranges
-    assert tile_order(10, 8, False, False, 2048) == 2
+    # 512 rows: the 16-element narrow tile in XCD ranges
     assert tile_order(9, 8, False, False, 4096) == 1
 
 

@@ -255,6 +255,6 @@ def test_narrow_halves_kernels_are_instantiated():
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     src = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
     got = {(int(a), int(b)) for a, b in re.findall(r"^FG_TILE_HALVES_NARROW\((\d+), (\d+)\)", src, flags=re.M)}
-    assert got == {(10, 8), (11, 8), (12, 8)}
+    assert got == {(11, 8), (12, 8)}
     hpp = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_tile.hpp")).read()
     assert "if constexpr (Lay::PADPOS && L == 1) return G;" in hpp
