@@ -197,11 +197,12 @@ bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise, bool reads_input)
     // 4096 points always exchange in halves (twice the columns per tile in
     // the same LDS; add_tile gives the timings); at 512 points halves lose
     // (41.5 .. 46.7 -> 45.8 .. 47.3 us per 128 MiB pass).  The 16-column
-    // pass of 1024 points (2D, chunked or not) takes the halves tile too.
+    // passes of 512 / 1024 points (2D, chunked or not) take the halves tile
+    // too.
     if (rowwise) return false;
     if (log_l > 10) return true;
     if (reads_input) return log_l >= 7 && g == tile_columns(log_l);
-    return log_l == 10 && g == 16;
+    return (log_l == 9 || log_l == 10) && g == 16;
 }
 
 bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }
@@ -530,15 +531,16 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     p->add_stockham(mod, log_cols, R, Buf::In, split ? Buf::Work : Buf::Out, p->policy(0, npass));
     if (!split) {
         // Column pass, in place: G adjacent columns of length R per tile.
-        // Chunked plans of 512, 2048 and 4096 rows take the cache-resident
+        // Chunked plans of 2048 and 4096 rows take the cache-resident
         // 8-column tiles, the others the wide tiles of the HBM passes (128 /
-        // 256 rows: 64 / 32 columns; 1024 rows: 16 columns in halves, output
-        // streamed): measured on gfx950 at 512 MiB in chunks of 256 MiB, us
-        // per execution, wide against 8 columns over 128 .. 4096 columns:
-        // 128 rows 0.8 .. 3.8 % faster, 256 rows 0 .. 2.6 %, 1024 rows 1.8 ..
-        // 7.4 % (1024 x 4096 369 -> 342); 512 rows even at 1024 / 2048
-        // columns, 2 .. 3 % slower at 128 / 512 (2.2 % faster at 4096).
-        const bool narrow = p->cached_ && (log_rows == 9 || log_rows > 10);
+        // 256 rows: 64 / 32 columns; 512 / 1024 rows: 16 columns in halves,
+        // output streamed): measured on gfx950 at 512 MiB in chunks of 256
+        // MiB, us per execution, wide against 8 columns over 128 .. 4096
+        // columns: 128 rows 0.8 .. 3.8 % faster, 256 rows 0 .. 2.6 %, 1024
+        // rows 1.8 .. 7.4 % (1024 x 4096 369 -> 342), 512 rows 0.5 .. 4.1 %
+        // from 512 columns (512 x 4096 345 -> 331), 0.5 % slower at 128 / 256
+        // (the 16-element 16-column tile: 2 .. 3 % slower there).
+        const bool narrow = p->cached_ && log_rows > 10;
         const uint32_t g = (uint32_t)std::min<uint64_t>(
             narrow ? cached_tile_columns(log_rows, false) : tile_columns(log_rows), C);
         TileGeom t{};

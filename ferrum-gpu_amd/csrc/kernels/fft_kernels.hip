@@ -408,8 +408,9 @@ FG_TILE_HALVES(10, 16)
 #define FG_TILE_HALVES_NARROW(LOGL, G) FG_TILE_HALVES_P(LOGL, G, _cc, true, true)
 FG_TILE_HALVES_NARROW(11, 8)
 FG_TILE_HALVES_NARROW(12, 8)
-// 2D column passes of 1024 rows of chunked plans: 16 columns, cached in,
-// streamed out.
+// 2D column passes of 512 / 1024 rows of chunked plans: 16 columns, cached
+// in, streamed out.
+FG_TILE_HALVES_P(9, 16, _cs, true, false)
 FG_TILE_HALVES_P(10, 16, _cs, true, false)
 // Row passes (last 1D digit: rows contiguous, transposed store): the widths
 // for HBM-resident input, then those for cache-resident input.

@@ -1,6 +1,6 @@
-"""2D column passes of 1024, 2048 and 4096 rows with the exchanges in halves:
-8-column tiles at 2048 / 4096 rows (fg_tile_l{11,12}_g8_h_cc) and their two
-tile orders, 16-column tiles at 1024 rows (fg_tile_l10_g16_h_cs).
+"""2D column passes of 512 to 4096 rows with the exchanges in halves: 8-column
+tiles at 2048 / 4096 rows (fg_tile_l{11,12}_g8_h_cc) and their two tile
+orders, 16-column tiles at 512 / 1024 rows (fg_tile_l{9,10}_g16_h_cs).
 
 A chunk whose grid is a multiple of 16 tiles runs in the line-group order
 (FG_TILE_ORDER_LINE_GROUPS), any other chunk in the natural order; the order
@@ -57,6 +57,8 @@ def _exec(dev, x, lr, lc, direction, normalize):
 # (log rows, log cols, batch, images per chunk), images above 16384 points
 # (smaller ones take the one-pass kernels); tiles per image = C / 8
 CASES = [
+    (9, 10, 3, 2),      # 16-column tiles: 64 per image
+    (9, 6, 7, 3),       # 64 columns: 4 tiles per image
     (10, 5, 11, 4),     # 16-column tiles: 2 per image
     (10, 9, 5, 2),      # 512 columns in three chunks
     (11, 4, 9, 3),      # 6 tiles per chunk: natural order throughout
@@ -80,8 +82,8 @@ def test_halves_column_pass_chunked(gpu_device, chunk_limit, lr, lc, batch, per_
     fwd, d, names = _exec(gpu_device, x, lr, lc, "forward", False)
     per, _, two = choose_chunk(image, batch, limit, two_in_flight_shape(True, lr, lc))
     assert per == per_chunk and not two
-    # 1024 rows: 16 columns, streamed out; 2048 / 4096 rows: 8 columns
-    assert names[-1] == ("fg_tile_l10_g16_h_cs" if lr == 10 else f"fg_tile_l{lr}_g8_h_cc"), names
+    # 512 / 1024 rows: 16 columns, streamed out; 2048 / 4096 rows: 8 columns
+    assert names[-1] == (f"fg_tile_l{lr}_g16_h_cs" if lr <= 10 else f"fg_tile_l{lr}_g8_h_cc"), names
     assert d["streams"] == 1
     assert d["units_per_chunk"] == per_chunk and d["chunks"] == -(-batch // per_chunk)
     assert rel_l2(fwd, oracle_2d_rect(x, lr, lc)) <= TOL

@@ -148,11 +148,11 @@ def tile_geometry_2d(log_n, batch, log_cols=None, cached=True):
     """Column FFT of each R x C image after the row pass, as FftPlan::make_2d builds it
     (R = 2^log_n rows, C = 2^log_cols columns, square by default): one tile pass over
     min(width, C) adjacent columns of length R, in place; the width is the
-    cache-resident one for chunked plans of 512, 2048 and 4096 rows, else the
-    HBM one."""
+    cache-resident one for chunked plans of 2048 and 4096 rows, else the HBM
+    one."""
     R = 1 << log_n
     C = R if log_cols is None else 1 << log_cols
-    narrow = cached and (log_n == 9 or log_n > 10)
+    narrow = cached and log_n > 10
     g = min(cached_tile_columns(log_n, False) if narrow else tile_columns(log_n), C)
     return [dict(log_l=log_n, g=g, rowwise=False, t0n=C // g, t1n=1,
                  is0=g, is1=0, is2=R * C, ics=1, ies=C,
@@ -172,15 +172,16 @@ def pass_policy(i, n, cached, g):
 
 def use_halves_tile(log_l, g, rowwise, reads_input):
     """use_halves_tile in fft_plan.cpp: the column pass that reads the plan's
-    input, and the cache-resident 8-column passes of 1024 .. 4096 points, run
-    the 32-element kernel with the exchanges in halves."""
+    input, the 8-column passes of 2048 / 4096 points and the 16-column 2D
+    column passes of 512 / 1024 points run the 32-element kernel with the
+    exchanges in halves."""
     if rowwise:
         return False
     if log_l > 10:
         return True
     if reads_input:
         return 7 <= log_l and g == tile_columns(log_l)
-    return log_l == 10 and g == 16
+    return log_l in (9, 10) and g == 16
 
 
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
