@@ -187,22 +187,22 @@ uint32_t cached_tile_columns(uint32_t log_l, bool rowwise) {
     return 8u;
 }
 
-bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise, bool reads_input) {
-    // Measured on gfx950 against the 16-element tiles at 512 MiB per plan (the
-    // first pass, us per 128 MiB chunk): 128 points 54.3 -> 50.6, 256: 57.0 ->
+bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise) {
+    // Column passes at the HBM width (tile_columns), 128 .. 1024 points, and
+    // the 8-column passes of 2048 / 4096 points exchange in halves.  Measured
+    // on gfx950 against the 16-element tiles: the 1D first pass at 512 MiB
+    // per plan, us per 128 MiB chunk, 128 points 54.3 -> 50.6, 256: 57.0 ->
     // 54.4 (config 4's pass: 52.8 -> 48.4), 512: 63.4 -> 59.4, 1024: 68.4 ->
-    // 61.0; whole plans 1-5 % faster for every 1D length 2^13 .. 2^24.
-    //
-    // 2D column passes over cache-resident data in 8-column tiles: 2048 /
-    // 4096 points always exchange in halves (twice the columns per tile in
-    // the same LDS; add_tile gives the timings); at 512 points halves lose
-    // (41.5 .. 46.7 -> 45.8 .. 47.3 us per 128 MiB pass).  The 16-column
-    // passes of 512 / 1024 points (2D, chunked or not) take the halves tile
-    // too.
+    // 61.0, whole plans 1-5 % faster for every 1D length 2^13 .. 2^24; 2D
+    // column passes (256 MiB chunks, us per plan at 512 MiB) 128 / 256 rows
+    // 0.2 .. 1.1 % faster, 512 rows 0.5 .. 4.1 % from 512 columns (0.5 %
+    // slower at 128 / 256), 1024 rows 1.8 .. 7.4 %.  2048 / 4096 points: twice the columns per tile in
+    // the same LDS (add_tile gives the timings).  The cache-resident
+    // 8-column passes of 128 .. 1024 points keep the 16-element tile: at 512
+    // points halves lost (41.5 .. 46.7 -> 45.8 .. 47.3 us per 128 MiB pass).
     if (rowwise) return false;
     if (log_l > 10) return true;
-    if (reads_input) return log_l >= 7 && g == tile_columns(log_l);
-    return (log_l == 9 || log_l == 10) && g == 16;
+    return log_l >= 7 && g == tile_columns(log_l);
 }
 
 bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }
@@ -341,7 +341,7 @@ void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g
     if ((rowwise ? geom.os0 : geom.is0) != g) fail(FG_ERR_INTERNAL, "tile geometry does not step by the tile width");
     // The pass that reads the caller's input (the first 1D pass) exchanges in
     // halves: twice the workgroups per CU to cover HBM latency.
-    const bool halves = use_halves_tile(log_l, g, rowwise, src == Buf::In);
+    const bool halves = use_halves_tile(log_l, g, rowwise);
     Step s;
     s.tile = true;
     if (narrow) {

@@ -214,10 +214,9 @@ uint32_t tile_columns(uint32_t log_l);
 // Columns (row-wise: rows) per tile for a pass that reads cache-resident data.
 uint32_t cached_tile_columns(uint32_t log_l, bool rowwise);
 // Whether a tile pass runs the 32-element kernel with the exchanges in halves
-// (fg_tile_l*_g*_h): the column pass that reads the plan's input, at the
-// HBM width, 128 .. 1024 points, and the 2D column passes of 1024 .. 4096
-// points (8 columns; 16 at 1024 points in two-stream and unchunked plans).
-bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise, bool reads_input);
+// (fg_tile_l*_g*_h): column passes at the HBM width (tile_columns) of 128 ..
+// 1024 points, and the 8-column passes of 2048 / 4096 points.
+bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise);
 // Whether the column FFT of an image with 2^log_rows rows runs as two passes.
 bool split_2d_columns(uint32_t log_rows);
 // Largest chunk (bytes of one chunk's array) a multi-launch plan created from

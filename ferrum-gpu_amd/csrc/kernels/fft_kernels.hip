@@ -359,36 +359,22 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 // and store through the caches, in XCD-aware order: the _cc policy alone.
 #define FG_TILE_NARROW(LOGL, G, RW, TAG) FG_TILE_P(LOGL, G, RW, TAG##_cc, true, true)
 
-// Column passes reading HBM (the first 1D pass; every pass of an unchunked
-// plan): 1D digits of 64..1024 points (G = 64/32/16 by length), and 2D column
-// FFTs of 16..1024 points over G = min(that width, image columns) adjacent
-// columns.
-FG_TILE(4, 16, false, c)
-FG_TILE(4, 32, false, c)
+// Column passes of 2D images of 16 .. 64 rows (at least 512 columns, so 64
+// per tile).  From 128 points up the wide column passes run the halves
+// tiles below.
 FG_TILE(4, 64, false, c)
-FG_TILE(5, 16, false, c)
-FG_TILE(5, 32, false, c)
 FG_TILE(5, 64, false, c)
-FG_TILE(6, 16, false, c)
-FG_TILE(6, 32, false, c)
 FG_TILE(6, 64, false, c)
-FG_TILE(7, 16, false, c)
-FG_TILE(7, 32, false, c)
-FG_TILE(7, 64, false, c)
-FG_TILE(8, 16, false, c)
-FG_TILE(8, 32, false, c)
-FG_TILE(9, 16, false, c)
-FG_TILE(10, 16, false, c)
-// Column passes over cache-resident data from 128 points up (1D middle
-// passes and 2D column FFTs of chunked plans): 8 columns per tile.
+// Column passes over cache-resident data of 1D middle digits (128 / 256
+// points): 8 columns per tile.
 FG_TILE_NARROW(7, 8, false, c)
 FG_TILE_NARROW(8, 8, false, c)
-FG_TILE_NARROW(9, 8, false, c)
-// First pass of a 1D multi-pass plan (input from HBM): the same column DFTs
-// and four-step twiddle with 32 elements per thread and the exchanges in
-// halves (fft_tile_halves_body): half the LDS of the tiles above, so twice
-// the workgroups per CU; at most 128 VGPRs (four waves per SIMD).  Policies:
-// none (unchunked) and _sc (a chunk's first pass).
+// Column passes at the HBM width from 128 points up (the first 1D pass, 1D
+// middle passes of unchunked plans, 2D column passes of 128 .. 1024 rows):
+// the column DFTs and four-step twiddle with 32 elements per thread and the
+// exchanges in halves (fft_tile_halves_body), half the LDS of the 16-element
+// tile, so twice the workgroups per CU; at most 128 VGPRs (four waves per
+// SIMD).  Policies: none (unchunked) and _sc (a chunk's first pass).
 #define FG_TILE_HALVES_P(LOGL, G, TAG, LC, SC)                                                             \
     extern "C" __global__ __launch_bounds__(G * HalvesShape<LOGL>::T) __attribute__((amdgpu_waves_per_eu(4))) \
     void fg_tile_l##LOGL##_g##G##_h##TAG(const float2* __restrict__ in, float2* __restrict__ out,              \
@@ -408,8 +394,10 @@ FG_TILE_HALVES(10, 16)
 #define FG_TILE_HALVES_NARROW(LOGL, G) FG_TILE_HALVES_P(LOGL, G, _cc, true, true)
 FG_TILE_HALVES_NARROW(11, 8)
 FG_TILE_HALVES_NARROW(12, 8)
-// 2D column passes of 512 / 1024 rows of chunked plans: 16 columns, cached
-// in, streamed out.
+// 2D column passes of chunked plans at the HBM width: 128 .. 1024 rows,
+// cached in, streamed out.
+FG_TILE_HALVES_P(7, 64, _cs, true, false)
+FG_TILE_HALVES_P(8, 32, _cs, true, false)
 FG_TILE_HALVES_P(9, 16, _cs, true, false)
 FG_TILE_HALVES_P(10, 16, _cs, true, false)
 // Row passes (last 1D digit: rows contiguous, transposed store): the widths

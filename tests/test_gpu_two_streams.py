@@ -207,10 +207,10 @@ def test_which_plans_take_two_streams(gpu_device, chunk_limit):
     assert ferrum_gpu.fft.Plan1D(10, 65536, gpu_device).describe()["streams"] == 1   # single pass
     assert ferrum_gpu.fft.Plan2D(12, 4, gpu_device).describe()["streams"] == 1   # narrow column tiles
     # every 2D plan runs one stream: 256 x 256 x 1024 (512 MiB) in two chunks
-    # of 256 MiB with the wide 32-column tiles
+    # of 256 MiB with the wide 32-column tiles exchanging in halves
     p2 = ferrum_gpu.fft.Plan2D(8, 1024, gpu_device)
     d2 = p2.describe()
-    assert d2["streams"] == 1 and d2["chunks"] == 2 and p2.kernel_names()[1] == "fg_tile_l8_g32_c_cs"
+    assert d2["streams"] == 1 and d2["chunks"] == 2 and p2.kernel_names()[1] == "fg_tile_l8_g32_h_cs"
     assert ferrum_gpu.fft.Plan2D(9, 2048, gpu_device, log_cols=6).describe()["streams"] == 1
     assert ferrum_gpu.fft.Plan2D(4, 2048, gpu_device, log_cols=11).describe()["streams"] == 1
     # 2^18 = 512 x 512: one chunk keeps the 8-row last pass on one stream,

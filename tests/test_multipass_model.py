@@ -170,18 +170,15 @@ def pass_policy(i, n, cached, g):
     return "_sc" if i == 0 else ("_cs" if i == n - 1 else "_cc")
 
 
-def use_halves_tile(log_l, g, rowwise, reads_input):
-    """use_halves_tile in fft_plan.cpp: the column pass that reads the plan's
-    input, the 8-column passes of 2048 / 4096 points and the 16-column 2D
-    column passes of 512 / 1024 points run the 32-element kernel with the
-    exchanges in halves."""
+def use_halves_tile(log_l, g, rowwise):
+    """use_halves_tile in fft_plan.cpp: column passes at the HBM width of 128 ..
+    1024 points and the 8-column passes of 2048 / 4096 points run the
+    32-element kernel with the exchanges in halves."""
     if rowwise:
         return False
     if log_l > 10:
         return True
-    if reads_input:
-        return 7 <= log_l and g == tile_columns(log_l)
-    return log_l in (9, 10) and g == 16
+    return 7 <= log_l and g == tile_columns(log_l)
 
 
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
@@ -189,8 +186,8 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
     16384 points, several beyond) or of 2D images with 2^log_n rows and
     2^log_cols columns, in launch order; ``streams``: 2 for plans with two
     chunks in flight (the two-stream widths)."""
-    def tile(p, pol, reads_input=False):
-        kind = "h" if use_halves_tile(p["log_l"], p["g"], p["rowwise"], reads_input) else \
+    def tile(p, pol):
+        kind = "h" if use_halves_tile(p["log_l"], p["g"], p["rowwise"]) else \
             ("r" if p["rowwise"] else "c")
         return f"fg_tile_l{p['log_l']}_g{p['g']}_{kind}{pol}"
 
@@ -200,7 +197,7 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
             # elements per thread, exchanges in halves; test_tile_halves_model)
             return [f"fg_fft_n{log_n}"]
         passes = tile_geometry_1d(log_n, 1, cached, streams)
-        return [tile(p, pass_policy(i, len(passes), cached, p["g"]), reads_input=(i == 0))
+        return [tile(p, pass_policy(i, len(passes), cached, p["g"]))
                 for i, p in enumerate(passes)]
     lc = log_n if log_cols is None else log_cols
     if log_n + lc <= 14:
@@ -229,13 +226,13 @@ def line_group_order(b, g):
     return ((j // s) * 8 + (b & 7)) * s + j % s
 
 
-def tile_order(log_l, g, rowwise, reads_input, tiles):
+def tile_order(log_l, g, rowwise, tiles):
     """TileGeom::remap of a pass (add_tile / exec in fft_plan.cpp): narrow tiles
     take the line-group order in halves, the XCD-range order otherwise, each
     only when the grid is a multiple of its unit; wide tiles the natural one."""
     if g >= 16:
         return 0
-    if use_halves_tile(log_l, g, rowwise, reads_input):
+    if use_halves_tile(log_l, g, rowwise):
         return 2 if tiles % (8 * (16 // g)) == 0 else 0
     return 1 if tiles % 8 == 0 else 0
 
@@ -360,18 +357,18 @@ def test_tile_orders_of_the_2d_column_passes():
     for log_rows in (11, 12):
         for log_cols in range(4, 13):
             p = tile_geometry_2d(log_rows, 1, log_cols)[0]
-            assert p["g"] == 8 and use_halves_tile(log_rows, 8, False, False)
+            assert p["g"] == 8 and use_halves_tile(log_rows, 8, False)
             # a full 256 MiB chunk (the default limit, one chunk at a time):
             # 2^22 / R tiles whatever C, so always line groups
             unit = 8 << (log_rows + log_cols)
             units, _, two = choose_chunk(unit, 1 << 20, 256 << 20, two_in_flight_shape(True, log_rows, log_cols))
             tiles = p["t0n"] * units
             assert not two and tiles == (1 << 22) >> log_rows
-            assert tile_order(log_rows, 8, False, False, tiles) == 2
+            assert tile_order(log_rows, 8, False, tiles) == 2
     # a short last chunk whose grid is no multiple of 16 keeps the natural order
-    assert tile_order(12, 8, False, False, 2 * 3) == 0
+    assert tile_order(12, 8, False, 2 * 3) == 0
     # 512 rows: the 16-element narrow tile in XCD ranges
-    assert tile_order(9, 8, False, False, 4096) == 1
+    assert tile_order(9, 8, False, 4096) == 1
 
 
 @pytest.mark.parametrize("log_l,g", [(11, 8), (10, 16), (10, 8), (9, 8), (8, 32), (8, 16), (8, 8),
