@@ -173,3 +173,29 @@ def test_plan_kernels_follow_the_tile_width_tables(gpu_device, chunk_limit, chun
             plan = ferrum_gpu.fft.Plan2D(lr, 1, gpu_device, log_cols=lc)
             assert plan.kernel_names() == plan_kernel_names(True, lr, chunked, lc), (lr, lc)
             plan.destroy()
+
+
+def test_default_chunking_of_the_baseline_configs(gpu_device, chunk_limit):
+    # The default limit (256 MiB of chunks in flight): configs 1-3 are single
+    # launches; config 4 (four 128 MiB transforms) runs two chunks of one at a
+    # time on two streams; config 5 (two 128 MiB images) one chunk of both on
+    # one stream.
+    import ferrum_gpu
+
+    chunk_limit(256 * MIB)
+    for log_n, batch in ((10, 256), (8, 256), (12, 256), (10, 65536)):
+        p = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
+        d = p.describe()
+        assert d["launches"] == 1 and d["chunks"] == 1 and d["streams"] == 1, (log_n, batch, d)
+        p.destroy()
+    p4 = ferrum_gpu.fft.Plan1D(24, 4, gpu_device)
+    d4 = p4.describe()
+    assert (d4["passes"], d4["chunks"], d4["units_per_chunk"], d4["streams"]) == (3, 4, 1, 2)
+    assert d4["cache_resident"]
+    p4.destroy()
+    p5 = ferrum_gpu.fft.Plan2D(12, 2, gpu_device)
+    d5 = p5.describe()
+    assert (d5["passes"], d5["chunks"], d5["units_per_chunk"], d5["streams"]) == (2, 1, 2, 1)
+    assert d5["cache_resident"] and d5["workspace_bytes"] == 0
+    assert p5.kernel_names() == ["fg_fft2d_rowpair_n12", "fg_tile_l11_g8_h_cc"]
+    p5.destroy()
