@@ -17,7 +17,7 @@ import pytest
 
 import oracle
 from conftest import normal_c64, rel_l2, uniform_c64
-from test_multipass_model import choose_chunk, plan_kernel_names, two_in_flight_shape
+from test_multipass_model import choose_chunk, plan_kernel_names, rowpair_2d, two_in_flight_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -90,7 +90,8 @@ def test_every_chunking_gives_the_same_bits(gpu_device, chunk_limit, two_d, log_
             assert d["chunks"] == -(-batch // per) and d["streams"] == (2 if two else 1)
             # first pass streams in, last streams out, middle passes stay
             # cached; narrow tiles always cached (the model's names per pass)
-            assert names[0].endswith("_sc")
+            # (the row-pair pass always streams in and stores cached: no suffix)
+            assert names[0].endswith("_sc") or names[0].startswith("fg_fft2d_rowpair_")
             assert names[:d["passes"]] == plan_kernel_names(two_d, log_n, cached=True, streams=d["streams"])
         assert d["launches"] == d["passes"] * d["chunks"] == len(names)
         outs[limit] = got
@@ -113,7 +114,11 @@ def test_chunked_inverse_and_in_place(gpu_device, chunk_limit, two_d, log_n, bat
     assert d["chunks"] == -(-batch // 2)
     assert rel_l2(got, ref) <= TOL
     got_ip, _, _ = _run(gpu_device, x, log_n, batch, two_d, "inverse", normalize, in_place=True)
-    assert np.array_equal(got_ip, got)
+    if two_d and rowpair_2d(log_n, log_n):
+        # out of place the plan pairs rows (another rounding of the same transform)
+        assert rel_l2(got_ip, got) <= TOL
+    else:
+        assert np.array_equal(got_ip, got)
 
 
 def test_chunked_split_layout(gpu_device, chunk_limit):

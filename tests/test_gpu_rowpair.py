@@ -1,9 +1,10 @@
-"""2D images of 4096 rows of 2048 / 4096 points out of place: the row pass over
-row pairs (fg_fft2d_rowpair_n{11,12}: rows r and r + 2048, stored as A + B to
-row 2r and (A - B) W_4096^r to row 2r + 1), then 2048-point column DFTs over
-the rows of each parity in place (fg_tile_l11_g8_h_cc, element stride 2C).
+"""2D images of 2048 / 4096 rows of 2048 / 4096 points out of place: the row
+pass over row pairs (fg_fft2d_rowpair_n{11,12}: rows r and r + R/2, stored as
+A + B to row 2r and (A - B) W_R^r to row 2r + 1), then R/2-point column DFTs
+over the rows of each parity in place (element stride 2C; fg_tile_l11_g8_h_cc
+at 4096 rows, fg_tile_l10_g16_h_cs at 2048).
 
-In place the same plan runs the row pass and the 4096-row column tiles.  Both
+In place the same plan runs the row pass and the R-row column tiles.  Both
 are checked against the oracle (the reference's 1D Stockham along rows, then
 along columns, as cpu_2d.rs:9-64 builds the 2D transform) within 1e-4, in both
 directions, chunked and unchunked (same bits: chunking only moves the
@@ -54,21 +55,20 @@ def _run(dev, x, lr, lc, direction="forward", normalize=False, in_place=False):
     return out, d, names
 
 
-# (log cols, batch, images per chunk)
-CASES = [(11, 3, 2), (12, 2, 1), (12, 1, 1)]
+# (log rows, log cols, batch, images per chunk)
+CASES = [(12, 11, 3, 2), (12, 12, 2, 1), (12, 12, 1, 1), (11, 11, 5, 2), (11, 12, 3, 2)]
 
 
-@pytest.mark.parametrize("lc,batch,per_chunk", CASES)
-def test_rowpair_out_of_place(gpu_device, chunk_limit, lc, batch, per_chunk):
-    lr = 12
+@pytest.mark.parametrize("lr,lc,batch,per_chunk", CASES)
+def test_rowpair_out_of_place(gpu_device, chunk_limit, lr, lc, batch, per_chunk):
     image = 8 << (lr + lc)
     x = uniform_c64(np.random.default_rng(900 + lc + batch), batch * (image // 8)).reshape(batch, 1 << lr, 1 << lc)
     chunk_limit(per_chunk * image)
-    print(f"[case] rowpair 4096x{1 << lc} batch={batch} chunk={per_chunk} images", flush=True)
+    print(f"[case] rowpair {1 << lr}x{1 << lc} batch={batch} chunk={per_chunk} images", flush=True)
     fwd, d, names = _run(gpu_device, x, lr, lc)
     assert rowpair_2d(lr, lc)
     assert names[:d["passes"]] == plan_kernel_names(True, lr, True, lc) == \
-        [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l11_g8_h_cc"]
+        [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l11_g8_h_cc" if lr == 12 else "fg_tile_l10_g16_h_cs"]
     assert d["workspace_bytes"] == 0 and d["streams"] == 1
     assert d["units_per_chunk"] == per_chunk and d["chunks"] == -(-batch // per_chunk)
     assert rel_l2(fwd, oracle_2d_rect(x, lr, lc)) <= TOL
@@ -84,11 +84,11 @@ def test_rowpair_out_of_place(gpu_device, chunk_limit, lc, batch, per_chunk):
     assert np.array_equal(one.view(np.uint32), fwd.view(np.uint32))
 
 
-@pytest.mark.parametrize("lc", [11, 12])
-def test_rowpair_in_place_takes_the_row_column_passes(gpu_device, lc):
-    lr, batch = 12, 2
+@pytest.mark.parametrize("lr,lc", [(12, 11), (12, 12), (11, 11), (11, 12)])
+def test_rowpair_in_place_takes_the_row_column_passes(gpu_device, lr, lc):
+    batch = 2
     x = uniform_c64(np.random.default_rng(950 + lc), batch << (lr + lc)).reshape(batch, 1 << lr, 1 << lc)
-    print(f"[case] rowpair plan in place 4096x{1 << lc} batch={batch}", flush=True)
+    print(f"[case] rowpair plan in place {1 << lr}x{1 << lc} batch={batch}", flush=True)
     got, _, _ = _run(gpu_device, x, lr, lc, in_place=True)
     want = oracle_2d_rect(x, lr, lc)
     assert rel_l2(got, want) <= TOL

@@ -95,10 +95,10 @@ def tile_geometry_1d(log_n, batch, cached=True, streams=1):
 
 
 def rowpair_2d(log_rows, log_cols):
-    """FftPlan::make_2d: images of 4096 rows of 2048 / 4096 points split their
-    column DFT radix-2 over the row index (kernels/fft_2d_rowpair.hpp) when
-    run out of place; in place they keep the row pass + 4096-row columns."""
-    return log_rows == 12 and log_cols >= 11
+    """FftPlan::make_2d: images of 2048 / 4096 rows of 2048 / 4096 points split
+    their column DFT radix-2 over the row index (kernels/fft_2d_rowpair.hpp)
+    when run out of place; in place they keep the row pass + R-row columns."""
+    return log_rows >= 11 and log_cols >= 11
 
 
 def rowpair_model(x):
@@ -204,8 +204,11 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
         # images of up to 16384 points: one pass (fg_fft2d_*, test_fft2d_small_model)
         return [f"fg_fft2d_l{log_n}_{lc}"]
     if rowpair_2d(log_n, lc):
-        # 4096 rows of 2048 / 4096 points: row pairs, then 2048-row halves
-        return [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l11_g8_h_cc"]
+        # row pairs, then R/2-row halves tiles over each row parity: 8
+        # columns at 4096 rows (narrow: always _cc), 16 at 2048 rows
+        if log_n == 12:
+            return [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l11_g8_h_cc"]
+        return [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l10_g16_h" + ("_cs" if cached else "")]
     passes = tile_geometry_2d(log_n, 1, lc, cached)
     n = len(passes) + 1
     return [f"fg_fft_n{lc}" + ("_sc" if cached else "")] + \
@@ -408,17 +411,18 @@ def test_rowpair_split_matches_fft2(R, C):
 
 
 def test_rowpair_geometry_stays_in_bounds():
-    # the column pass's tiles (8 columns, the rows of one parity) read and
+    # the column pass's tiles (8 / 16 columns, the rows of one parity) read and
     # write the image's elements, each exactly once and each in its own tile
     # (so the pass runs in place); the row pass's workgroups write rows 2r and
     # 2r + 1 of what they read from rows r and r + R/2, every row once
-    for R, C in ((4096, 4096), (4096, 2048)):
-        t0n, t1n, g, L = C // 8, 2, 8, R // 2
+    for R, C in ((4096, 4096), (4096, 2048), (2048, 2048), (2048, 4096)):
+        g = 8 if R == 4096 else 16
+        t0n, t1n, L = C // g, 2, R // 2
         t0 = np.arange(t0n)[:, None, None, None]
         t1 = np.arange(t1n)[None, :, None, None]
         c = np.arange(g)[None, None, :, None]
         k = np.arange(L)[None, None, None, :]
-        idx = t0 * 8 + t1 * C + c + k * (2 * C)
+        idx = t0 * g + t1 * C + c + k * (2 * C)
         assert idx.min() == 0 and idx.max() == R * C - 1 and len(np.unique(idx)) == R * C
         r = np.arange(R // 2)
         assert sorted(np.concatenate([r, r + R // 2])) == list(range(R))
