@@ -587,8 +587,8 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         b.oes = R1 * C;
         p->add_tile(mod, l2, g, false, b, (uint64_t)b.t0n * b.t1n, Buf::Work, Buf::Out, p->policy(2, npass));
     }
-    if (log_rows >= 11 && log_cols >= 11) {
-        // 2048 / 4096 rows of 2048 / 4096 points, out of place: the column
+    if (log_rows >= 11 && log_cols >= 10) {
+        // 2048 / 4096 rows of 1024 .. 4096 points, out of place: the column
         // DFT split radix-2 over the row index.  The row pass transforms rows
         // r and r + R/2 of an image in one workgroup and stores A + B and
         // (A - B) W_R^r to output rows 2r and 2r + 1
@@ -598,7 +598,9 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         // takes the CU's LDS), 16 at 2048 rows (whole 128-byte lines).
         // Measured on gfx950 at 512 MiB per execution against the two passes
         // above, us: 4096 x 4096 398 -> 388, 2048 x 4096 373 -> 348, 2048 x
-        // 2048 363 -> 359.  In-place executions keep the two passes above.
+        // 2048 363 -> 359, 2048 x 1024 365 -> 352, 4096 x 1024 375 -> 367
+        // (even in another A/B).  In-place executions keep the two passes
+        // above.
         p->steps_in_place_ = std::move(p->steps_);
         p->steps_.clear();
         Step s;
@@ -606,7 +608,9 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         s.log_rows = log_rows;
         s.name = "fg_fft2d_rowpair_n" + std::to_string(log_cols);
         s.fn = HipBackend::get_kernel(mod, s.name.c_str());
-        s.block = Dim3(256);  // two rows of 128 threads (16 / 32 elements each at 2048 / 4096 points)
+        // two rows of 64 / 128 / 128 threads (16 / 16 / 32 elements each at
+        // 1024 / 2048 / 4096 points)
+        s.block = Dim3(log_cols == 10 ? 128 : 256);
         s.src = Buf::In;
         s.dst = Buf::Out;
         s.tw = p->stage_table(log_cols, 4);

@@ -311,15 +311,21 @@ FG_FFT2D_HALVES(9, 4)
 FG_FFT2D_HALVES(9, 5)
 FG_FFT2D_HALVES(10, 4)
 
-// Row pass of 2D plans of 4096 rows of 2048 / 4096 points: rows r and
-// r + 2048 per workgroup of 256 threads, combined radix-2 over the row index
-// (fft_2d_rowpair.hpp), so the column pass runs 2048-row tiles.  2048 points:
-// the 16-element layout (128 threads and 17 KB of LDS per row); 4096 points:
+// Row pass of 2D plans of 2048 / 4096 rows of 1024 .. 4096 points: rows r
+// and r + R/2 per workgroup, combined radix-2 over the row index
+// (fft_2d_rowpair.hpp), so the column pass runs R/2-row tiles.  1024 / 2048
+// points: the 16-element layout (64 / 128 threads and 8.5 / 17 KB of LDS per
+// row, 128 / 256 threads per workgroup); 4096 points:
 // 32 elements per thread with the exchanges in halves (128 threads and 17 KB
 // per row, four workgroups per CU), measured on gfx950 per 4096 x 4096 image
 // against the 16-element layout (512 threads, 68 KB, two per CU): whole plan
 // 101.4 -> 99.1 us, same bits.
 #include "fft_2d_rowpair.hpp"
+extern "C" __global__ __launch_bounds__(128) void fg_fft2d_rowpair_n10(
+    const float2* __restrict__ in, float2* __restrict__ out, const float2* __restrict__ tw,
+    const float2* __restrict__ big, uint64_t pairs, uint32_t log_rows, uint32_t flags) {
+    fft2d_rowpair_body<10>(in, out, tw, big, pairs, log_rows, flags);
+}
 extern "C" __global__ __launch_bounds__(256) void fg_fft2d_rowpair_n11(
     const float2* __restrict__ in, float2* __restrict__ out, const float2* __restrict__ tw,
     const float2* __restrict__ big, uint64_t pairs, uint32_t log_rows, uint32_t flags) {

@@ -233,7 +233,7 @@ FG_API int fg_fft_plan_chunking(fg_fft_plan_t plan, int *passes, size_t *units_p
  * call, crates/ferrum-gpu-py/src/lib.rs:142-233). */
 FG_API int fg_fft_plan_streams(fg_fft_plan_t plan, int *streams);
 /* Kernel name of launch `index` of an execution out of place (d_in != d_out).
- * 2D plans of 2048 or 4096 rows of 2048 or 4096 columns run other kernels in
+ * 2D plans of 2048 or 4096 rows of 1024 .. 4096 columns run other kernels in
  * place (fg_fft_n<log_cols> rows, then column tiles of all the rows), as many
  * launches. */
 FG_API int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char *name, size_t cap);

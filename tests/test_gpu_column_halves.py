@@ -63,7 +63,7 @@ CASES = [
     (10, 9, 5, 2),      # 512 columns in three chunks
     (11, 4, 9, 3),      # 6 tiles per chunk: natural order throughout
     (11, 7, 5, 2),
-    (11, 10, 3, 1),     # 2048 x 1024 (2048 columns and more: row pairs, test_gpu_rowpair.py)
+    (11, 9, 3, 1),      # 2048 x 512 (1024 columns and more: row pairs, test_gpu_rowpair.py)
     (12, 4, 11, 8),     # 16 tiles per chunk, the last chunk 6
     (12, 6, 3, 2),      # 16 tiles per chunk, the last 8 (natural)
     (12, 9, 2, 1),

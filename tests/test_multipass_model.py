@@ -95,10 +95,10 @@ def tile_geometry_1d(log_n, batch, cached=True, streams=1):
 
 
 def rowpair_2d(log_rows, log_cols):
-    """FftPlan::make_2d: images of 2048 / 4096 rows of 2048 / 4096 points split
+    """FftPlan::make_2d: images of 2048 / 4096 rows of 1024 .. 4096 points split
     their column DFT radix-2 over the row index (kernels/fft_2d_rowpair.hpp)
     when run out of place; in place they keep the row pass + R-row columns."""
-    return log_rows >= 11 and log_cols >= 11
+    return log_rows >= 11 and log_cols >= 10
 
 
 def rowpair_model(x):
@@ -415,7 +415,7 @@ def test_rowpair_geometry_stays_in_bounds():
     # write the image's elements, each exactly once and each in its own tile
     # (so the pass runs in place); the row pass's workgroups write rows 2r and
     # 2r + 1 of what they read from rows r and r + R/2, every row once
-    for R, C in ((4096, 4096), (4096, 2048), (2048, 2048), (2048, 4096)):
+    for R, C in ((4096, 4096), (4096, 2048), (4096, 1024), (2048, 2048), (2048, 4096), (2048, 1024)):
         g = 8 if R == 4096 else 16
         t0n, t1n, L = C // g, 2, R // 2
         t0 = np.arange(t0n)[:, None, None, None]
