@@ -44,9 +44,22 @@ struct fg_device {
     std::map<std::tuple<int, uint32_t, uint32_t, size_t>, CachedPlan> plans;
     uint64_t plan_clock = 0;
     Buffer<Cf32, HipBackend> staging;
+    Buffer<Cf32, HipBackend> staging_out;  // out-of-place outputs (plans whose in-place form differs)
     fg::Pointwise pointwise;  // elementwise kernels of fft_module
     std::atomic<int> dependents{0};  // live plans and captured graphs made on this device
     std::unique_ptr<fg::HostStager> stager;  // pinned pieces of the host path (first large call)
+    // fg_fft_exec_split_noalloc: calls on this device take turns at the
+    // scratch area.  Outside stream capture each call waits for the previous
+    // call's last launch (scratch_done, recorded on its stream) before its
+    // first, so calls on different streams run one after another on the GPU.
+    std::mutex scratch_mu;
+    hipEvent_t scratch_done = nullptr;
+    ~fg_device() {
+        if (scratch_done) {
+            (void)hipSetDevice(dev->handle()->ordinal);
+            (void)hipEventDestroy(scratch_done);
+        }
+    }
 };
 
 struct fg_module {
@@ -119,6 +132,7 @@ fg_device* open_device(int ordinal) {
     // device, resolved once with the device current (scratch.hip).
     HipBackend::bind(h);
     fg::scratch_init(h->ordinal);
+    fg::hip_check(hipEventCreateWithFlags(&d->scratch_done, hipEventDisableTiming), "hipEventCreateWithFlags");
     return d.release();
 }
 
@@ -177,14 +191,27 @@ Direction parse_dir(int direction) {
 constexpr size_t kStagedBytes = 2u << 20;
 
 // Host path shared by the 1D and 2D entry points: stage through one device
-// buffer (grown on demand, kept per device), run in place, copy back.
+// buffer (grown on demand, kept per device), run in place, copy back.  Plans
+// whose in-place execution runs other kernels (the row pairs of 2D plans of
+// 2048 / 4096 rows run out of place only) run out of place into a second
+// staging buffer, so the host path gives the bits of the device path's
+// out-of-place fg_fft_exec.
 void run_host(fg_device* d, int dims, uint32_t log_n, uint32_t log_rows, size_t batch, size_t total,
               const float* in, float* out, Direction dir, bool normalize) {
     std::lock_guard<std::mutex> g(d->mu);
     FftPlan& plan = cached_plan(d, dims, log_n, log_rows, batch);
-    if (d->staging.len() < total) {
-        d->staging.reset();
-        d->staging = d->dev->alloc<Cf32>(total);
+    auto grow = [&](Buffer<Cf32, HipBackend>& b) {
+        if (b.len() < total) {
+            b.reset();
+            b = d->dev->alloc<Cf32>(total);
+        }
+    };
+    grow(d->staging);
+    Cf32* src = d->staging.data();
+    Cf32* dst = src;
+    if (plan.in_place_differs()) {
+        grow(d->staging_out);
+        dst = d->staging_out.data();
     }
     const auto& h = d->dev->handle();
     const size_t bytes = total * sizeof(Cf32);
@@ -192,14 +219,14 @@ void run_host(fg_device* d, int dims, uint32_t log_n, uint32_t log_rows, size_t 
         // Through pinned pieces and parallel host copies (host_stage.hpp).
         if (!d->stager) d->stager.reset(new fg::HostStager(h));
         const hipStream_t s = d->dev->default_stream();
-        d->stager->to_device(d->staging.data(), in, bytes, s);
-        plan.exec(d->staging.data(), d->staging.data(), dir, normalize, s);
-        d->stager->to_host(out, d->staging.data(), bytes, s);
+        d->stager->to_device(src, in, bytes, s);
+        plan.exec(src, dst, dir, normalize, s);
+        d->stager->to_host(out, dst, bytes, s);
         return;
     }
-    HipBackend::copy_async(h, d->staging.data(), in, bytes, hipMemcpyHostToDevice, nullptr);
-    plan.exec(d->staging.data(), d->staging.data(), dir, normalize, nullptr);
-    HipBackend::copy_async(h, out, d->staging.data(), bytes, hipMemcpyDeviceToHost, nullptr);
+    HipBackend::copy_async(h, src, in, bytes, hipMemcpyHostToDevice, nullptr);
+    plan.exec(src, dst, dir, normalize, nullptr);
+    HipBackend::copy_async(h, out, dst, bytes, hipMemcpyDeviceToHost, nullptr);
     d->dev->sync();
 }
 
@@ -530,9 +557,24 @@ int fg_fft_exec_split_noalloc(fg_fft_plan_t plan, const void* d_in_re, const voi
         need(plan, "plan");
         const Direction dir = parse_dir(direction);
         std::string why;
-        void* scratch = fg::scratch_device_ptr(plan->dev->dev->handle()->ordinal, &why);
-        plan->plan->exec_split_into(d_in_re, d_in_im, d_out_re, d_out_im, dir, normalize != 0, (hipStream_t)stream,
-                                    scratch, fg::kScratchBytes, why);
+        fg_device* d = plan->dev;
+        void* scratch = fg::scratch_device_ptr(d->dev->handle()->ordinal, &why);
+        const hipStream_t s = stream ? (hipStream_t)stream : d->dev->default_stream();
+        // Single-pass plans touch no scratch; a capturing stream cannot wait
+        // for an event recorded outside its capture, so captured calls keep
+        // the documented race between calls that overlap.
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        HipBackend::bind(d->dev->handle());
+        fg::hip_check(hipStreamIsCapturing(s, &cap), "hipStreamIsCapturing");
+        const bool serialize = plan->plan->split_staged_exec();
+        std::unique_lock<std::mutex> lock(d->scratch_mu, std::defer_lock);
+        if (serialize && cap == hipStreamCaptureStatusNone) {
+            lock.lock();
+            fg::hip_check(hipStreamWaitEvent(s, d->scratch_done, 0), "hipStreamWaitEvent");
+        }
+        plan->plan->exec_split_into(d_in_re, d_in_im, d_out_re, d_out_im, dir, normalize != 0, s, scratch,
+                                    fg::kScratchBytes, why);
+        if (lock.owns_lock()) fg::hip_check(hipEventRecord(d->scratch_done, s), "hipEventRecord");
     });
 }
 
@@ -627,17 +669,25 @@ int fg_graph_destroy(fg_graph_t graph) {
     });
 }
 
-int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char* name, size_t cap) {
+static int plan_kernel(fg_fft_plan_t plan, int index, char* name, size_t cap, bool in_place) {
     return guarded([&] {
         need(plan, "plan");
         need(name, "name");
-        auto names = plan->plan->kernel_names();
+        auto names = plan->plan->kernel_names(in_place);
         if (index < 0 || (size_t)index >= names.size()) fg::invalid("launch index out of range");
         if (cap) {
             strncpy(name, names[index].c_str(), cap - 1);
             name[cap - 1] = 0;
         }
     });
+}
+
+int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char* name, size_t cap) {
+    return plan_kernel(plan, index, name, cap, false);
+}
+
+int fg_fft_plan_kernel_in_place(fg_fft_plan_t plan, int index, char* name, size_t cap) {
+    return plan_kernel(plan, index, name, cap, true);
 }
 
 int fg_fft_set_chunk_bytes(size_t bytes) {
@@ -667,6 +717,13 @@ int fg_fft_plan_streams(fg_fft_plan_t plan, int* streams) {
         need(plan, "plan");
         need(streams, "streams");
         *streams = plan->plan->streams();
+    });
+}
+
+int fg_fft_plan_set_streams(fg_fft_plan_t plan, int streams) {
+    return guarded([&] {
+        need(plan, "plan");
+        plan->plan->set_streams(streams);
     });
 }
 

@@ -1,6 +1,8 @@
 // fft_plan.cpp -- plan construction and stream-ordered execution.
 #include "fft_plan.hpp"
 
+#include "launch_limits.h"
+
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -311,8 +313,6 @@ void FftPlan::add_stockham(const HipBackend::Module& mod, uint32_t log_l, uint64
     Step s;
     s.name = "fg_fft_n" + std::to_string(log_l) + (latency ? "_lat" : "") + policy;
     s.fn = HipBackend::get_kernel(mod, s.name.c_str());
-    const uint64_t blocks = (per_unit * chunk_ + g.fpb - 1) / g.fpb;
-    if (blocks > 0x7fffffffull) invalid("batch too large for one launch");
     s.block = Dim3(((1u << log_l) >> g.log_e) * g.fpb);
     s.fpb = g.fpb;
     s.src = src;
@@ -329,7 +329,7 @@ void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g
     // The kernel reads columns at stride 1 (column-wise) or elements at stride
     // 1 (row-wise) and always writes columns at stride 1.
     if ((rowwise ? geom.ies : geom.ics) != 1 || geom.ocs != 1) fail(FG_ERR_INTERNAL, "tile geometry not unit-stride");
-    if (tiles_per_unit == 0 || tiles_per_unit * chunk_ > 0x7fffffffull) invalid("too many tiles for one launch");
+    if (tiles_per_unit == 0) fail(FG_ERR_INTERNAL, "tile pass with no tiles");
     // Narrow tiles (g < 16: 32- or 64-byte pieces of each 128-byte line) load
     // and store through the caches whatever the chunking, in XCD-aware tile
     // order, so the pieces of a line from neighbouring tiles meet in one
@@ -367,24 +367,47 @@ void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g
 }
 
 FftPlan::ChunkStream::ChunkStream(const HipBackend::DeviceHandle& d) : dev(d) {
+    stream = HipBackend::chunk_stream(dev);
     HipBackend::bind(dev);
     hip_check(hipEventCreateWithFlags(&fork, hipEventDisableTiming), "hipEventCreateWithFlags");
-    hipError_t e = hipEventCreateWithFlags(&join, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);  // default priority
+    const hipError_t e = hipEventCreateWithFlags(&join, hipEventDisableTiming);
     if (e != hipSuccess) {
-        if (join) (void)hipEventDestroy(join);
         (void)hipEventDestroy(fork);
-        hip_check(e, "hipStreamCreateWithFlags");
+        hip_check(e, "hipEventCreateWithFlags");
     }
 }
 
 FftPlan::ChunkStream::~ChunkStream() {
-    try {
-        HipBackend::destroy_stream(dev, stream);  // waits for the stream's work
-    } catch (...) {
-    }
+    (void)hipSetDevice(dev->ordinal);
+    // The plan's last execution joined the chunk stream back here (an event
+    // never recorded completes at once); later work of other plans on the
+    // shared stream is theirs.
+    (void)hipEventSynchronize(join);
     (void)hipEventDestroy(fork);
     (void)hipEventDestroy(join);
+}
+
+void FftPlan::set_streams(int n) {
+    if (n != 1 && n != 2) invalid("streams must be 1 or 2, got " + std::to_string(n));
+    if (n == 2 && !aux_) invalid("this plan runs on one stream (two-stream plans: multi-pass 1D of two or more chunks)");
+    use_aux_ = n == 2;
+}
+
+void FftPlan::fit_launches() {
+    // Each step's largest units per launch; chunk_ takes the smallest.
+    uint64_t most = chunk_;
+    for (const std::vector<Step>* v : {&steps_, &steps_in_place_})
+        for (const Step& s : *v) {
+            const uint64_t threads = s.block.product();
+            // Stockham and one-pass 2D kernels: fpb units per workgroup;
+            // row-pair and tile passes: per_unit workgroups per unit.
+            const bool per_block = !s.tile && !s.rowpair;
+            const uint64_t m = per_block ? fg_max_units_per_launch(s.per_unit, s.fpb, threads)
+                                         : fg_max_units_per_launch(s.per_unit, 1, threads);
+            if (m == 0) invalid("one transform of this plan exceeds a single kernel launch");
+            most = std::min(most, m);
+        }
+    chunk_ = (size_t)most;
 }
 
 std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Module& mod, uint32_t log_n,
@@ -400,6 +423,7 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         p->main_kernel_ = p->steps_[0].name;
         p->split_fn_ = HipBackend::get_kernel(mod, (p->main_kernel_ + "_split").c_str());
         p->pw_ = Pointwise(mod);
+        p->fit_launches();
         return p;
     }
 
@@ -482,6 +506,7 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
     }
     p->main_kernel_ = p->steps_[0].name;
     p->pw_ = Pointwise(mod);
+    p->fit_launches();
     return p;
 }
 
@@ -505,7 +530,6 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         s.fn = HipBackend::get_kernel(mod, s.name.c_str());
         s.fpb = FG_SMALL2D_FPI(log_rows, log_cols);
         s.block = Dim3(FG_SMALL2D_BLOCK(log_rows, log_cols));
-        if ((batch + s.fpb - 1) / s.fpb > 0x7fffffffull) invalid("batch too large for one launch");
         s.src = Buf::In;
         s.dst = Buf::Out;
         s.tw = p->stage_table(log_cols, FG_SMALL2D_LOGE(log_rows, log_cols));
@@ -515,6 +539,7 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         p->main_kernel_ = s.name;
         p->split_fn_ = HipBackend::get_kernel(mod, (s.name + "_split").c_str());
         p->pw_ = Pointwise(mod);
+        p->fit_launches();
         return p;
     }
     const bool split = split_2d_columns(log_rows);
@@ -632,13 +657,15 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
     }
     p->main_kernel_ = p->steps_.back().name;
     p->pw_ = Pointwise(mod);
+    p->fit_launches();
     return p;
 }
 
-std::vector<std::string> FftPlan::kernel_names() const {
+std::vector<std::string> FftPlan::kernel_names(bool in_place) const {
+    const std::vector<Step>& steps = (in_place && !steps_in_place_.empty()) ? steps_in_place_ : steps_;
     std::vector<std::string> v;
     for (size_t c = 0; c < chunks(); ++c)
-        for (const Step& s : steps_) v.push_back(s.name);
+        for (const Step& s : steps) v.push_back(s.name);
     return v;
 }
 
@@ -667,7 +694,7 @@ void FftPlan::exec(const void* in, void* out, Direction dir, bool normalize, hip
     const uint64_t unit = elems();
     const hipStream_t main = stream ? stream : HipBackend::default_stream(dev_->handle());
     const std::vector<Step>& steps = (in == out && !steps_in_place_.empty()) ? steps_in_place_ : steps_;
-    bool two = aux_ != nullptr;
+    bool two = streams() == 2;
     if (two) {
         // Under stream capture the plan stays on the captured stream.
         hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
@@ -774,16 +801,24 @@ void FftPlan::split_one_launch(const void* in_re, const void* in_im, void* out_r
     uint32_t flags = dir == Direction::Inverse ? (FG_PASS_CONJ_IN | FG_PASS_CONJ_SCALE_OUT) : 0u;
     float sc = scale_for(dir, normalize);
     const void* tw = s.tw;
-    uint64_t count = s.per_unit * batch_;
-    const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
-    if (s.small2d) {
-        const void* twc = s.tw_cols;
-        void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, (void*)&twc, &count, &sc, &flags};
-        HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
-        return;
+    const void* twc = s.tw_cols;
+    const uint64_t unit = elems();
+    // One launch per chunk (one chunk unless the batch exceeds a launch).
+    for (uint64_t u0 = 0; u0 < batch_; u0 += chunk_) {
+        uint64_t count = s.per_unit * std::min<uint64_t>(chunk_, batch_ - u0);
+        const float* ir = static_cast<const float*>(in_re) + u0 * unit;
+        const float* ii = static_cast<const float*>(in_im) + u0 * unit;
+        float* orr = static_cast<float*>(out_re) + u0 * unit;
+        float* oi = static_cast<float*>(out_im) + u0 * unit;
+        const Dim3 grid((uint32_t)((count + s.fpb - 1) / s.fpb));
+        if (s.small2d) {
+            void* args[] = {&ir, &ii, &orr, &oi, (void*)&tw, (void*)&twc, &count, &sc, &flags};
+            HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
+        } else {
+            void* args[] = {&ir, &ii, &orr, &oi, (void*)&tw, &count, &sc, &flags};
+            HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
+        }
     }
-    void* args[] = {(void*)&in_re, (void*)&in_im, &out_re, &out_im, (void*)&tw, &count, &sc, &flags};
-    HipBackend::launch(dev_->handle(), stream, split_fn_, grid, s.block, 0, args);
 }
 
 void FftPlan::split_staged(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,

@@ -62,10 +62,19 @@ public:
     // launch i on the stream launch i runs on (chunk_stream()).
     void exec(const void* in, void* out, Direction dir, bool normalize, hipStream_t stream,
               hipEvent_t* events = nullptr) const;
-    // 1, or 2 for multi-pass 1D plans of two or more chunks.
-    int streams() const { return aux_ ? 2 : 1; }
-    // The stream a chunk's launches run on: 0 the caller's, 1 the plan's own.
-    int chunk_stream(size_t chunk) const { return aux_ ? (int)(chunk & 1) : 0; }
+    // 1, or 2 for multi-pass 1D plans of two or more chunks (unless
+    // set_streams(1) turned the second stream off).
+    int streams() const { return (aux_ && use_aux_) ? 2 : 1; }
+    // The most streams this plan can run on (2: it has the second stream's
+    // workspace and events).
+    int max_streams() const { return aux_ ? 2 : 1; }
+    // Runs the plan's chunks on one stream (1) or, where max_streams() is 2,
+    // alternately on two (2, the default).  Same bits either way; executions
+    // must not be in flight while it changes.
+    void set_streams(int n);
+    // The stream a chunk's launches run on: 0 the caller's, 1 the device's
+    // chunk stream (HipBackend::chunk_stream).
+    int chunk_stream(size_t chunk) const { return streams() == 2 ? (int)(chunk & 1) : 0; }
     // exec() on the split layout: real and imaginary parts in separate f32
     // arrays of batch * elems() each (the reference's *_split kernels,
     // kernels_body.rs:509-626).  Single-pass plans read and write the split
@@ -82,8 +91,13 @@ public:
     void exec_split_into(const void* in_re, const void* in_im, void* out_re, void* out_im, Direction dir,
                          bool normalize, hipStream_t stream, void* staging, size_t staging_bytes,
                          const std::string& no_staging) const;
-    // Launches exec_split makes: 1 for single-pass plans, launches() + 2 otherwise.
-    int split_launches() const { return split_fn_ ? 1 : launches() + 2; }
+    // Launches exec_split makes: one per chunk for single-pass plans (one
+    // chunk unless the batch exceeds one launch, fit_launches), launches() +
+    // 2 otherwise.
+    int split_launches() const { return split_fn_ ? (int)chunks() : launches() + 2; }
+    // Whether exec_split stages through an interleaved buffer (multi-launch
+    // plans) rather than reading and writing the split arrays directly.
+    bool split_staged_exec() const { return split_fn_ == nullptr; }
 
     Kind kind() const { return kind_; }
     // 1D: log2 of the length; 2D: log2 of the row length (columns).
@@ -101,8 +115,14 @@ public:
     bool cache_resident() const { return cached_; }
     const std::string& main_kernel() const { return main_kernel_; }
     size_t workspace_bytes() const { return work_.bytes() + work2_.bytes(); }
-    // Kernel names in launch order (out of place; steps_in_place_ has as many passes).
-    std::vector<std::string> kernel_names() const;
+    // Kernel names in launch order of an out-of-place execution, or of an
+    // in-place one (in != out): the two differ for the 2D plans of 2048 /
+    // 4096 rows of 1024 .. 4096 points, whose out-of-place form runs the row
+    // pairs (same launch count).
+    std::vector<std::string> kernel_names(bool in_place = false) const;
+    // Whether in-place executions run other kernels than out-of-place ones
+    // (same transform to rounding, not bit for bit).
+    bool in_place_differs() const { return !steps_in_place_.empty(); }
 
 private:
     // Buffers are named symbolically and bound at exec: the caller's input,
@@ -128,15 +148,17 @@ private:
         TileGeom geom{};                        // tile: addressing (flags/scale/remap set at exec)
     };
 
-    // The second stream of a two-stream plan and its fork / join events,
-    // released with the plan (after the stream's work is done).
+    // The second stream of a two-stream plan -- the device's one chunk stream,
+    // shared by every two-stream plan on the device (HipBackend::chunk_stream)
+    // -- and the plan's own fork / join events, released with the plan after
+    // its last join has completed.
     struct ChunkStream {
         explicit ChunkStream(const HipBackend::DeviceHandle& dev);
         ~ChunkStream();
         ChunkStream(const ChunkStream&) = delete;
         ChunkStream& operator=(const ChunkStream&) = delete;
         HipBackend::DeviceHandle dev;
-        hipStream_t stream = nullptr;
+        hipStream_t stream = nullptr;  // not owned
         hipEvent_t fork = nullptr, join = nullptr;
     };
 
@@ -167,6 +189,11 @@ private:
     // makes two or more of them (returns true), else of all of it.
     bool choose_chunk(bool two_in_flight);
     const char* policy(size_t i, size_t n) const;
+    // Lowers chunk_ so that every launch of steps_ and steps_in_place_ fits
+    // one HIP dispatch (launch_limits.h): a batch beyond that runs in
+    // several launches.  Called once the steps are built; a workspace sized
+    // for the old chunk_ stays large enough.
+    void fit_launches();
 
     HipDevice* dev_;
     Kind kind_;
@@ -182,6 +209,7 @@ private:
     Buffer<Cf32, HipBackend> work_;
     Buffer<Cf32, HipBackend> work2_;         // the odd chunks' workspace (two-stream 1D plans)
     std::unique_ptr<ChunkStream> aux_;       // two-stream plans: the odd chunks' stream
+    bool use_aux_ = true;                    // set_streams
     std::string main_kernel_;
     HipBackend::KernelHandle split_fn_ = nullptr;  // single-pass plans: the split-layout twin
     Pointwise pw_;

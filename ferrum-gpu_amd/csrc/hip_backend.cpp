@@ -5,6 +5,8 @@
 
 #include <string.h>
 
+#include "launch_limits.h"
+
 // The launch extension of libamdhip64 that stamps start / stop events from
 // the kernel dispatch itself (declared in hip/hip_ext.h, whose C++ templates
 // need the HIP compiler; this file is plain g++).
@@ -28,10 +30,11 @@ void hip_check(hipError_t e, const char* what) {
 }
 
 HipDeviceState::~HipDeviceState() {
-    if (stream) {
+    for (hipStream_t s : {chunk_stream, stream}) {
+        if (!s) continue;
         (void)hipSetDevice(ordinal);
-        (void)hipStreamSynchronize(stream);
-        (void)hipStreamDestroy(stream);
+        (void)hipStreamSynchronize(s);
+        (void)hipStreamDestroy(s);
     }
 }
 
@@ -148,11 +151,27 @@ HipBackend::KernelHandle HipBackend::get_kernel(const Module& mod, const char* n
     return f;
 }
 
-void HipBackend::launch(const DeviceHandle& dev, Stream stream, KernelHandle k, Dim3 grid, Dim3 block,
-                        uint32_t shared_bytes, void** args) {
+namespace {
+
+// A launch whose work-items along some dimension exceed the dispatch packet's
+// 32-bit grid size is refused here, before HIP sees it (launch_limits.h).
+void check_launch(HipBackend::KernelHandle k, Dim3 grid, Dim3 block) {
     if (!k) invalid("launch of a null kernel");
     if (grid.product() == 0 || block.product() == 0) invalid("launch with an empty grid or block");
-    if (block.product() > 1024) invalid("block of " + std::to_string(block.product()) + " threads exceeds 1024");
+    if (block.product() > FG_MAX_BLOCK_THREADS)
+        invalid("block of " + std::to_string(block.product()) + " threads exceeds 1024");
+    const uint32_t g[3] = {grid.x, grid.y, grid.z}, b[3] = {block.x, block.y, block.z};
+    for (int d = 0; d < 3; ++d)
+        if ((uint64_t)g[d] * b[d] > FG_MAX_LAUNCH_ITEMS)
+            invalid("launch of " + std::to_string(g[d]) + " x " + std::to_string(b[d]) + " work-items along one " +
+                    "dimension exceeds 2^32 - 1");
+}
+
+}  // namespace
+
+void HipBackend::launch(const DeviceHandle& dev, Stream stream, KernelHandle k, Dim3 grid, Dim3 block,
+                        uint32_t shared_bytes, void** args) {
+    check_launch(k, grid, block);
     bind(dev);
     hip_check(hipModuleLaunchKernel(k, grid.x, grid.y, grid.z, block.x, block.y, block.z, shared_bytes,
                                     stream ? stream : dev->stream, args, nullptr),
@@ -161,16 +180,9 @@ void HipBackend::launch(const DeviceHandle& dev, Stream stream, KernelHandle k, 
 
 void HipBackend::launch_stamped(const DeviceHandle& dev, Stream stream, KernelHandle k, Dim3 grid, Dim3 block,
                                 uint32_t shared_bytes, void** args, hipEvent_t stop) {
-    if (!k) invalid("launch of a null kernel");
-    if (grid.product() == 0 || block.product() == 0) invalid("launch with an empty grid or block");
-    if (block.product() > 1024) invalid("block of " + std::to_string(block.product()) + " threads exceeds 1024");
+    check_launch(k, grid, block);
+    // The extension takes the grid in work-items (32 bits each, as checked).
     const uint64_t gx = (uint64_t)grid.x * block.x, gy = (uint64_t)grid.y * block.y, gz = (uint64_t)grid.z * block.z;
-    if (gx > 0xffffffffull || gy > 0xffffffffull || gz > 0xffffffffull) {
-        // Beyond the extension's 32-bit work sizes: a plain launch and a marker.
-        launch(dev, stream, k, grid, block, shared_bytes, args);
-        hip_check(hipEventRecord(stop, stream ? stream : dev->stream), "hipEventRecord");
-        return;
-    }
     bind(dev);
     hip_check(hipExtModuleLaunchKernel(k, (uint32_t)gx, (uint32_t)gy, (uint32_t)gz, block.x, block.y, block.z,
                                        shared_bytes, stream ? stream : dev->stream, args, nullptr, nullptr, stop, 0),
@@ -187,6 +199,12 @@ HipBackend::Stream HipBackend::create_stream(const DeviceHandle& dev) {
     hipStream_t s = nullptr;
     hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
     return s;
+}
+
+HipBackend::Stream HipBackend::chunk_stream(const DeviceHandle& dev) {
+    std::lock_guard<std::mutex> lock(dev->chunk_mu);
+    if (!dev->chunk_stream) dev->chunk_stream = create_stream(dev);
+    return dev->chunk_stream;
 }
 
 void HipBackend::destroy_stream(const DeviceHandle& dev, Stream s) {

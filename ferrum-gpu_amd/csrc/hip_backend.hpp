@@ -10,6 +10,7 @@
 
 #include <functional>
 #include <memory>
+#include <mutex>
 #include <string>
 
 #include "backend.hpp"
@@ -21,6 +22,10 @@ namespace fg {
 struct HipDeviceState {
     int ordinal = 0;
     hipStream_t stream = nullptr;
+    // The device's chunk stream (HipBackend::chunk_stream), created on first
+    // use; default priority like every stream here.
+    std::mutex chunk_mu;
+    hipStream_t chunk_stream = nullptr;
     std::string arch;  // gcnArchName up to the first ':' (e.g. "gfx950")
     int cu_count = 0;
     int clock_khz = 0;
@@ -90,6 +95,12 @@ struct HipBackend {
 
     static Stream create_stream(const DeviceHandle& dev);
     static void destroy_stream(const DeviceHandle& dev, Stream s);
+    // The one extra stream per device on which two-stream FFT plans run their
+    // odd chunks (created at the first call, destroyed with the device), so
+    // such plans add one stream to the device however many exist: with four
+    // hardware queues per process (GPU_MAX_HW_QUEUES), each plan's own stream
+    // would push the chunk stream onto a queue shared with the caller's.
+    static Stream chunk_stream(const DeviceHandle& dev);
 
     // Runs `record` on a private stream under thread-local stream capture and
     // instantiates what it enqueued as one executable graph; nothing executes

@@ -106,10 +106,12 @@ _sig("fg_fft_exec", _vp, _vp, _vp, _i, _i, _vp)
 _sig("fg_fft_plan_describe", _vp, _P(_i), ctypes.c_char_p, _sz, _P(_sz))
 _sig("fg_fft_exec_events", _vp, _vp, _vp, _i, _i, _vp, _P(_vp), _i)
 _sig("fg_fft_plan_kernel", _vp, _i, ctypes.c_char_p, _sz)
+_sig("fg_fft_plan_kernel_in_place", _vp, _i, ctypes.c_char_p, _sz)
 _sig("fg_fft_set_chunk_bytes", _sz)
 _sig("fg_fft_get_chunk_bytes", _P(_sz))
 _sig("fg_fft_plan_chunking", _vp, _P(_i), _P(_sz), _P(_i), _P(_i))
 _sig("fg_fft_plan_streams", _vp, _P(_i))
+_sig("fg_fft_plan_set_streams", _vp, _i)
 _sig("fg_fft_1d_c2c_pow2_host", _vp, _vp, _vp, _sz, _u32, _i, _i)
 _sig("fg_fft_2d_c2c_pow2_host", _vp, _vp, _vp, _u32, _sz, _i, _i)
 _sig("fg_stream_copy", _vp, _vp, _vp, _sz, _vp)

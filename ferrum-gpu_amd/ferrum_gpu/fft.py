@@ -262,13 +262,23 @@ class _Plan:
                                             int(bool(normalize)), int(reps), ctypes.byref(g)))
         return Graph(self.device, g, keep=(self,))
 
-    def kernel_names(self) -> list[str]:
+    def kernel_names(self, in_place: bool = False) -> list[str]:
+        """Kernel of each launch, in launch order, of an out-of-place execution
+        (or of an in-place one: 2D plans of 2048 / 4096 rows of 1024 .. 4096
+        columns run other kernels in place)."""
+        fn = _n.lib.fg_fft_plan_kernel_in_place if in_place else _n.lib.fg_fft_plan_kernel
         names = []
         for i in range(self.describe()["launches"]):
             buf = ctypes.create_string_buffer(128)
-            _n.check(_n.lib.fg_fft_plan_kernel(self._p, i, buf, 128))
+            _n.check(fn(self._p, i, buf, 128))
             names.append(buf.value.decode())
         return names
+
+    def set_streams(self, streams: int) -> None:
+        """Run the chunks on one stream (1) or, for a plan created with
+        describe()["streams"] == 2, on two again (2); same bits either way.
+        No execution of the plan may be in flight."""
+        _n.check(_n.lib.fg_fft_plan_set_streams(self._p, int(streams)))
 
     def describe(self) -> dict:
         launches = ctypes.c_int()

@@ -224,19 +224,33 @@ FG_API int fg_fft_plan_chunking(fg_fft_plan_t plan, int *passes, size_t *units_p
                                 int *cached);
 /* Streams an execution runs on: 1, or 2 for multi-pass 1D plans of two or
  * more chunks, which run the odd chunks (launches passes*c .. passes*c +
- * passes - 1 of chunk c) on a second stream of their own with a second
- * workspace, forked from the
- * caller's stream when the execution starts and
- * joined back to it when it ends (so work enqueued on the caller's stream
- * afterwards sees the whole output).  On a capturing stream every chunk runs
- * on the captured stream.  No counterpart in the reference (one stream per
- * call, crates/ferrum-gpu-py/src/lib.rs:142-233). */
+ * passes - 1 of chunk c) with a second workspace on the device's chunk
+ * stream (one per device, shared by every two-stream plan on it), forked
+ * from the caller's stream when the execution starts and joined back to it
+ * when it ends (so work enqueued on the caller's stream afterwards sees the
+ * whole output).  On a capturing stream every chunk runs on the captured
+ * stream.  The overlap of the two chunks needs the chunk stream on a
+ * hardware queue of its own (HIP gives a process GPU_MAX_HW_QUEUES = 4 by
+ * default).  No counterpart in the reference (one stream per call,
+ * crates/ferrum-gpu-py/src/lib.rs:142-233). */
 FG_API int fg_fft_plan_streams(fg_fft_plan_t plan, int *streams);
+/* Runs a plan's chunks on one stream (streams = 1) or, for a plan that
+ * fg_fft_plan_streams reported at 2 when it was created, on two again
+ * (streams = 2; FG_ERR_INVALID_ARGUMENT for other plans or values).  Same
+ * results bit for bit either way; no execution of the plan may be in flight
+ * while it changes.  For callers whose own streams already occupy the
+ * hardware queues, and for timing each pass on its own.  No counterpart in
+ * the reference. */
+FG_API int fg_fft_plan_set_streams(fg_fft_plan_t plan, int streams);
 /* Kernel name of launch `index` of an execution out of place (d_in != d_out).
  * 2D plans of 2048 or 4096 rows of 1024 .. 4096 columns run other kernels in
  * place (fg_fft_n<log_cols> rows, then column tiles of all the rows), as many
- * launches. */
+ * launches: fg_fft_plan_kernel_in_place names those.  The two forms agree to
+ * rounding, not bit for bit.  A plan's launches are passes * chunks; a batch
+ * beyond one launch's 2^32 - 1 work-items (single-pass plans too) runs in
+ * several chunks rather than being refused or truncated. */
 FG_API int fg_fft_plan_kernel(fg_fft_plan_t plan, int index, char *name, size_t cap);
+FG_API int fg_fft_plan_kernel_in_place(fg_fft_plan_t plan, int index, char *name, size_t cap);
 /* Number of kernel launches per execution and the name of the kernel that
  * moves the most bytes (what the bench times and profiles). */
 FG_API int fg_fft_plan_describe(fg_fft_plan_t plan, int *launches, char *main_kernel, size_t cap,
@@ -274,7 +288,10 @@ FG_API int fg_transpose_c64(fg_device_t dev, const void *d_in, void *d_out, uint
  * (the reference's fft_c2c_{256_r16s,1024,4096_4step_reg}_split kernels,
  * crates/ferrum-gpu-fft-kernels/src/kernels_body.rs:509-626, 986-1130,
  * 1463-1610, for every plan).  Same results as fg_fft_exec on the interleaved
- * data.  Each array 4-byte aligned (FG_ERR_INVALID_ARGUMENT otherwise);
+ * data; multi-launch plans run that execution in place on their staging
+ * buffer, so for 2D plans of 2048 / 4096 rows of 1024 .. 4096 columns (whose
+ * in-place execution differs, fg_fft_plan_kernel_in_place) the results equal
+ * an in-place fg_fft_exec bit for bit and an out-of-place one to rounding.  Each array 4-byte aligned (FG_ERR_INVALID_ARGUMENT otherwise);
  * d_out_re / d_out_im may equal d_in_re / d_in_im; no other overlap.
  * Single-pass plans (1D, N <= 32768; 2D images of up to 16384 points) run one
  * launch; other plans stage through an interleaved buffer the plan allocates
@@ -295,10 +312,16 @@ FG_API int fg_fft_exec_split(fg_fft_plan_t plan, const void *d_in_re, const void
  * allocated buffer; a plan whose batch needs more staging (8 bytes per
  * element of batch * elements) is refused with FG_ERR_INVALID_ARGUMENT.
  * Single-pass plans need no staging and run as fg_fft_exec_split does.
- * Same results as fg_fft_exec_split, bit for bit.  All callers on one GPU
- * share its scratch area, which keeps the last call's contents: calls that
- * overlap in time on one GPU (different streams, threads or plans) race;
- * calls ordered on one stream do not.  Stream-ordered, asynchronous. */
+ * Same results as fg_fft_exec_split, bit for bit (so, for the 2D plans named
+ * there, the in-place interleaved execution's bits).  All callers on one GPU
+ * share its scratch area, which keeps the last call's contents.  Outside
+ * stream capture, calls that stage through it run one after another on the
+ * GPU in the order they were made (each waits, on its stream, for an event
+ * the previous one recorded after its last launch; the event is created at
+ * fg_device_open), whatever streams or threads make them.  Captured calls
+ * cannot wait for work outside their capture: graphs replayed so that they
+ * overlap in time each other or other calls on one GPU race.
+ * Stream-ordered, asynchronous. */
 FG_API int fg_fft_exec_split_noalloc(fg_fft_plan_t plan, const void *d_in_re, const void *d_in_im,
                                      void *d_out_re, void *d_out_im, int direction, int normalize,
                                      fg_stream_t stream);

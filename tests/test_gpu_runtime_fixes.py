@@ -140,3 +140,87 @@ def test_first_split_call_refused_under_capture(gpu_device, dims, log_n, batch):
     graph.destroy()
     plan.destroy()
     small.destroy()
+
+
+def test_batches_beyond_one_launch_run_in_chunks(gpu_device):
+    # A single-pass plan whose batch exceeds one launch's 2^32 - 1 work-items
+    # runs as several launches (never a truncated grid): N = 4 at 2^32
+    # transforms is 64 work-items per 64 transforms, so 2^32 - 64 transforms
+    # per launch and two launches.  Created, described, never executed here.
+    import ferrum_gpu
+
+    print("[case] Plan1D(2, 2**32) and Plan1D(2, 2**32 - 64): chunking only", flush=True)
+    p = ferrum_gpu.fft.Plan1D(2, 2**32, gpu_device)
+    d = p.describe()
+    assert d["launches"] == 2 and d["chunks"] == 2 and d["units_per_chunk"] == 2**32 - 64
+    assert p.kernel_names() == ["fg_fft_n2", "fg_fft_n2"]
+    p.destroy()
+    q = ferrum_gpu.fft.Plan1D(2, 2**32 - 64, gpu_device)
+    assert q.describe()["launches"] == 1
+    q.destroy()
+
+
+def test_in_place_kernel_names(gpu_device):
+    # 4096 x 4096 (config 5): out of place the row pairs and 2048-row column
+    # tiles, in place the 4096-point rows and 4096-row column tiles, as many
+    # launches; every other plan names the same kernels both ways
+    import ferrum_gpu
+
+    p = ferrum_gpu.fft.Plan2D(12, 2, gpu_device)
+    assert p.kernel_names() == ["fg_fft2d_rowpair_n12", "fg_tile_l11_g8_h_cc"]
+    assert p.kernel_names(in_place=True) == ["fg_fft_n12_sc", "fg_tile_l12_g8_h_cc"]
+    p.destroy()
+    for plan in (ferrum_gpu.fft.Plan1D(24, 4, gpu_device), ferrum_gpu.fft.Plan2D(10, 4, gpu_device),
+                 ferrum_gpu.fft.Plan1D(10, 4096, gpu_device)):
+        assert plan.kernel_names(in_place=True) == plan.kernel_names()
+        plan.destroy()
+
+
+def test_batch_beyond_one_launch_executes_in_chunks(gpu_device):
+    # 2^32 transforms of N = 4 (128 GiB, in place): two launches, the second
+    # of 64 transforms at byte offset 32 * (2^32 - 64).  The transforms on
+    # both sides of the launch boundary, and the first and last, equal the
+    # same plan kernel on a small batch bit for bit and the oracle to 1e-6.
+    import ferrum_gpu
+    from ferrum_gpu import _native as N
+    from ferrum_gpu import synthetic
+    from ferrum_gpu.hip import DeviceBuffer
+
+    if gpu_device.info()["total_mem"] < (200 << 30):
+        pytest.skip("needs a GPU with 200 GiB or more")
+    batch = 2**32
+    n = 4 * batch
+    print("[case] Plan1D(2, 2**32) in place over 128 GiB, two launches", flush=True)
+    try:
+        buf = DeviceBuffer(gpu_device, 8 * n)
+    except N.FerrumGpuError as e:
+        pytest.skip(f"128 GiB not available: {e}")
+    try:
+        synthetic.uniform(gpu_device, buf, n, 77)
+        gpu_device.sync()
+        lanes = [0, 1, 2**32 - 66, 2**32 - 65, 2**32 - 64, 2**32 - 63, 2**32 - 2, 2**32 - 1]
+
+        def read(lane):
+            h = np.empty(4, np.complex64)
+            N.check(N.lib.fg_copy_d2h(gpu_device.handle, h.ctypes.data, buf.ptr + 32 * lane, 32))
+            return h
+
+        x = np.concatenate([read(lane) for lane in lanes])
+        plan = ferrum_gpu.fft.Plan1D(2, batch, gpu_device)
+        assert plan.describe()["launches"] == 2
+        plan.execute(buf, buf, "forward", False)
+        gpu_device.sync()
+        got = np.concatenate([read(lane) for lane in lanes])
+        plan.destroy()
+    finally:
+        buf.free()
+    small = ferrum_gpu.fft.Plan1D(2, len(lanes), gpu_device)
+    a, b = DeviceBuffer(gpu_device, small.nbytes), DeviceBuffer(gpu_device, small.nbytes)
+    a.copy_from_host(x)
+    small.execute(a, b, "forward", False)
+    gpu_device.sync()
+    want = np.empty_like(x)
+    b.copy_to_host(want)
+    small.destroy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert rel_l2(got, oracle.fft_1d(x, 2)) <= 1e-6

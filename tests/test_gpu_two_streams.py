@@ -270,3 +270,47 @@ def test_2d_plans_run_one_stream_in_every_chunking(gpu_device, chunk_limit, lr, 
     assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
     assert rel_l2(outs[0][0], oracle_2d_rect(x, lr, lc)) <= TOL
     assert rel_l2(outs[0][1], x) <= TOL
+
+
+def test_set_streams_one_and_back_same_bits(gpu_device, chunk_limit):
+    # set_streams(1) runs the two-stream plan's chunks on the caller's stream
+    # alone (the bench's per-pass figures), set_streams(2) restores the
+    # overlap; the output is the same bits every way, and the chunk stream is
+    # one per device, shared by every two-stream plan
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer
+
+    log_n, batch = 20, 4
+    n = 1 << log_n
+    chunk_limit(2 * n * 8)
+    x = normal_c64(np.random.default_rng(91), batch * n)
+    print("[case] set_streams 2 -> 1 -> 2, log_n=20 batch=4", flush=True)
+    plan = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
+    other = ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device)
+    assert plan.describe()["streams"] == 2 and other.describe()["streams"] == 2
+    a, b = DeviceBuffer(gpu_device, plan.nbytes), DeviceBuffer(gpu_device, plan.nbytes)
+    a.copy_from_host(x)
+    outs = []
+    for streams, p in ((2, plan), (1, plan), (2, plan), (2, other)):
+        p.set_streams(streams)
+        assert p.describe()["streams"] == streams
+        for direction, normalize in (("forward", False), ("inverse", True)):
+            p.execute(a, b, direction, normalize)
+            gpu_device.sync()
+            o = np.empty_like(x)
+            b.copy_to_host(o)
+            outs.append(o)
+    for i, o in enumerate(outs):   # forward, inverse, forward, inverse, ...
+        assert np.array_equal(o.view(np.uint32), outs[i % 2].view(np.uint32)), i
+    assert _lanes(outs[0], x, log_n, batch) <= TOL
+    # one-stream plans refuse a second stream; bad values are refused
+    single = ferrum_gpu.fft.Plan1D(10, 64, gpu_device)
+    with pytest.raises(Exception):
+        single.set_streams(2)
+    with pytest.raises(Exception):
+        plan.set_streams(3)
+    single.set_streams(1)
+    for p in (plan, other, single):
+        p.destroy()
+    a.free()
+    b.free()

@@ -140,3 +140,66 @@ def test_noalloc_call_captured_on_a_fresh_plan(gpu_device):
     graph.destroy()
     plan.destroy()
     eager_plan.destroy()
+
+
+def test_noalloc_two_stream_plan(gpu_device):
+    # a multi-pass plan with two chunks in flight (chunk limit lowered to
+    # 16 MiB: 8 MiB chunks, describe()["streams"] == 2) staged through the
+    # scratch area: its odd chunks run on the device's chunk stream, the
+    # join brings them back before the deinterleave
+    import ferrum_gpu
+    from ferrum_gpu import _native as N
+
+    saved = ferrum_gpu.fft.get_chunk_bytes()
+    ferrum_gpu.fft.set_chunk_bytes(16 << 20)
+    try:
+        log_n, batch = 20, 8
+        plan = _plan(gpu_device, 1, log_n, batch)
+    finally:
+        ferrum_gpu.fft.set_chunk_bytes(saved)
+    d = plan.describe()
+    print(f"[case] noalloc two-stream plan {d}", flush=True)
+    assert d["streams"] == 2 and d["chunks"] == 8
+    n = batch << log_n
+    x = normal_c64(np.random.default_rng(8), n)
+    ins, outs = _parts(gpu_device, x)
+    for direction, normalize in (("forward", False), ("inverse", True)):
+        N.check(_call(N.lib.fg_fft_exec_split_noalloc, plan, ins, outs, direction, normalize))
+        got = _read(gpu_device, outs, n)
+        outs2 = _parts(gpu_device, x)[1]
+        N.check(_call(N.lib.fg_fft_exec_split, plan, ins, outs2, direction, normalize))
+        assert np.array_equal(got.view(np.uint32), _read(gpu_device, outs2, n).view(np.uint32))
+        assert rel_l2(got, oracle.fft_1d(x, log_n, direction, normalize, threads=8)) <= TOL
+    plan.destroy()
+
+
+def test_noalloc_calls_on_two_streams_take_turns(gpu_device):
+    # two staging calls made back to back on two streams, no host
+    # synchronisation between them: the second waits on its stream for the
+    # first's last launch, so neither overwrites the other's staged data
+    from ferrum_gpu import _native as N
+    from ferrum_gpu.hip import Stream
+
+    shapes = [(1, 20, 8), (1, 17, 16)]
+    plans, data = [], []
+    for i, (dims, log_n, batch) in enumerate(shapes):
+        n = batch << log_n
+        x = normal_c64(np.random.default_rng(60 + i), n)
+        plans.append(_plan(gpu_device, dims, log_n, batch))
+        data.append((x, n, log_n) + _parts(gpu_device, x))
+    streams = [Stream(gpu_device), Stream(gpu_device)]
+    print("[case] noalloc calls on two streams", flush=True)
+    for rep in range(3):
+        for (x, n, log_n, ins, outs), plan, s in zip(data, plans, streams):
+            N.check(_call(N.lib.fg_fft_exec_split_noalloc, plan, ins, outs, "forward", False, s.handle))
+        for s in streams:
+            s.sync()
+        for (x, n, log_n, ins, outs), plan in zip(data, plans):
+            got = _read(gpu_device, outs, n)
+            ref2 = _parts(gpu_device, x)[1]
+            N.check(_call(N.lib.fg_fft_exec_split, plan, ins, ref2, "forward", False))
+            assert np.array_equal(got.view(np.uint32), _read(gpu_device, ref2, n).view(np.uint32)), rep
+    for s in streams:
+        s.destroy()
+    for p in plans:
+        p.destroy()
