@@ -22,6 +22,13 @@ before the first), which gives each kernel's duration for the roofline.  With
 --graph G the steps are recorded G at a time into a HIP graph and the timed
 steps run as K / G replays (for the launch-bound configurations 1 and 2).
 
+With the default workload the same run then times the other BASELINE
+configurations (cfg1, cfg2_256, cfg2_4096, cfg4, cfg5) the way the reference's
+bench does (10 warmup and 100 timed steps, the median step;
+crates/ferrum-gpu-bench/src/lib.rs:31-37,148-213) and reports them under
+`configs` in the same line: per-step and per-pass times, physical bytes for the
+multi-pass plans, and the relative L2 error against the CPU oracle.
+
 Prints ONE JSON line on stdout (progress goes to stderr):
   value        = algorithmic bytes per step / wall time per step, GB/s (FFT:
                  16 * elems * batch per transform executed)
@@ -265,9 +272,18 @@ class FftWorkload:
         # Two-stream plans run the odd chunks on the plan's second stream:
         # launch i of an execution (chunk i // passes) stamps its event there.
         self.streams = 1 if layout == "split" else self.describe["streams"]
+        self._passes = passes
         L = len(kernels)
         self.launch_streams = [(i // passes) % 2 if self.streams == 2 else 0 for _ in steps for i in range(L)]
         self.exec_bounds = [(j * L, (j + 1) * L) for j in range(len(steps))]
+
+    def set_streams(self, n):
+        """Runs the plan's chunks on n streams (the plan's set_streams) and
+        keeps the per-launch stream map of launch_durations in step."""
+        self.plan.set_streams(n)
+        self.streams = n
+        L = len(self.kernels)
+        self.launch_streams = [(i // self._passes) % 2 if n == 2 else 0 for _ in self.steps for i in range(L)]
 
     def bind_events(self, events):
         """The per-step form run() takes of one step's launch events (built
@@ -293,6 +309,25 @@ class FftWorkload:
             else:
                 self.plan.execute_recording(self.bufs[j], self.bufs[j + 1], events[j], direction, normalize,
                                             stream)
+
+    def step_outputs(self):
+        """The output of every step of the chain (interleaved layout)."""
+        outs = []
+        for buf in self.bufs[1:]:
+            out = self.np.empty_like(self.x)
+            buf.copy_to_host(out)
+            outs.append(out)
+        return outs
+
+    def free(self):
+        """Release the device buffers and the plan (the bench's other
+        configurations run in the same process)."""
+        for b in getattr(self, "bufs", []):
+            b.free()
+        for pair in getattr(self, "parts", []):
+            for b in pair:
+                b.free()
+        self.plan.destroy()
 
     def output(self):
         np = self.np
@@ -328,8 +363,10 @@ class FftWorkload:
             return out.reshape(-1)
 
         y = self.x
+        self.cpu_outputs = []
         for direction, normalize in self.steps:
             y = run(y, direction, normalize)
+            self.cpu_outputs.append(y)
         return y
 
     def config(self):
@@ -621,6 +658,216 @@ def steady_state(np, per_kernel, dominant_key: str, graph: bool):
             "pre_ramp": bool(ratio is not None and ratio > 1.02)}
 
 
+# The BASELINE configurations the default run reports beside config 3, and
+# the reference bench's method for them: 10 warmup launches, then 100 timed
+# ones, the median reported (crates/ferrum-gpu-bench/src/lib.rs:31-37,148-213).
+EXTRA_CONFIGS = ["cfg1", "cfg2_256", "cfg2_4096", "cfg4", "cfg5"]
+CONFIG_STEPS, CONFIG_WARMUP = 100, 10
+GRAPH_STEPS_PER_REPLAY = 20
+
+
+def timed_steps(dev, wl, stream, steps: int, warmup: int, clocks=None) -> dict:
+    """`warmup` untimed steps, then `steps` timed ones back to back with an
+    event stamped by every launch (plus one before the first).  Returns the
+    host wall time, each launch key's durations (launch_durations) and each
+    step's GPU time (from the end of the previous step's last launch to the
+    end of its own)."""
+    from ferrum_gpu.hip import Event
+
+    for _ in range(warmup):
+        wl.run(stream)
+    dev.sync()
+    launches = len(wl.launch_names)
+    start = Event(dev)
+    evs = [[Event(dev) for _ in range(launches)] for _ in range(steps)]
+    bound = [wl.bind_events(e) for e in evs]
+    dev.sync()
+    ctx = clocks if clocks is not None else _NullContext()
+    with ctx:
+        t0 = time.perf_counter()
+        start.record(stream)
+        for k in range(steps):
+            wl.run(stream, bound[k])
+        dev.sync()
+        wall = time.perf_counter() - t0
+    per_kernel = launch_durations(start, evs, wl)
+    ends = [max(start.elapsed_ms(e) for e in row) for row in evs]
+    step_ms = [ends[0]] + [ends[k] - ends[k - 1] for k in range(1, steps)]
+    return {"wall_s": wall, "per_kernel": per_kernel, "step_ms": step_ms, "gpu_ms": ends[-1]}
+
+
+class _NullContext:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+
+def graph_step_ms(dev, wl, stream, steps: int, warmup: int, per_graph: int) -> float:
+    """GPU time per step with `per_graph` steps recorded into one HIP graph and
+    replayed steps / per_graph times between two events (the launch-bound
+    configurations' figure without the host's per-launch cost)."""
+    from ferrum_gpu.hip import Capture, Event
+
+    with Capture(dev, keep=[wl]) as cap:
+        for _ in range(per_graph):
+            wl.run(cap.stream)
+    graph = cap.graph
+    for _ in range(-(-warmup // per_graph)):
+        graph.launch(stream)
+    dev.sync()
+    start, end = Event(dev), Event(dev)
+    reps = max(1, steps // per_graph)
+    start.record(stream)
+    for _ in range(reps):
+        graph.launch(stream)
+    end.record(stream)
+    dev.sync()
+    ms = start.elapsed_ms(end) / (reps * per_graph)
+    graph.destroy()
+    return ms
+
+
+def pass_table(np, wl, per_kernel: dict) -> list:
+    """Each pass of the plan (launch key "i:kernel"): its launches' mean and
+    median duration and the algorithmic bytes one launch moves over them."""
+    rows = []
+    for key in sorted(per_kernel, key=lambda k: int(k.split(":", 1)[0])):
+        v = per_kernel[key]
+        avg, med = float(np.mean(v)), float(np.median(v))
+        gbs = wl.bytes_per_launch / (avg * 1e-3) / 1e9
+        rows.append({"pass": int(key.split(":", 1)[0]), "kernel": key.split(":", 1)[1], "launches": len(v),
+                     "avg_ms": round(avg, 5), "median_ms": round(med, 5), "bytes_per_launch": wl.bytes_per_launch,
+                     "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    return rows
+
+
+def fp64_spot_check(np, wl, outs) -> float:
+    """Relative L2 error of sampled bins of the first step's output (forward)
+    against a direct DFT in fp64 (the reference's dft_naive_interleaved,
+    layout_study.rs:5-21): 1D, bins of the first and last transform (16 up
+    to 32768 points, 4 beyond: each bin costs O(N)); 2D, 8 bins (k1, k2) of
+    the first and last image by a separable fp64 DFT."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import oracle  # test infrastructure: the checker only
+
+    x, got = wl.x, outs[0]
+    n, b = wl.elems, wl.batch
+    rng = np.random.default_rng(wl.log_n)
+    errs, refs = [], []
+    for lane in sorted({0, b - 1}):
+        xs, gs = x[lane * n:(lane + 1) * n], got[lane * n:(lane + 1) * n]
+        if wl.dims == 1:
+            # O(N) per bin with a cos and sin per term: 16 bins up to 32768
+            # points, 4 beyond, one bin per thread (the C call drops the GIL)
+            extra = 12 if n <= (1 << 15) else 1
+            bins = np.unique(np.concatenate([[0, 1, n // 2, n - 1][:4 if extra > 1 else 3],
+                                             rng.integers(0, n, extra)]))
+            with ThreadPoolExecutor(max_workers=max(1, min(16, host_cores()))) as ex:
+                exact = np.concatenate(list(ex.map(lambda k: oracle.dft_bins_f64(xs, [k]), bins.tolist())))
+            sample = gs[bins]
+        else:
+            side = 1 << wl.log_n
+            img = xs.reshape(side, side).astype(np.complex128)
+            ks = rng.integers(0, side, (8, 2))
+            ks[0] = (0, 0)
+            idx = np.arange(side)
+            exact = np.array([np.exp(-2j * np.pi * k1 * idx / side) @ (img @ np.exp(-2j * np.pi * k2 * idx / side))
+                              for k1, k2 in ks])
+            sample = gs.reshape(side, side)[ks[:, 0], ks[:, 1]]
+        errs.append(sample.astype(np.complex128) - exact)
+        refs.append(exact)
+    e, r = np.concatenate(errs), np.concatenate(refs)
+    return float(np.linalg.norm(e) / np.linalg.norm(r))
+
+
+def config_record(np, N, dev, stream, name: str, steps: int, warmup: int, ramp_ms: float) -> tuple:
+    """Times one BASELINE configuration on the GPU and returns (record, workload,
+    outputs); the CPU checks are added by check_config afterwards."""
+    wl = FftWorkload(name, np, dev)
+    log(f"config {name}: {wl.desc}")
+    clock_ramp(N, dev, wl, stream, ramp_ms)
+    run = timed_steps(dev, wl, stream, steps, warmup)
+    step_ms = run["step_ms"]
+    med, mean = float(np.median(step_ms)), run["gpu_ms"] / steps
+    d = wl.describe
+    passes = pass_table(np, wl, run["per_kernel"])
+    rec = {
+        "workload": wl.desc,
+        "kernels": wl.kernels,
+        "plan": {k: d[k] for k in ("launches", "passes", "chunks", "units_per_chunk", "streams", "cache_resident")},
+        "steps": steps, "warmup": warmup,
+        "ms_per_step": round(med, 5),
+        "ms_per_step_mean": round(mean, 5),
+        "value": round(wl.algo_bytes / (med * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "pct_hbm_peak": round(100.0 * wl.algo_bytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+        "gflops": round(wl.flops / (med * 1e-3) / 1e9, 2),
+        "algorithmic_bytes_per_step": wl.algo_bytes,
+        "passes": passes,
+        "timing": "GPU events stamped by every launch, steps back to back; ms_per_step is the median step "
+                  "(the reference bench's statistic), value = algorithmic bytes / that median",
+    }
+    if d["passes"] > 1:
+        phys = d["passes"] * wl.algo_bytes
+        rec["physical_bytes_per_step"] = phys
+        rec["physical_gbs"] = round(phys / (med * 1e-3) / 1e9, 1)
+        rec["physical_pct_hbm_peak"] = round(100.0 * phys / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
+        rec["physical_note"] = ("each pass reads and writes every element once: passes x 16 bytes x elements per "
+                                "step; intermediate passes are served partly by the Infinity Cache")
+    if d["streams"] == 2:
+        rec["passes_note"] = ("two chunks in flight on two streams: each launch's duration is its time while "
+                              "sharing the GPU with the other stream's launch; passes_one_stream times the same "
+                              "plan with its chunks on one stream (each pass alone on the GPU)")
+        wl.set_streams(1)
+        try:
+            one = timed_steps(dev, wl, stream, steps, warmup)
+        finally:
+            wl.set_streams(2)
+        rec["passes_one_stream"] = pass_table(np, wl, one["per_kernel"])
+        rec["ms_per_step_one_stream"] = round(float(np.median(one["step_ms"])), 5)
+    if wl.batch * wl.elems <= (1 << 22):
+        # launch-bound sizes: the same steps as graph replays (no host cost per launch)
+        g = graph_step_ms(dev, wl, stream, steps, warmup, GRAPH_STEPS_PER_REPLAY)
+        rec["graph_ms_per_step"] = round(g, 5)
+        rec["graph_value"] = round(wl.algo_bytes / (g * 1e-3) / 1e9, 2)
+    wl.run(stream)
+    dev.sync()
+    outs = wl.step_outputs()
+    wl.free()
+    return rec, wl, outs
+
+
+def check_config(np, rec: dict, wl, outs) -> None:
+    """Adds the CPU oracle's verdict to a config record: relative L2 error of
+    every step's output against the oracle's (computed outside the timed
+    region), the round trip for forward + inverse chains, the fp64 spot
+    check, and the oracle's own time on this host."""
+    threads = max(1, min(16, host_cores(), wl.batch))
+    t0 = time.perf_counter()
+    wl.cpu(threads)
+    secs = time.perf_counter() - t0
+    refs = wl.cpu_outputs
+
+    def rel(a, b):
+        a = a.astype(np.complex128)
+        b = b.astype(np.complex128)
+        return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+    rec["rel_l2_vs_cpu"] = max(rel(o, r) for o, r in zip(outs, refs))
+    rec["rel_l2_vs_cpu_per_step"] = [rel(o, r) for o, r in zip(outs, refs)]
+    if len(wl.steps) == 2:
+        rec["roundtrip_rel_l2"] = rel(outs[1], wl.x)
+    rec["fp64_bins_rel_l2"] = fp64_spot_check(np, wl, outs)
+    rec["cpu_oracle"] = {"seconds": round(secs, 4), "threads": threads,
+                         "gbs": round(wl.algo_bytes / secs / 1e9, 4),
+                         "note": "the C oracle (oracle/oracle.c -O3) on this host, one pass, as the checker"}
+    rec["parity_ok"] = bool(rec["rel_l2_vs_cpu"] <= 1e-4 and rec["fp64_bins_rel_l2"] <= 1e-4 and
+                            rec.get("roundtrip_rel_l2", 0.0) <= 1e-4)
+
+
 def gate_check(result, min_frac):
     """The throughput gate of --min-frac: None without one, else whether the
     dominant kernel's roofline fraction reached it."""
@@ -650,6 +897,14 @@ def main() -> int:
                     help="throughput gate: after printing the JSON line, exit with status 3 if the dominant "
                          "kernel's roofline fraction is below F (the reference's perf-gate, "
                          "crates/ferrum-gpu-bench/src/bin/perf-gate.rs, gates a ratio the same way)")
+    ap.add_argument("--configs", default="auto", metavar="LIST",
+                    help="comma-separated BASELINE configurations to time after the workload and report under "
+                         "`configs` (" + ",".join(EXTRA_CONFIGS) + "); 'auto' (default): all of them when the "
+                         "workload is cfg3, none otherwise; 'none': skip")
+    ap.add_argument("--config-steps", type=int, default=CONFIG_STEPS,
+                    help="timed steps per extra configuration (the reference bench: 100)")
+    ap.add_argument("--config-warmup", type=int, default=CONFIG_WARMUP,
+                    help="warmup steps per extra configuration (the reference bench: 10)")
     ap.add_argument("--graph", type=int, default=0, metavar="G",
                     help="record G steps into one HIP graph and time replays of it (for launch-bound "
                          "workloads); --steps must be a multiple of G.  0: one host launch per kernel")
@@ -664,6 +919,20 @@ def main() -> int:
         return 2
     if args.graph < 0 or (args.graph and args.steps % args.graph):
         print("bench.py: --graph G needs G >= 1 dividing --steps", file=sys.stderr)
+        return 2
+    if args.configs == "auto":
+        config_names = list(EXTRA_CONFIGS) if args.workload == "cfg3" else []
+    elif args.configs == "none":
+        config_names = []
+    else:
+        config_names = [c for c in args.configs.split(",") if c]
+        bad = [c for c in config_names if c not in EXTRA_CONFIGS]
+        if bad:
+            print(f"bench.py: --configs takes {','.join(EXTRA_CONFIGS)}, 'auto' or 'none'; got {bad}",
+                  file=sys.stderr)
+            return 2
+    if args.config_steps < 1 or args.config_warmup < 0:
+        print("bench.py: --config-steps must be >= 1 and --config-warmup >= 0", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -686,27 +955,12 @@ def main() -> int:
     if ramp:
         log(f"clock ramp: {ramp['copies']} copy launches in {ramp['ms']} ms")
     if not args.graph:
-        for _ in range(args.warmup):
-            wl.run(stream)
-        dev.sync()
-        log(f"warmup {args.warmup} done")
-
-        # One event after every launch (plus one before the first): launch i ran
-        # between consecutive events.  One marker per launch costs ~2 us of gap per
-        # launch; a pair per launch measured ~6 us.
-        start = Event(dev)
-        evs = [[Event(dev) for _ in range(launches)] for _ in range(args.steps)]
-        bound = [wl.bind_events(e) for e in evs]
-        dev.sync()
-        with clocks:
-            t0 = time.perf_counter()
-            start.record(stream)
-            for k in range(args.steps):
-                wl.run(stream, bound[k])
-            dev.sync()
-            wall = time.perf_counter() - t0
-        log(f"timed {args.steps} steps in {wall * 1e3:.3f} ms")
-        per_kernel = launch_durations(start, evs, wl)
+        # One event stamped by every launch (plus one before the first): launch
+        # i ran between consecutive events of its stream.
+        run = timed_steps(dev, wl, stream, args.steps, args.warmup, clocks)
+        wall = run["wall_s"]
+        log(f"warmup {args.warmup} done; timed {args.steps} steps in {wall * 1e3:.3f} ms")
+        per_kernel = run["per_kernel"]
     else:
         # G steps per graph, replayed steps / G times between two events: the
         # GPU time per launch is the replay time over all the launches in it
@@ -763,6 +1017,14 @@ def main() -> int:
     dev.sync()
     out = wl.output()
 
+    # The other BASELINE configurations, timed on the GPU one after another
+    # (their CPU checks come after the headline's CPU baseline below).
+    extra = []
+    for name in config_names:
+        extra.append((name,) + config_record(np, N, dev, stream, name, args.config_steps, args.config_warmup,
+                                             args.ramp_ms))
+        log(f"config {name}: {extra[-1][1]['ms_per_step']} ms per step (median of {args.config_steps})")
+
     host = None
     if not args.no_host_path and isinstance(wl, FftWorkload) and wl.layout == "interleaved":
         host = host_path_rate(np, wl, dev)
@@ -774,6 +1036,15 @@ def main() -> int:
         base, multi, err = cpu_baseline(np, wl, out, args.cpu_budget)
         log(f"cpu baseline {base['value']} GB/s (1 core), {multi['value']} GB/s ({multi['cores']} cores); "
             f"gpu-vs-cpu {'max abs diff' if wl.exact else 'rel_l2'} {err:.3e}")
+
+    configs = None
+    if extra:
+        configs = {}
+        for name, rec, cwl, outs in extra:
+            check_config(np, rec, cwl, outs)
+            log(f"config {name}: rel_l2 {rec['rel_l2_vs_cpu']:.3e}, fp64 bins {rec['fp64_bins_rel_l2']:.3e}")
+            configs[name] = rec
+        del extra
 
     config = {"workload": wl.desc, "name": args.workload}
     config.update(wl.config())
@@ -817,6 +1088,8 @@ def main() -> int:
         "clock_ramp": ramp,
         "steady_state": steady,
     }
+    if configs is not None:
+        result["configs"] = configs
     if args.graph:
         result["launch_mode"] = f"HIP graph of {args.graph} steps per replay"
     else:

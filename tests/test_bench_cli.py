@@ -7,6 +7,7 @@ import os
 import subprocess
 import sys
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -23,7 +24,9 @@ def test_more_than_one_gpu_is_refused_with_a_message():
     assert "one GPU" in r.stderr and r.stdout == ""
 
 
-@pytest.mark.parametrize("args", [["--steps", "0"], ["--warmup", "-1"], ["--graph", "3", "--steps", "10"]])
+@pytest.mark.parametrize("args", [["--steps", "0"], ["--warmup", "-1"], ["--graph", "3", "--steps", "10"],
+                                  ["--configs", "cfg3"], ["--configs", "cfg1,bogus"], ["--config-steps", "0"],
+                                  ["--config-warmup", "-1"]])
 def test_bad_arguments_are_refused(args):
     r = run_bench(*args)
     assert r.returncode == 2 and r.stdout == ""
@@ -130,3 +133,101 @@ def test_launch_durations_two_executions_per_step():
     evs = [[_Ev(2), _Ev(5)], [_Ev(6), _Ev(9)]]
     got = bench.launch_durations(_Ev(0), evs, wl)
     assert got == {"0:f": [2, 1], "0:i": [3, 3]}
+
+
+def test_extra_configs_are_the_other_baseline_configs():
+    # the default run reports configs 1, 2, 4 and 5 beside config 3, timed as
+    # the reference bench times (10 warmup, 100 timed, the median step)
+    import bench
+
+    assert bench.EXTRA_CONFIGS == ["cfg1", "cfg2_256", "cfg2_4096", "cfg4", "cfg5"]
+    assert (bench.CONFIG_STEPS, bench.CONFIG_WARMUP) == (100, 10)
+
+
+class _FakeFft:
+    """The parts of bench.FftWorkload that pass_table / check_config read,
+    over a small forward + inverse chain computed with numpy in fp64 (the
+    'GPU output' here) and the real C oracle as the checker."""
+
+    def __init__(self, dims, log_n, batch, steps):
+        import numpy as np
+
+        rng = np.random.default_rng(7)
+        self.np = np
+        self.dims, self.log_n, self.batch, self.steps = dims, log_n, batch, steps
+        self.elems = (1 << log_n) if dims == 1 else 1 << (2 * log_n)
+        n = self.elems * batch
+        self.x = (rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)).astype(np.complex64)
+        self.algo_bytes = 16 * n * len(steps)
+        self.bytes_per_launch = 16 * n
+        self.real = bench_real(self)
+
+    def cpu(self, threads):
+        return self.real.cpu(threads)
+
+    @property
+    def cpu_outputs(self):
+        return self.real.cpu_outputs
+
+
+def bench_real(fake):
+    import bench
+
+    wl = bench.FftWorkload.__new__(bench.FftWorkload)
+    wl.np, wl.dims, wl.log_n, wl.batch, wl.steps, wl.x = fake.np, fake.dims, fake.log_n, fake.batch, fake.steps, fake.x
+    return wl
+
+
+def _numpy_chain(fake):
+    np = fake.np
+    shape = (fake.batch, 1 << fake.log_n) if fake.dims == 1 else (fake.batch, 1 << fake.log_n, 1 << fake.log_n)
+    y = fake.x.reshape(shape).astype(np.complex128)
+    outs = []
+    for direction, normalize in fake.steps:
+        f = np.fft.fft if fake.dims == 1 else np.fft.fft2
+        fi = np.fft.ifft if fake.dims == 1 else np.fft.ifft2
+        y = f(y) if direction == "forward" else (fi(y) if normalize else fi(y) * (y[0].size))
+        outs.append(y.reshape(-1).astype(np.complex64))
+    return outs
+
+
+@pytest.mark.parametrize("dims,log_n,batch,steps", [
+    (1, 8, 4, [("forward", False), ("inverse", True)]),
+    (1, 10, 3, [("forward", False)]),
+    (2, 5, 2, [("forward", False)]),
+])
+def test_check_config_keys_and_verdict(dims, log_n, batch, steps):
+    # the oracle's verdict on a config record: per-step rel-L2 against the C
+    # oracle, the round trip of forward + inverse chains, the fp64 bins, the
+    # oracle's own time; numpy's complex128 transform passes all of them
+    import bench
+
+    fake = _FakeFft(dims, log_n, batch, steps)
+    outs = _numpy_chain(fake)
+    rec = {}
+    bench.check_config(fake.np, rec, fake, outs)
+    assert rec["parity_ok"] is True
+    assert len(rec["rel_l2_vs_cpu_per_step"]) == len(steps)
+    assert 0 <= rec["rel_l2_vs_cpu"] <= 1e-5 and rec["fp64_bins_rel_l2"] <= 1e-5
+    assert ("roundtrip_rel_l2" in rec) == (len(steps) == 2)
+    assert set(rec["cpu_oracle"]) >= {"seconds", "threads", "gbs", "note"}
+    # a planted mistake (one bin conjugated in the first step's output) fails the verdict
+    bad = [o.copy() for o in outs]
+    bad[0][1] = np.conj(bad[0][1]) + 1.0
+    rec2 = {}
+    bench.check_config(fake.np, rec2, fake, bad)
+    assert rec2["rel_l2_vs_cpu"] > 1e-4 and rec2["parity_ok"] is False
+
+
+def test_pass_table_rates():
+    import bench
+
+    class W:
+        bytes_per_launch = 1 << 28
+
+    per = {"1:fg_tile_b": [0.05, 0.04, 0.06], "0:fg_tile_a": [0.04, 0.04]}
+    rows = bench.pass_table(np, W, per)
+    assert [r["pass"] for r in rows] == [0, 1] and [r["kernel"] for r in rows] == ["fg_tile_a", "fg_tile_b"]
+    assert rows[0]["avg_ms"] == 0.04 and rows[1]["median_ms"] == 0.05 and rows[1]["launches"] == 3
+    assert rows[0]["gbs"] == pytest.approx((1 << 28) / 0.04e-3 / 1e9, abs=0.051)
+    assert rows[0]["frac"] == pytest.approx(rows[0]["gbs"] / 8000.0, abs=1e-4)

@@ -31,12 +31,13 @@ OPS = ["cmul", "cmul_split", "deinterleave", "interleave", "transpose"]
 SMALL = {"cfg1", "cfg2_256", "cfg2_4096"}
 
 
-def run_bench(workload, *extra):
+def run_bench(workload, *extra, timeout=110):
     cpu = ["--cpu-budget", "0"] if workload in SMALL else ["--no-cpu"]
-    print(f"[case] bench.py --workload {workload} {' '.join(cpu + list(extra))}", flush=True)
+    configs = [] if "--configs" in extra else ["--configs", "none"]
+    print(f"[case] bench.py --workload {workload} {' '.join(cpu + configs + list(extra))}", flush=True)
     r = subprocess.run([sys.executable, BENCH, "--workload", workload, "--steps", "4", "--warmup", "2",
-                        "--no-host-path", "--ramp-ms", "5", *cpu, *extra],
-                       capture_output=True, text=True, timeout=110)
+                        "--no-host-path", "--ramp-ms", "5", *cpu, *configs, *extra],
+                       capture_output=True, text=True, timeout=timeout)
     assert r.returncode == 0, r.stderr[-2000:]
     lines = [ln for ln in r.stdout.splitlines() if ln.strip()]
     assert len(lines) == 1, r.stdout
@@ -73,3 +74,45 @@ def test_bench_line_keeps_the_contract(workload):
 def test_bench_graph_replay_line():
     d = run_bench("cfg1", "--graph", "2")
     assert d["value"] > 0 and "graph" in d["launch_mode"]
+
+
+def test_default_run_reports_every_baseline_config():
+    # the driver's default run (config 3) also times configs 1, 2, 4 and 5
+    # and reports them under `configs`: per-step and per-pass times, physical
+    # bytes of the multi-pass plans, and the oracle's verdict on each output
+    d = run_bench("cfg3", "--configs", "auto", "--config-steps", "6", "--config-warmup", "2", timeout=115)
+    cf = d["configs"]
+    assert sorted(cf) == ["cfg1", "cfg2_256", "cfg2_4096", "cfg4", "cfg5"]
+    for name, rec in cf.items():
+        assert rec["steps"] == 6 and rec["warmup"] == 2, name
+        assert rec["ms_per_step"] > 0 and rec["value"] > 0 and rec["gflops"] > 0, name
+        assert rec["pct_hbm_peak"] == pytest.approx(100 * rec["value"] / 8000.0, abs=0.01), name
+        assert rec["rel_l2_vs_cpu"] <= 1e-4 and rec["fp64_bins_rel_l2"] <= 1e-4 and rec["parity_ok"], name
+        assert rec["passes"] and all(p["avg_ms"] > 0 and p["median_ms"] > 0 for p in rec["passes"]), name
+        assert rec["cpu_oracle"]["seconds"] > 0, name
+    for name in ("cfg2_256", "cfg2_4096"):
+        assert len(cf[name]["rel_l2_vs_cpu_per_step"]) == 2 and cf[name]["roundtrip_rel_l2"] <= 1e-4
+    for name in ("cfg1", "cfg2_256", "cfg2_4096"):
+        assert cf[name]["graph_ms_per_step"] > 0
+    for name, passes in (("cfg4", 3), ("cfg5", 2)):
+        rec = cf[name]
+        assert rec["plan"]["passes"] == passes and len(rec["passes"]) == passes
+        assert rec["physical_bytes_per_step"] == passes * rec["algorithmic_bytes_per_step"]
+        assert rec["physical_gbs"] == pytest.approx(passes * rec["value"], rel=0.01)
+    assert cf["cfg4"]["plan"]["streams"] == 2
+    assert len(cf["cfg4"]["passes_one_stream"]) == 3 and cf["cfg4"]["ms_per_step_one_stream"] > 0
+
+
+def test_north_star_gate():
+    # the reference's perf gate (crates/ferrum-gpu-bench/src/bin/perf-gate.rs:
+    # 20,102-116) applied to the north-star target: config 3's kernel at 70 %
+    # of the 8 TB/s HBM peak or better, after a clock ramp and 200 warmup
+    # steps; bench.py exits 3 (and this test fails) below it
+    print("[case] bench.py --workload cfg3 --min-frac 0.70", flush=True)
+    r = subprocess.run([sys.executable, BENCH, "--workload", "cfg3", "--steps", "100", "--warmup", "200",
+                        "--no-host-path", "--no-cpu", "--configs", "none", "--min-frac", "0.70"],
+                       capture_output=True, text=True, timeout=110)
+    lines = [ln for ln in r.stdout.splitlines() if ln.strip()]
+    assert len(lines) == 1, r.stderr[-2000:]
+    gate = json.loads(lines[0])["gate"]
+    assert r.returncode == 0 and gate["passed"], gate
