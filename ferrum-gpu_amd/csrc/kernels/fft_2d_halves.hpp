@@ -193,6 +193,7 @@ __device__ __forceinline__ void fft2d_halves_body(const IO io, const float2* __r
     // f is uniform over the workgroup (the host launches batch of them, N/32
     // threads each); threads beyond N/32 in a larger block would only idle
     if (f >= batch || t >= H::T) return;
+    stagger_lockstep_start<(H::HALF + H::HALF / 16) * 8, H::T>();  // 16384-point images
     float2 x[H::E], y[H::E];
 #pragma unroll
     for (int m = 0; m < H::E; ++m) x[m] = io.load_row(f * H::N + H::T * m, t);

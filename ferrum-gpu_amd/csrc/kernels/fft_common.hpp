@@ -199,6 +199,40 @@ struct SplitIO {
     }
 };
 
+// Lock-step start of kernels that hold at most two workgroups per CU.
+// Every CU starts its first workgroups together, so with one or two per CU
+// all CUs load, transform and store in step, round after round: HBM idles
+// while every CU transforms, and the CUs wait together on memory.  Delaying
+// the first round's workgroups by 0, 1, ..., 15 us (by their per-XCD index:
+// workgroup b runs on XCD b % 8 as its (b / 8)-th) puts the CUs out of step
+// for the whole launch, since each CU's next workgroup starts when its
+// previous one ends.  Measured on gfx950 at 512 MiB per launch (us): 32768-
+// point transforms (one 1024-thread workgroup per CU) 265 -> 247, 16384-point
+// ones (two per CU) 199 -> 193, 128 x 128 images (two per CU) 217 -> 203;
+// kernels with four or more workgroups per CU lost (N = 1024: 169 -> 182,
+// N = 8192: 181 -> 185), as did the multi-pass tiles, whose chained launches
+// are out of step already.  Only grids of at least two full rounds wait, so a
+// batch that fills the GPU once or less runs without delay.  The wait is a
+// bounded poll of the 100 MHz constant clock (s_memrealtime) with s_sleep.
+constexpr unsigned kGpuCus = 256;          // MI355X: 8 XCDs x 32 CUs
+constexpr long long kStaggerTicks = 100;   // 1 us per phase at the 100 MHz wall clock
+constexpr unsigned kStaggerPhases = 16;
+
+template <int LDS_BYTES, int THREADS>
+__device__ __forceinline__ void stagger_lockstep_start() {
+    // workgroups per CU: the LDS (160 KB) and, at up to 128 VGPRs, 16 waves
+    constexpr int by_lds = 163840 / LDS_BYTES, by_waves = 1024 / THREADS;
+    constexpr int per_cu = by_lds < by_waves ? by_lds : by_waves;
+    if constexpr (per_cu >= 1 && per_cu <= 2) {
+        constexpr unsigned first = kGpuCus * per_cu;
+        if (gridDim.x >= 2 * first && blockIdx.x < first) {
+            const long long wait = kStaggerTicks * (long long)((blockIdx.x >> 3) % kStaggerPhases);
+            const long long t0 = wall_clock64();
+            while (wall_clock64() - t0 < wait) __builtin_amdgcn_s_sleep(4);
+        }
+    }
+}
+
 // Wave-scope ordering of LDS traffic: a wave's LDS operations execute in
 // program order, so a compiler-level barrier plus wavefront-scope fences is
 // enough between one wave's LDS writes and its own later reads.

@@ -447,6 +447,7 @@ __device__ __forceinline__ void fft_row_halves_body(const IO io, const float2* _
     const int t = threadIdx.x;
     const uint64_t f = blockIdx.x;
     if (f >= batch) return;  // uniform over the workgroup (the host launches batch of them)
+    stagger_lockstep_start<(H::HALF + H::HALF / 16) * 8, H::T>();  // 16384 / 32768 points
     float2 x[H::E], y[H::E];
 #pragma unroll
     for (int m = 0; m < H::E; ++m) x[m] = io.load_row(f * H::N + H::T * m, t);
