@@ -5,9 +5,10 @@ Default workload (the one the north-star target is quoted
 on): batched 1D forward C2C complex64 FFT, N = 1024, batch = 65536 (512 MiB in,
 512 MiB out), re/im iid N(0,1) from seed 3, device-resident buffers.
 `--workload` selects the other BASELINE configurations (cfg1, cfg2_256,
-cfg2_4096, cfg4, cfg5), 1D lengths 8192 / 16384 on the single-pass path (1d_8192,
-1d_16384: 512 MiB batches), 2D images on the one-pass path (2d_64, 2d_128: 512 MiB
-batches of 64x64 / 128x128 images) and the operations beside the path (cfg3_split: config 3
+cfg2_4096, cfg4, cfg5), 1D lengths 8192 .. 32768 on the single-pass path
+(1d_8192, 1d_16384, 1d_32768) and 2^16 / 2^18 / 2^20 on the two-pass path
+(1d_2p16, 1d_2p18, 1d_2p20), 2D images on the one-pass path (2d_64, 2d_128) and
+on the two-pass path (2d_512, 2d_1024), all 512 MiB batches and the operations beside the path (cfg3_split: config 3
 in the split layout; cmul, cmul_split, deinterleave, interleave: the pointwise
 kernels over config 3's 2^26 elements; transpose: an 8192 x 8192 complex64
 matrix).
@@ -75,6 +76,16 @@ FFT_WORKLOADS = {
                  "1D forward C2C FFT N=16384 batch=4096 complex64 (single pass), re/im iid N(0,1) seed 9"),
     "1d_32768": (1, 15, 2048, 10, "normal", [("forward", False)], "interleaved",
                  "1D forward C2C FFT N=32768 batch=2048 complex64 (single pass), re/im iid N(0,1) seed 10"),
+    "1d_2p16": (1, 16, 1024, 11, "normal", [("forward", False)], "interleaved",
+                "1D forward C2C FFT N=2^16 batch=1024 complex64 (two passes), re/im iid N(0,1) seed 11"),
+    "1d_2p18": (1, 18, 256, 12, "normal", [("forward", False)], "interleaved",
+                "1D forward C2C FFT N=2^18 batch=256 complex64 (two passes), re/im iid N(0,1) seed 12"),
+    "1d_2p20": (1, 20, 64, 13, "normal", [("forward", False)], "interleaved",
+                "1D forward C2C FFT N=2^20 batch=64 complex64 (two passes), re/im iid N(0,1) seed 13"),
+    "2d_512": (2, 9, 256, 14, "uniform", [("forward", False)], "interleaved",
+               "2D forward C2C FFT 512x512 batch=256 complex64 (two passes), re/im iid U[-1,1) seed 14"),
+    "2d_1024": (2, 10, 64, 15, "uniform", [("forward", False)], "interleaved",
+                "2D forward C2C FFT 1024x1024 batch=64 complex64 (two passes), re/im iid U[-1,1) seed 15"),
     "2d_64": (2, 6, 16384, 6, "uniform", [("forward", False)], "interleaved",
               "2D forward C2C FFT 64x64 batch=16384 complex64 (one-pass path), re/im iid U[-1,1) seed 6"),
     "2d_128": (2, 7, 4096, 7, "uniform", [("forward", False)], "interleaved",
@@ -90,6 +101,14 @@ OP_WORKLOADS = {
     "deinterleave": (1 << 26, "interleaved complex64 -> (re, im) f32 arrays, 2^26 elements, N(0,1) seed 3"),
     "interleave": (1 << 26, "(re, im) f32 arrays -> interleaved complex64, 2^26 elements, N(0,1) seed 3"),
     "transpose": (1 << 26, "out-of-place transpose of an 8192x8192 complex64 matrix, N(0,1) seed 3"),
+    # Shape copies (fg_copy_shape_*): out = in with an FFT kernel's access
+    # shape, workgroup size and LDS, no arithmetic -- that kernel's
+    # memory-only floor on the same bytes.
+    "shape_n10": (1 << 26, "copy with fg_fft_n10's access shape (config 3: 65536 x 1024 complex64), N(0,1) seed 3"),
+    "shape_n14": (1 << 26, "copy with fg_fft_n14's access shape (4096 x 16384 complex64), N(0,1) seed 3"),
+    "shape_n15": (1 << 26, "copy with fg_fft_n15's access shape (2048 x 32768 complex64), N(0,1) seed 3"),
+    "shape_cfg5col": (1 << 25, "in-place copy with config 5's column pass geometry (fg_tile_l11_g8_h_cc over two "
+                               "4096x4096 images: 2048-row tiles of 8 columns per row parity), U[-1,1) seed 5"),
 }
 WORKLOADS = sorted(FFT_WORKLOADS) + sorted(OP_WORKLOADS)
 
@@ -379,8 +398,37 @@ class FftWorkload:
         return f"full workload ({self.batch} transforms x {len(self.steps)} direction(s))"
 
 
+class TileGeomC:
+    """ctypes mirror of TileGeom (ferrum-gpu_amd/csrc/kernels/tile_geom.h)."""
+
+    @staticmethod
+    def make(**kw):
+        import ctypes
+
+        class TileGeom(ctypes.Structure):
+            _fields_ = ([(n, ctypes.c_uint64) for n in ("is0", "is1", "is2", "os0", "os1", "os2", "ics", "ies",
+                                                        "ocs", "oes")] +
+                        [(n, ctypes.c_uint32) for n in ("t0n", "t1n", "twc", "tw0", "tw1", "log_m", "flags")] +
+                        [("scale", ctypes.c_float), ("remap", ctypes.c_uint32)])
+
+        g = TileGeom()
+        g.scale = 1.0
+        for k, v in kw.items():
+            setattr(g, k, v)
+        return g
+
+
+def cfg5_column_geom(log_n: int):
+    """The geometry of the column pass of a 2D plan of 2^log_n x 2^log_n
+    images after the row pairs (FftPlan::make_2d): tiles of 8 columns over
+    the rows of each parity (element stride 2C), in place, line-group order."""
+    C = 1 << log_n
+    return TileGeomC.make(t0n=C // 8, t1n=2, is0=8, os0=8, is1=C, os1=C, is2=C * C, os2=C * C, ics=1, ocs=1,
+                          ies=2 * C, oes=2 * C, remap=2)
+
+
 class OpWorkload:
-    """One launch per step of a pointwise kernel or the transpose."""
+    """One launch per step of a pointwise kernel, the transpose or a shape copy."""
 
     def __init__(self, name, np, dev):
         from ferrum_gpu.hip import DeviceBuffer
@@ -427,6 +475,34 @@ class OpWorkload:
             self.d_out = [DeviceBuffer(dev, 8 * n)]
             self.algo_bytes = 16 * n
             kernel = "fg_interleave_c64_vec"
+        elif name.startswith("shape_"):
+            import ctypes
+
+            from ferrum_gpu.hip import Module
+
+            if name == "shape_cfg5col":
+                a = make_input(np, dev, n, 5, "uniform")
+                self.inputs = [a]
+                self.parts = []
+                self.d_in = [DeviceBuffer(dev, 8 * n)]
+                self.d_in[0].copy_from_host(a)
+                self.d_out = self.d_in            # in place, as the column pass runs
+                self.geom = cfg5_column_geom(12)
+                self.grid = (4096 // 8) * 2 * (n >> 24)
+                self.block = 512
+                kernel = "fg_copy_shape_tile_l11_g8_h_cc"
+            else:
+                log_n = int(name[len("shape_n"):])
+                self.d_in = [DeviceBuffer(dev, 8 * n)]
+                self.d_in[0].copy_from_host(a)
+                self.d_out = [DeviceBuffer(dev, 8 * n)]
+                self.batch = ctypes.c_uint64(n >> log_n)
+                self.grid = (n >> log_n) // 2 if log_n == 10 else n >> log_n
+                self.block = 128 if log_n == 10 else (1 << log_n) // 32
+                kernel = f"fg_copy_shape_n{log_n}"
+            self.algo_bytes = 16 * n
+            self.exact = True
+            self.fn = Module(dev).kernel(kernel)
         else:  # transpose
             self.side = 1 << 13
             assert self.side * self.side == n
@@ -450,7 +526,13 @@ class OpWorkload:
         from ferrum_gpu import pointwise
 
         d, i, o = self.dev, self.d_in, self.d_out
-        if self.name == "cmul":
+        if self.name.startswith("shape_"):
+            import ctypes
+
+            ptrs = [ctypes.c_void_p(i[0].ptr), ctypes.c_void_p(o[0].ptr)]
+            args = ptrs + [self.geom] if self.name == "shape_cfg5col" else ptrs + [self.batch]
+            self.fn.launch((self.grid,), (self.block,), args, stream=stream)
+        elif self.name == "cmul":
             pointwise.cmul(d, i[0], i[1], o[0], self.n, stream)
         elif self.name == "cmul_split":
             pointwise.cmul_split(d, i[0], i[1], i[2], i[3], o[0], o[1], self.n, stream)
@@ -482,6 +564,8 @@ class OpWorkload:
 
         np = self.np
         a = self.inputs[0]
+        if self.name.startswith("shape_"):
+            return a.copy()   # a copy: the output is the input
         if self.name == "transpose":
             out = a.copy()
             side = self.side
@@ -527,6 +611,9 @@ class OpWorkload:
     def config(self):
         if self.name == "transpose":
             return {"rows": self.side, "cols": self.side, "batch": 1, "layout": "interleaved complex64"}
+        if self.name.startswith("shape_"):
+            return {"elements": self.n, "kernel": self.kernels[0], "grid": self.grid, "block": self.block,
+                    "layout": "interleaved complex64" + (", in place" if self.name == "shape_cfg5col" else "")}
         return {"elements": self.n,
                 "layout": "split re/im f32 arrays" if self.name == "cmul_split" else "see workload"}
 

@@ -456,3 +456,29 @@ extern "C" __global__ __launch_bounds__(256) void fg_fill_c64(float2* __restrict
                                                              uint32_t normal) {
     fill_c64_body(out, n, seed, normal);
 }
+
+// ------------------------------------------------------------ shape copies
+//
+// fg_copy_shape_*: out = in with the access shape, workgroup size and LDS of
+// an FFT kernel and no arithmetic (shape_copy.hpp): the memory-only floor of
+// that kernel, timed by the bench beside it.  n10: fg_fft_n10 (config 3);
+// n14 / n15: fg_fft_n14 / fg_fft_n15; tile_l11_g8_h_cc: config 5's column
+// pass (launched with that pass's geometry, in place).
+#include "shape_copy.hpp"
+
+extern "C" __global__ __launch_bounds__(128) void fg_copy_shape_n10(const float2* __restrict__ in,
+                                                                   float2* __restrict__ out, uint64_t batch) {
+    copy_shape_x2_1024(in, out, batch);
+}
+extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void fg_copy_shape_n14(
+    const float2* __restrict__ in, float2* __restrict__ out, uint64_t batch) {
+    copy_shape_rows_halves<14>(in, out, batch);
+}
+extern "C" __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) void fg_copy_shape_n15(
+    const float2* __restrict__ in, float2* __restrict__ out, uint64_t batch) {
+    copy_shape_rows_halves<15>(in, out, batch);
+}
+extern "C" __global__ __launch_bounds__(8 * HalvesShape<11>::T) __attribute__((amdgpu_waves_per_eu(4))) void
+fg_copy_shape_tile_l11_g8_h_cc(const float2* __restrict__ in, float2* __restrict__ out, TileGeom g) {
+    copy_shape_tile_halves<11, 8, true, true>(in, out, g);
+}

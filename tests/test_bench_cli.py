@@ -83,9 +83,13 @@ def test_throughput_gate():
 def test_single_pass_workloads():
     import bench
 
-    for name, log_n, batch in (("1d_8192", 13, 8192), ("1d_16384", 14, 4096), ("1d_32768", 15, 2048)):
+    for name, log_n, batch in (("1d_8192", 13, 8192), ("1d_16384", 14, 4096), ("1d_32768", 15, 2048),
+                               ("1d_2p16", 16, 1024), ("1d_2p18", 18, 256), ("1d_2p20", 20, 64)):
         dims, ln, b, *_ = bench.FFT_WORKLOADS[name]
         assert (dims, ln, b) == (1, log_n, batch) and b << ln == 1 << 26   # 512 MiB
+    for name, log_n, batch in (("2d_64", 6, 16384), ("2d_128", 7, 4096), ("2d_512", 9, 256), ("2d_1024", 10, 64)):
+        dims, ln, b, *_ = bench.FFT_WORKLOADS[name]
+        assert (dims, ln, b) == (2, log_n, batch) and b << (2 * ln) == 1 << 26
 
 
 class _Ev:
@@ -231,3 +235,30 @@ def test_pass_table_rates():
     assert rows[0]["avg_ms"] == 0.04 and rows[1]["median_ms"] == 0.05 and rows[1]["launches"] == 3
     assert rows[0]["gbs"] == pytest.approx((1 << 28) / 0.04e-3 / 1e9, abs=0.051)
     assert rows[0]["frac"] == pytest.approx(rows[0]["gbs"] / 8000.0, abs=1e-4)
+
+
+def test_shape_copy_geometry_is_config5s_column_pass():
+    # bench.py's shape_cfg5col launches the column pass's geometry: tiles of 8
+    # columns over the rows of each parity, element stride 2C, in place, line
+    # groups; every element of both images is read and written exactly once
+    import bench
+
+    g = bench.cfg5_column_geom(12)
+    C = 4096
+    assert (g.t0n, g.t1n, g.is0, g.is1, g.is2, g.ies, g.ics) == (C // 8, 2, 8, C, C * C, 2 * C, 1)
+    assert (g.os0, g.os1, g.os2, g.oes, g.ocs) == (g.is0, g.is1, g.is2, g.ies, g.ics)
+    assert g.remap == 2 and g.log_m == 0 and g.flags == 0 and g.scale == 1.0
+    tiles = g.t0n * g.t1n * 2
+    assert tiles % (8 * 2) == 0          # the line-group order applies (grid a multiple of 8 s)
+    b = np.arange(tiles)
+    t0, t1, t2 = b % g.t0n, (b // g.t0n) % g.t1n, b // (g.t0n * g.t1n)
+    base = t0 * g.is0 + t1 * g.is1 + t2 * g.is2
+    idx = (base[:, None, None] + np.arange(8)[None, :, None] + np.arange(2048)[None, None, :] * g.ies).ravel()
+    assert idx.min() == 0 and idx.max() == 2 * C * C - 1 and len(np.unique(idx)) == 2 * C * C
+
+
+def test_shape_copy_workloads_are_listed():
+    import bench
+
+    for name in ("shape_n10", "shape_n14", "shape_n15", "shape_cfg5col"):
+        assert name in bench.OP_WORKLOADS and name in bench.WORKLOADS
