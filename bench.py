@@ -109,6 +109,8 @@ OP_WORKLOADS = {
     "shape_n15": (1 << 26, "copy with fg_fft_n15's access shape (2048 x 32768 complex64), N(0,1) seed 3"),
     "shape_cfg5col": (1 << 25, "in-place copy with config 5's column pass geometry (fg_tile_l11_g8_h_cc over two "
                                "4096x4096 images: 2048-row tiles of 8 columns per row parity), U[-1,1) seed 5"),
+    "shape_cfg5row": (1 << 25, "copy with config 5's row-pair pass shape (fg_fft2d_rowpair_n12: rows r and r + 2048 "
+                               "of two 4096x4096 images in, rows 2r and 2r + 1 out), U[-1,1) seed 5"),
 }
 WORKLOADS = sorted(FFT_WORKLOADS) + sorted(OP_WORKLOADS)
 
@@ -480,7 +482,19 @@ class OpWorkload:
 
             from ferrum_gpu.hip import Module
 
-            if name == "shape_cfg5col":
+            if name == "shape_cfg5row":
+                a = make_input(np, dev, n, 5, "uniform")
+                self.inputs = [a]
+                self.parts = []
+                self.d_in = [DeviceBuffer(dev, 8 * n)]
+                self.d_in[0].copy_from_host(a)
+                self.d_out = [DeviceBuffer(dev, 8 * n)]
+                self.pairs = ctypes.c_uint64(n >> 13)      # 2048 row pairs per 4096 x 4096 image
+                self.log_rows = ctypes.c_uint32(12)
+                self.grid = n >> 13
+                self.block = 256
+                kernel = "fg_copy_shape_rowpair_n12"
+            elif name == "shape_cfg5col":
                 a = make_input(np, dev, n, 5, "uniform")
                 self.inputs = [a]
                 self.parts = []
@@ -530,7 +544,12 @@ class OpWorkload:
             import ctypes
 
             ptrs = [ctypes.c_void_p(i[0].ptr), ctypes.c_void_p(o[0].ptr)]
-            args = ptrs + [self.geom] if self.name == "shape_cfg5col" else ptrs + [self.batch]
+            if self.name == "shape_cfg5col":
+                args = ptrs + [self.geom]
+            elif self.name == "shape_cfg5row":
+                args = ptrs + [self.pairs, self.log_rows]
+            else:
+                args = ptrs + [self.batch]
             self.fn.launch((self.grid,), (self.block,), args, stream=stream)
         elif self.name == "cmul":
             pointwise.cmul(d, i[0], i[1], o[0], self.n, stream)
@@ -564,6 +583,10 @@ class OpWorkload:
 
         np = self.np
         a = self.inputs[0]
+        if self.name == "shape_cfg5row":
+            # row r of each image's first half to row 2r, row r + 2048 to row 2r + 1
+            imgs = a.reshape(-1, 2, 2048, 4096)
+            return np.ascontiguousarray(imgs.transpose(0, 2, 1, 3)).reshape(-1)
         if self.name.startswith("shape_"):
             return a.copy()   # a copy: the output is the input
         if self.name == "transpose":

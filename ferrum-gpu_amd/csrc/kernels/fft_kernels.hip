@@ -462,8 +462,9 @@ extern "C" __global__ __launch_bounds__(256) void fg_fill_c64(float2* __restrict
 // fg_copy_shape_*: out = in with the access shape, workgroup size and LDS of
 // an FFT kernel and no arithmetic (shape_copy.hpp): the memory-only floor of
 // that kernel, timed by the bench beside it.  n10: fg_fft_n10 (config 3);
-// n14 / n15: fg_fft_n14 / fg_fft_n15; tile_l11_g8_h_cc: config 5's column
-// pass (launched with that pass's geometry, in place).
+// n14 / n15: fg_fft_n14 / fg_fft_n15; rowpair_n12 and tile_l11_g8_h_cc:
+// config 5's row and column passes (the column pass launched with that
+// pass's geometry, in place).
 #include "shape_copy.hpp"
 
 extern "C" __global__ __launch_bounds__(128) void fg_copy_shape_n10(const float2* __restrict__ in,
@@ -481,4 +482,8 @@ extern "C" __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu
 extern "C" __global__ __launch_bounds__(8 * HalvesShape<11>::T) __attribute__((amdgpu_waves_per_eu(4))) void
 fg_copy_shape_tile_l11_g8_h_cc(const float2* __restrict__ in, float2* __restrict__ out, TileGeom g) {
     copy_shape_tile_halves<11, 8, true, true>(in, out, g);
+}
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void fg_copy_shape_rowpair_n12(
+    const float2* __restrict__ in, float2* __restrict__ out, uint64_t pairs, uint32_t log_rows) {
+    copy_shape_rowpair_halves<12>(in, out, pairs, log_rows);
 }

@@ -99,4 +99,32 @@ __device__ __forceinline__ void copy_shape_tile_halves(const float2* __restrict_
         gstore<STORE_CACHED>(reinterpret_cast<float2*>(out_tile + m * row_step + lane_off), x[m]);
 }
 
+// fg_fft2d_rowpair_n<LOGN> with 32 elements per thread
+// (fft2d_rowpair_halves_body): rows r and r + R/2 of an image per workgroup
+// of 2T threads, streamed in, stored cached to rows 2r and 2r + 1 (each
+// row's values to its own output row: a permutation of the rows), two
+// N/2 + N/32-slot LDS regions.
+template <int LOGN>
+__device__ __forceinline__ void copy_shape_rowpair_halves(const float2* __restrict__ in, float2* __restrict__ out,
+                                                          uint64_t pairs, uint32_t log_rows) {
+    using H = HalvesShape<LOGN>;
+    __shared__ float2 lds[2][H::HALF + H::HALF / 16];
+    const int s = threadIdx.x / H::T;
+    const int t = threadIdx.x - s * H::T;
+    const uint64_t p = blockIdx.x;
+    if (p >= pairs) return;
+    const uint64_t half = 1ull << (log_rows - 1);
+    const uint64_t r = p & (half - 1);
+    const uint64_t first = (p >> (log_rows - 1)) << log_rows;
+    const InterleavedIOT<false, true> io{in, out};
+    const uint64_t row_in = first + r + (s ? half : 0);
+    float2 x[H::E];
+#pragma unroll
+    for (int m = 0; m < H::E; ++m) x[m] = io.load_row(row_in * H::N + H::T * m, t);
+    x[0] = touch_lds(&lds[0][0], x[0]);
+    const uint64_t row_out = first + 2 * r + s;
+#pragma unroll
+    for (int m = 0; m < H::E; ++m) io.store_row(row_out * H::N + H::T * m, t, x[m]);
+}
+
 }  // namespace fg

@@ -260,5 +260,5 @@ def test_shape_copy_geometry_is_config5s_column_pass():
 def test_shape_copy_workloads_are_listed():
     import bench
 
-    for name in ("shape_n10", "shape_n14", "shape_n15", "shape_cfg5col"):
+    for name in ("shape_n10", "shape_n14", "shape_n15", "shape_cfg5col", "shape_cfg5row"):
         assert name in bench.OP_WORKLOADS and name in bench.WORKLOADS

@@ -26,7 +26,7 @@ BENCH = os.path.join(ROOT, "bench.py")
 FFT = ["cfg1", "cfg2_256", "cfg2_4096", "cfg3", "cfg3_split", "cfg4", "cfg5", "1d_8192", "1d_16384",
        "1d_32768", "1d_2p16", "1d_2p18", "1d_2p20", "2d_64", "2d_128", "2d_512", "2d_1024"]
 OPS = ["cmul", "cmul_split", "deinterleave", "interleave", "transpose", "shape_n10", "shape_n14", "shape_n15",
-       "shape_cfg5col"]
+       "shape_cfg5col", "shape_cfg5row"]
 
 
 SMALL = {"cfg1", "cfg2_256", "cfg2_4096"}
