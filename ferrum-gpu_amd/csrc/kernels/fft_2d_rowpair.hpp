@@ -83,16 +83,48 @@ __device__ __forceinline__ void fft2d_rowpair_body(const float2* __restrict__ in
     else rowpair_combine<Sh::E, Sh::T, 1>(x, t, lds[0], io, row_out, Sh::N, w);
 }
 
-// The same pass with 32 elements per thread and each row's exchanges in
-// halves (fft_stockham.hpp, RowHalvesStages): 2T = N/16 threads and N/2 +
-// N/32 LDS positions per row, half the LDS of the 16-element layout.
+// Stages S0 .. SL of one row with the exchanges between them (the exchange
+// after SL is the caller's): y holds stage SL's outputs on return.
+template <int LOGN, int S0, int SL>
+struct RowHalvesPrefix {
+    __device__ __forceinline__ static void run(float2* x, float2* y, int t, const float2* __restrict__ tw,
+                                               float2* __restrict__ lds) {
+        halves_stage<LOGN, S0>(x, y, t, tw);
+        if constexpr (S0 < SL) {
+            row_halves_exchange<LOGN, S0>(y, x, t, lds);
+            RowHalvesPrefix<LOGN, S0 + 1, SL>::run(x, y, t, tw, lds);
+        }
+    }
+};
+
+// The row-pair pass with 32 elements per thread (N/16 threads: two rows of
+// T = N/32) and the pair combined in registers.  Half s of the
+// workgroup runs row s's stages up to the one before the last (each row in
+// its own LDS region, exchanges in halves); the exchange before the last
+// stage then crosses the rows: each row scatters into its own region as
+// usual, and thread t of half s gathers, from both regions, the inputs of
+// last-stage butterfly b = T s + t of both rows (positions b + (N/16) p), so
+// it holds outputs b + (N/16) q of both rows after the last stage and stores
+// A + B and (A - B) W_R^r directly.  Every element goes through the same
+// arithmetic as when each half runs its own row's last stage and the pair
+// is exchanged through LDS afterwards (the same butterflies and twiddles,
+// only run by other threads), without that exchange; the two rows' last
+// butterflies share their twiddle reads.
+// Measured on gfx950 against the same pass with each row's last exchange
+// in its own region and the pair exchanged after it (same bits): config 5
+// row pass 88.1 -> 86.4 us per 512 MiB launch, step 186.8 -> 185.1 us.
 template <int LOGN>
-__device__ __forceinline__ void fft2d_rowpair_halves_body(const float2* __restrict__ in, float2* __restrict__ out,
-                                                          const float2* __restrict__ tw,
-                                                          const float2* __restrict__ big, uint64_t pairs,
-                                                          uint32_t log_rows, uint32_t flags) {
+__device__ __forceinline__ void fft2d_rowpair_fused_body(const float2* __restrict__ in, float2* __restrict__ out,
+                                                         const float2* __restrict__ tw,
+                                                         const float2* __restrict__ big, uint64_t pairs,
+                                                         uint32_t log_rows, uint32_t flags) {
     using H = HalvesShape<LOGN>;
     static_assert(H::T % 64 == 0, "whole waves per row");
+    static_assert(H::REM == 0 && H::NSTAGES >= 2, "radix-16 stages only: two last-stage butterflies per thread");
+    constexpr int SP = H::NSTAGES - 2;   // the stage before the last
+    constexpr int LL = H::N / 16;        // the last stage's L: butterflies per row
+    constexpr int LLP = LL + LL / 16;    // lds_pos(x + LL) - lds_pos(x)
+    using St = HalvesStage<LOGN, SP>;
     __shared__ float2 lds[2][H::HALF + H::HALF / 16];
     const int s = threadIdx.x / H::T;  // the same for a whole wave
     const int t = threadIdx.x - s * H::T;
@@ -110,15 +142,48 @@ __device__ __forceinline__ void fft2d_rowpair_halves_body(const float2* __restri
 #pragma unroll
         for (int m = 0; m < H::E; ++m) x[m] = cconj(x[m]);
     }
-    RowHalvesStages<LOGN, 0>::run(x, y, t, tw, lds[s]);
-    __syncthreads();  // every read of the last exchange is done
-    if (s == 0) rowpair_send<H::E, H::T, 0>(y, t, lds[0]);
-    else rowpair_send<H::E, H::T, 1>(y, t, lds[1]);
-    __syncthreads();
+    RowHalvesPrefix<LOGN, 0, SP>::run(x, y, t, tw, lds[s]);
+    // The cross exchange: round h, own region's writes as row_halves_exchange
+    // (positions below / above N/2), then both regions' reads of inputs
+    // p in [8h, 8h + 8) of butterfly b (x[p]: row 0, x[16 + p]: row 1).
+    const int b = H::T * s + t;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        __syncthreads();  // the previous round's (or exchange's) readers are done
+#pragma unroll
+        for (int ii = 0; ii < St::NB / 2; ++ii) {
+            const int i = h * (St::NB / 2) + ii;
+            const int bb = t + H::T * i;
+            const int d0 = (bb >> (4 * SP)) * St::L * 16 + (bb & (St::L - 1)) - H::HALF * h;
+            float2* base = &lds[s][0] + lds_pos<>(d0);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) base[q * (St::L + St::L / 16)] = y[i + St::NB * q];
+        }
+        __syncthreads();
+        const float2* r0 = &lds[0][0] + lds_pos<>(b);
+        const float2* r1 = &lds[1][0] + lds_pos<>(b);
+#pragma unroll
+        for (int pp = 0; pp < 8; ++pp) {
+            x[8 * h + pp] = r0[pp * LLP];
+            x[16 + 8 * h + pp] = r1[pp * LLP];
+        }
+    }
+    // The last stage for both rows: butterfly b, k = b (j = 0), outputs q at b + LL q.
+    const float2* twl = tw + stockham_tw_offset<LOGN, 4>(H::NSTAGES - 1);
+#pragma unroll
+    for (int row = 0; row < 2; ++row) {
+        apply_stage_twiddles_at<16, LL>(x + 16 * row, twl, b);
+        Dft<16>::run(x + 16 * row);
+    }
     const float2 w = big[r << (12 - log_rows)];
     const uint64_t row_out = first + 2 * r;
-    if (s == 0) rowpair_combine<H::E, H::T, 0>(y, t, lds[1], io, row_out, H::N, w);
-    else rowpair_combine<H::E, H::T, 1>(y, t, lds[0], io, row_out, H::N, w);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const float2 a = x[q], c = x[16 + q];
+        const uint64_t pos = (uint64_t)LL * q + H::T * s;
+        io.store_row(row_out * H::N + pos, t, make_float2(a.x + c.x, a.y + c.y));
+        io.store_row((row_out + 1) * H::N + pos, t, cmul(make_float2(a.x - c.x, a.y - c.y), w));
+    }
 }
 
 }  // namespace fg

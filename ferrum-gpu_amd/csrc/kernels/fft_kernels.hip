@@ -317,9 +317,10 @@ FG_FFT2D_HALVES(10, 4)
 // points: the 16-element layout (64 / 128 threads and 8.5 / 17 KB of LDS per
 // row, 128 / 256 threads per workgroup); 4096 points:
 // 32 elements per thread with the exchanges in halves (128 threads and 17 KB
-// per row, four workgroups per CU), measured on gfx950 per 4096 x 4096 image
-// against the 16-element layout (512 threads, 68 KB, two per CU): whole plan
-// 101.4 -> 99.1 us, same bits.
+// per row, four workgroups per CU; the last exchange crosses the pair so the
+// pair combines in registers, fft2d_rowpair_fused_body), measured on gfx950
+// per 4096 x 4096 image against the 16-element layout (512 threads, 68 KB,
+// two per CU): whole plan 101.4 -> 99.1 us, same bits.
 #include "fft_2d_rowpair.hpp"
 extern "C" __global__ __launch_bounds__(128) void fg_fft2d_rowpair_n10(
     const float2* __restrict__ in, float2* __restrict__ out, const float2* __restrict__ tw,
@@ -334,7 +335,7 @@ extern "C" __global__ __launch_bounds__(256) void fg_fft2d_rowpair_n11(
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void fg_fft2d_rowpair_n12(
     const float2* __restrict__ in, float2* __restrict__ out, const float2* __restrict__ tw,
     const float2* __restrict__ big, uint64_t pairs, uint32_t log_rows, uint32_t flags) {
-    fft2d_rowpair_halves_body<12>(in, out, tw, big, pairs, log_rows, flags);
+    fft2d_rowpair_fused_body<12>(in, out, tw, big, pairs, log_rows, flags);
 }
 
 // ------------------------------------------------------- multi-pass tiles

@@ -100,7 +100,7 @@ __device__ __forceinline__ void copy_shape_tile_halves(const float2* __restrict_
 }
 
 // fg_fft2d_rowpair_n<LOGN> with 32 elements per thread
-// (fft2d_rowpair_halves_body): rows r and r + R/2 of an image per workgroup
+// (fft2d_rowpair_fused_body): rows r and r + R/2 of an image per workgroup
 // of 2T threads, streamed in, stored cached to rows 2r and 2r + 1 (each
 // row's values to its own output row: a permutation of the rows), two
 // N/2 + N/32-slot LDS regions.

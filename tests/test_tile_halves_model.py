@@ -258,3 +258,46 @@ def test_narrow_halves_kernels_are_instantiated():
     assert got == {(11, 8), (12, 8)}
     hpp = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_tile.hpp")).read()
     assert "if constexpr (Lay::PADPOS && L == 1) return G;" in hpp
+
+
+def test_rowpair_cross_exchange_model():
+    # fft2d_rowpair_fused_body (4096-point rows, 128 threads per row): the
+    # exchange before the last stage writes each row's stage-1 outputs into
+    # its own LDS region in two rounds (the row exchange's writes) and reads,
+    # in round h, inputs p in [8h, 8h + 8) of last-stage butterfly
+    # b = 128 s + t of both rows from both regions.  Every read slot holds, in
+    # that round, position b + 256 p of its row; slots stay in bounds and no
+    # slot is written twice in a round; each thread's 2 x 16 inputs are
+    # exactly its butterfly's positions b + 256 p, p < 16.
+    N, T, HALF = 4096, 128, 2048
+    NB, L, S = 2, 16, 1
+
+    def lds_pos(p):
+        return p + (p >> 4)
+
+    got = {}
+    for h in range(2):
+        written = {}
+        for s in range(2):
+            for t in range(T):
+                for ii in range(NB // 2):
+                    bb = t + T * (h * (NB // 2) + ii)
+                    d0 = (bb >> (4 * S)) * L * 16 + (bb & (L - 1)) - HALF * h
+                    for q in range(16):
+                        slot = lds_pos(d0) + q * (L + L // 16)
+                        assert slot == lds_pos(d0 + q * L) and 0 <= d0 + q * L < HALF
+                        assert (s, slot) not in written
+                        written[(s, slot)] = d0 + q * L + HALF * h
+        assert len(written) == 2 * HALF
+        for s in range(2):
+            for t in range(T):
+                b = T * s + t
+                for pp in range(8):
+                    slot = lds_pos(b) + pp * (256 + 16)
+                    assert slot < HALF + HALF // 16
+                    for row in range(2):
+                        got.setdefault((s, t, row), []).append(written[(row, slot)])
+    for (s, t, row), positions in got.items():
+        b = T * s + t
+        assert positions == [b + 256 * p for p in range(16)]
+    assert len(got) == 2 * T * 2
