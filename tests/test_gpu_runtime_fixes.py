@@ -224,3 +224,41 @@ def test_batch_beyond_one_launch_executes_in_chunks(gpu_device):
     small.destroy()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     assert rel_l2(got, oracle.fft_1d(x, 2)) <= 1e-6
+
+
+@pytest.mark.parametrize("kind,log_n,batch", [("1d", 15, 600), ("1d", 14, 1100), ("2d", 7, 1100)])
+def test_staggered_start_keeps_the_bits(gpu_device, kind, log_n, batch):
+    # The kernels with one or two workgroups per CU delay their first round's
+    # workgroups when the grid spans two or more rounds (fg_fft_n15 from 512
+    # transforms, fg_fft_n14 and 16384-point images from 1024).  The delay
+    # changes no arithmetic: transforms at both ends of such a batch equal,
+    # bit for bit, the same transforms run as a batch of 8 (no delay), and
+    # the oracle within 1e-4, forward and normalised inverse.
+    import ferrum_gpu
+    from ferrum_gpu.hip import DeviceBuffer
+
+    elems = 1 << (log_n if kind == "1d" else 2 * log_n)
+    x = normal_c64(np.random.default_rng(log_n * 7 + batch), batch * elems)
+    lanes = [0, 1, 2, 3, batch - 4, batch - 3, batch - 2, batch - 1]
+    sub = np.concatenate([x[i * elems:(i + 1) * elems] for i in lanes])
+    print(f"[case] stagger {kind} log_n={log_n} batch={batch}", flush=True)
+    mk = ferrum_gpu.fft.Plan1D if kind == "1d" else ferrum_gpu.fft.Plan2D
+    for direction, normalize in (("forward", False), ("inverse", True)):
+        outs = []
+        for data, b in ((x, batch), (sub, len(lanes))):
+            plan = mk(log_n, b, gpu_device)
+            a, o = DeviceBuffer(gpu_device, plan.nbytes), DeviceBuffer(gpu_device, plan.nbytes)
+            a.copy_from_host(data)
+            plan.execute(a, o, direction, normalize)
+            gpu_device.sync()
+            y = np.empty_like(data)
+            o.copy_to_host(y)
+            outs.append(y)
+            plan.destroy()
+            a.free()
+            o.free()
+        big = np.concatenate([outs[0][i * elems:(i + 1) * elems] for i in lanes])
+        assert np.array_equal(big.view(np.uint32), outs[1].view(np.uint32))
+        ref = (oracle.fft_1d(sub, log_n, direction, normalize, threads=8) if kind == "1d"
+               else oracle.fft_2d(sub, log_n, direction, normalize))
+        assert rel_l2(outs[1], ref) <= 1e-4
