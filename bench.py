@@ -774,6 +774,18 @@ def steady_state(np, per_kernel, dominant_key: str, graph: bool):
 EXTRA_CONFIGS = ["cfg1", "cfg2_256", "cfg2_4096", "cfg4", "cfg5"]
 CONFIG_STEPS, CONFIG_WARMUP = 100, 10
 GRAPH_STEPS_PER_REPLAY = 20
+# The reference's one published table (README.md:123-153): batched 1D forward
+# C2C at batch 256, µs per FFT = median event-timed launch / batch, on an RTX
+# 5060 Laptop GPU (sm_120) at a locked 1500 MHz graphics clock, CUDA 13.1.
+# Configs 1 and 2 are exactly those shapes.
+REFERENCE_US_PER_FFT = {
+    "cfg1": (0.102, "fft_c2c_1024"),
+    "cfg2_256": (0.035, "fft_c2c_256"),
+    "cfg2_4096": (0.509, "fft_c2c_4096"),
+}
+REFERENCE_TABLE_NOTE = ("the reference's published table (README.md:123-153): median of 100 event-timed "
+                        "launches / batch 256, RTX 5060 Laptop GPU (sm_120), graphics clock locked at 1500 MHz, "
+                        "CUDA 13.1 -- other hardware")
 
 
 def timed_steps(dev, wl, stream, steps: int, warmup: int, clocks=None) -> dict:
@@ -943,6 +955,16 @@ def config_record(np, N, dev, stream, name: str, steps: int, warmup: int, ramp_m
         g = graph_step_ms(dev, wl, stream, steps, warmup, GRAPH_STEPS_PER_REPLAY)
         rec["graph_ms_per_step"] = round(g, 5)
         rec["graph_value"] = round(wl.algo_bytes / (g * 1e-3) / 1e9, 2)
+    if name in REFERENCE_US_PER_FFT:
+        # per FFT as the reference's table counts it: one direction's launch / batch
+        ffts = wl.batch * len(wl.steps)
+        us = med * 1e3 / ffts
+        ref_us, ref_kernel = REFERENCE_US_PER_FFT[name]
+        rec["us_per_fft"] = round(us, 5)
+        rec["reference_published"] = {"us_per_fft": ref_us, "kernel": ref_kernel, "note": REFERENCE_TABLE_NOTE}
+        rec["reference_over_this"] = round(ref_us / us, 2)
+        if "graph_ms_per_step" in rec:
+            rec["graph_us_per_fft"] = round(rec["graph_ms_per_step"] * 1e3 / ffts, 5)
     wl.run(stream)
     dev.sync()
     outs = wl.step_outputs()

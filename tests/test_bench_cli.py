@@ -250,11 +250,14 @@ def test_shape_copy_geometry_is_config5s_column_pass():
     assert g.remap == 2 and g.log_m == 0 and g.flags == 0 and g.scale == 1.0
     tiles = g.t0n * g.t1n * 2
     assert tiles % (8 * 2) == 0          # the line-group order applies (grid a multiple of 8 s)
-    b = np.arange(tiles)
-    t0, t1, t2 = b % g.t0n, (b // g.t0n) % g.t1n, b // (g.t0n * g.t1n)
-    base = t0 * g.is0 + t1 * g.is1 + t2 * g.is2
+    # one image's tiles cover its C * C elements exactly once; the second
+    # image's tiles are the first's shifted by is2 = C * C
+    b = np.arange(g.t0n * g.t1n)
+    t0, t1 = b % g.t0n, b // g.t0n
+    base = t0 * g.is0 + t1 * g.is1
     idx = (base[:, None, None] + np.arange(8)[None, :, None] + np.arange(2048)[None, None, :] * g.ies).ravel()
-    assert idx.min() == 0 and idx.max() == 2 * C * C - 1 and len(np.unique(idx)) == 2 * C * C
+    counts = np.bincount(idx, minlength=C * C)
+    assert len(counts) == C * C and counts.min() == 1 and counts.max() == 1
 
 
 def test_shape_copy_workloads_are_listed():
@@ -262,3 +265,13 @@ def test_shape_copy_workloads_are_listed():
 
     for name in ("shape_n10", "shape_n14", "shape_n15", "shape_cfg5col", "shape_cfg5row"):
         assert name in bench.OP_WORKLOADS and name in bench.WORKLOADS
+
+
+def test_reference_table_is_the_published_one():
+    # README.md:137-144 of the reference: µs per FFT at batch 256
+    import bench
+
+    assert {k: v[0] for k, v in bench.REFERENCE_US_PER_FFT.items()} == {"cfg1": 0.102, "cfg2_256": 0.035,
+                                                                        "cfg2_4096": 0.509}
+    for name in bench.REFERENCE_US_PER_FFT:
+        assert bench.FFT_WORKLOADS[name][2] == 256

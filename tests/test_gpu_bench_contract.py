@@ -95,6 +95,8 @@ def test_default_run_reports_every_baseline_config():
         assert len(cf[name]["rel_l2_vs_cpu_per_step"]) == 2 and cf[name]["roundtrip_rel_l2"] <= 1e-4
     for name in ("cfg1", "cfg2_256", "cfg2_4096"):
         assert cf[name]["graph_ms_per_step"] > 0
+        assert cf[name]["us_per_fft"] > 0 and cf[name]["reference_over_this"] > 0
+        assert cf[name]["reference_published"]["us_per_fft"] in (0.102, 0.035, 0.509)
     for name, passes in (("cfg4", 3), ("cfg5", 2)):
         rec = cf[name]
         assert rec["plan"]["passes"] == passes and len(rec["passes"]) == passes
