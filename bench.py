@@ -1152,10 +1152,17 @@ def main() -> int:
     # The other BASELINE configurations, timed on the GPU one after another
     # (their CPU checks come after the headline's CPU baseline below).
     extra = []
+    # A configuration that raises records its error instead of costing the
+    # headline line (a GPU fault ends the process either way).
+    config_errors = {}
     for name in config_names:
-        extra.append((name,) + config_record(np, N, dev, stream, name, args.config_steps, args.config_warmup,
-                                             args.ramp_ms))
-        log(f"config {name}: {extra[-1][1]['ms_per_step']} ms per step (median of {args.config_steps})")
+        try:
+            extra.append((name,) + config_record(np, N, dev, stream, name, args.config_steps, args.config_warmup,
+                                                 args.ramp_ms))
+            log(f"config {name}: {extra[-1][1]['ms_per_step']} ms per step (median of {args.config_steps})")
+        except Exception as e:  # noqa: BLE001 -- reported in the JSON line
+            config_errors[name] = f"{type(e).__name__}: {e}"
+            log(f"config {name} failed: {config_errors[name]}")
 
     host = None
     if not args.no_host_path and isinstance(wl, FftWorkload) and wl.layout == "interleaved":
@@ -1170,12 +1177,18 @@ def main() -> int:
             f"gpu-vs-cpu {'max abs diff' if wl.exact else 'rel_l2'} {err:.3e}")
 
     configs = None
-    if extra:
+    if config_names:
         configs = {}
         for name, rec, cwl, outs in extra:
-            check_config(np, rec, cwl, outs)
-            log(f"config {name}: rel_l2 {rec['rel_l2_vs_cpu']:.3e}, fp64 bins {rec['fp64_bins_rel_l2']:.3e}")
+            try:
+                check_config(np, rec, cwl, outs)
+                log(f"config {name}: rel_l2 {rec['rel_l2_vs_cpu']:.3e}, fp64 bins {rec['fp64_bins_rel_l2']:.3e}")
+            except Exception as e:  # noqa: BLE001 -- reported in the JSON line
+                rec["check_error"] = f"{type(e).__name__}: {e}"
+                rec["parity_ok"] = False
             configs[name] = rec
+        for name, err in config_errors.items():
+            configs[name] = {"error": err, "parity_ok": False}
         del extra
 
     config = {"workload": wl.desc, "name": args.workload}
