@@ -1022,7 +1022,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of single-thread CPU timing")
     ap.add_argument("--no-host-path", action="store_true",
                     help="skip timing the host-array entry points (PCIe-inclusive)")
-    ap.add_argument("--ramp-ms", type=float, default=40.0,
+    ap.add_argument("--ramp-ms", type=float, default=200.0,
                     help="before the warmup steps, run the plain copy kernel for this long (wall ms) so "
                          "that the shader clock leaves its idle level; reported as clock_ramp, 0 = off")
     ap.add_argument("--min-frac", type=float, default=None, metavar="F",
