@@ -148,9 +148,14 @@ std::vector<uint32_t> split_1d(uint32_t log_n) {
     // 16384 complex of LDS), three passes beyond 2^20.  Narrow tiles (2048 /
     // 4096-point digits) are for cache-resident data only: reading the input
     // from HBM in 32-byte pieces measured 2.9x slower than 256-byte ones.
+    // Two digits: the last (the row-wise pass that streams the output out)
+    // of at least 256 points, the first of at most 1024.  Measured on gfx950
+    // at 512 MiB per execution, us: 2^18 as 512 * 512 366.9 / 368.1, as
+    // 1024 * 256 356.0, as 256 * 1024 379.2; 2^16 as 256 * 256 326.7 /
+    // 327.9, as 128 * 512 345.8, 512 * 128 345.5, 64 * 1024 380.9.
     if (log_n <= 20) {
-        const uint32_t a = log_n / 2;
-        return {log_n - a, a};
+        const uint32_t a = log_n >= 16 ? std::min<uint32_t>(10, log_n - 8) : log_n - log_n / 2;
+        return {a, log_n - a};
     }
     const uint32_t base = log_n / 3, rest = log_n - 3 * base;
     return {base + (rest > 0 ? 1u : 0u), base + (rest > 1 ? 1u : 0u), base};
