@@ -10,6 +10,7 @@
 // with it the workgroups-per-CU limit) and returns every element unchanged.
 #pragma once
 #include "fft_tile.hpp"
+#include "fft_2d_rowpair.hpp"
 
 namespace fg {
 
@@ -100,7 +101,8 @@ __device__ __forceinline__ void copy_shape_tile_halves(const float2* __restrict_
 }
 
 // fg_fft2d_rowpair_n<LOGN> with 32 elements per thread
-// (fft2d_rowpair_fused_body): rows r and r + R/2 of an image per workgroup
+// (fft2d_rowpair_fused_body): rows r and r + R/2 of an image per workgroup,
+// images in the kernel's order (rowpair_index)
 // of 2T threads, streamed in, stored cached to rows 2r and 2r + 1 (each
 // row's values to its own output row: a permutation of the rows), two
 // N/2 + N/32-slot LDS regions.
@@ -111,8 +113,8 @@ __device__ __forceinline__ void copy_shape_rowpair_halves(const float2* __restri
     __shared__ float2 lds[2][H::HALF + H::HALF / 16];
     const int s = threadIdx.x / H::T;
     const int t = threadIdx.x - s * H::T;
-    const uint64_t p = blockIdx.x;
-    if (p >= pairs) return;
+    if (blockIdx.x >= pairs) return;
+    const uint64_t p = rowpair_index(blockIdx.x, pairs, log_rows);
     const uint64_t half = 1ull << (log_rows - 1);
     const uint64_t r = p & (half - 1);
     const uint64_t first = (p >> (log_rows - 1)) << log_rows;

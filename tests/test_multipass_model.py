@@ -17,11 +17,15 @@ with numpy so the index arithmetic is proven here.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
 import oracle
 from conftest import rel_l2, uniform_c64
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def tile_columns(log_l):
@@ -427,6 +431,37 @@ def test_rowpair_geometry_stays_in_bounds():
         r = np.arange(R // 2)
         assert sorted(np.concatenate([r, r + R // 2])) == list(range(R))
         assert sorted(np.concatenate([2 * r, 2 * r + 1])) == list(range(R))
+
+
+def rowpair_index(b, pairs, log_rows):
+    """rowpair_index in kernels/fft_2d_rowpair.hpp: 4096-row images in reverse
+    order within a launch, rows in order; other heights in the natural order."""
+    if log_rows != 12:
+        return b
+    lh = log_rows - 1
+    images = pairs >> lh
+    return ((images - 1 - (b >> lh)) << lh) | (b & ((1 << lh) - 1))
+
+
+@pytest.mark.parametrize("log_rows,images", [(12, 1), (12, 2), (12, 5), (11, 3)])
+def test_rowpair_order_is_a_permutation(log_rows, images):
+    # every workgroup of a launch takes a different pair of the launch's
+    # images; 4096-row launches start with their last image and end with the
+    # first (the image the column pass starts with), rows ascending in each
+    half = 1 << (log_rows - 1)
+    pairs = images * half
+    b = np.arange(pairs)
+    p = rowpair_index(b, pairs, log_rows)
+    assert sorted(p.tolist()) == list(range(pairs))
+    assert np.array_equal(p & (half - 1), b & (half - 1))
+    if log_rows == 12:
+        assert p[0] == (images - 1) * half and p[-1] == half - 1
+    else:
+        assert np.array_equal(p, b)
+    src = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_2d_rowpair.hpp")).read()
+    assert "if (log_rows != 12) return b;" in src
+    assert "return ((images - 1 - (b >> lh)) << lh) | (b & ((1ull << lh) - 1));" in src
+    assert src.count("const uint64_t p = rowpair_index(blockIdx.x, pairs, log_rows);") == 2
 
 
 def test_chunk_choice_bounds_the_bytes_in_flight():
