@@ -50,15 +50,17 @@ __device__ __forceinline__ void rowpair_combine(const float2* x, int t, const fl
 // column pass starts with the launch's first image, so that image's rows are
 // the last ones stored and are still in the Infinity Cache when a chunk is
 // larger than the cache, and its 8-column tiles (half lines) gain from it.
-// Measured on gfx950 (three alternating runs, us): config 5 (two 4096 x 4096
-// images) 183.3 -> 181.8 per step (column pass 97.3 -> 95.9); at 512 MiB per
+// Measured on gfx950 (alternating runs on four boxes, us): config 5 (two
+// 4096 x 4096 images) per step -1.5, -4.4, +0.8, -1.2 (the column pass 1.7
+// .. 4.1 faster on every box, the row pass up to 0.7 slower); at 512 MiB per
 // execution 4096 x 4096 381 -> 379, 4096 x 2048 376 -> 370, 4096 x 1024 368
 // -> 361.  The 2048-row plans (16-column tiles, whole lines) lost 0.3 .. 1.2
 // % and keep the natural order.
 __device__ __forceinline__ uint64_t rowpair_index(uint64_t b, uint64_t pairs, uint32_t log_rows) {
-    if (log_rows != 12) return b;
     const uint32_t lh = log_rows - 1;
-    const uint64_t images = pairs >> lh;  // the host launches R/2 pairs per image
+    // the plans launch R/2 pairs per image; any other count keeps the natural order
+    if (log_rows != 12 || (pairs & ((1ull << lh) - 1)) != 0) return b;
+    const uint64_t images = pairs >> lh;
     return ((images - 1 - (b >> lh)) << lh) | (b & ((1ull << lh) - 1));
 }
 

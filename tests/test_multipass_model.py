@@ -436,9 +436,9 @@ def test_rowpair_geometry_stays_in_bounds():
 def rowpair_index(b, pairs, log_rows):
     """rowpair_index in kernels/fft_2d_rowpair.hpp: 4096-row images in reverse
     order within a launch, rows in order; other heights in the natural order."""
-    if log_rows != 12:
-        return b
     lh = log_rows - 1
+    if log_rows != 12 or pairs & ((1 << lh) - 1):
+        return b
     images = pairs >> lh
     return ((images - 1 - (b >> lh)) << lh) | (b & ((1 << lh) - 1))
 
@@ -459,7 +459,9 @@ def test_rowpair_order_is_a_permutation(log_rows, images):
     else:
         assert np.array_equal(p, b)
     src = open(os.path.join(ROOT, "ferrum-gpu_amd", "csrc", "kernels", "fft_2d_rowpair.hpp")).read()
-    assert "if (log_rows != 12) return b;" in src
+    assert "if (log_rows != 12 || (pairs & ((1ull << lh) - 1)) != 0) return b;" in src
+    # a count that is not whole images (no plan launches one) keeps the natural order
+    assert np.array_equal(rowpair_index(b[:-1], pairs - 1, log_rows), b[:-1])
     assert "return ((images - 1 - (b >> lh)) << lh) | (b & ((1ull << lh) - 1));" in src
     assert src.count("const uint64_t p = rowpair_index(blockIdx.x, pairs, log_rows);") == 2
 
