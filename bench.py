@@ -796,13 +796,15 @@ def timed_steps(dev, wl, stream, steps: int, warmup: int, clocks=None) -> dict:
     end of its own)."""
     from ferrum_gpu.hip import Event
 
-    for _ in range(warmup):
-        wl.run(stream)
-    dev.sync()
+    # The events exist before the warmup steps, so that the GPU does not sit
+    # idle (and the shader clock does not drop) between the last warmup step
+    # and the timed ones while the host creates them.
     launches = len(wl.launch_names)
     start = Event(dev)
     evs = [[Event(dev) for _ in range(launches)] for _ in range(steps)]
     bound = [wl.bind_events(e) for e in evs]
+    for _ in range(warmup):
+        wl.run(stream)
     dev.sync()
     ctx = clocks if clocks is not None else _NullContext()
     with ctx:
