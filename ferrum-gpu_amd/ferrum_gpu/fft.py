@@ -17,7 +17,7 @@ import operator
 import numpy as np
 
 from ferrum_gpu import _native as _n
-from ferrum_gpu.hip import Device, DeviceBuffer, EventList, Graph
+from ferrum_gpu.hip import Device, DeviceBuffer, EventList, Graph, _release
 
 __all__ = ["fft_1d_c2c_pow2", "fft_2d_c2c_pow2", "fft2_c2c_pow2", "Plan1D", "Plan2D", "Graph", "transpose",
            "set_chunk_bytes", "get_chunk_bytes", "MIN_LOG_N", "MAX_LOG_N", "MIN_LOG_N_2D", "MAX_LOG_N_2D"]
@@ -302,7 +302,10 @@ class _Plan:
 
     def __del__(self):  # pragma: no cover
         try:
-            self.destroy()
+            if getattr(self, "_p", None) is not None and self._p.value:
+                # released after any Capture block open on this thread (ferrum_gpu.hip._release)
+                _release(_n.lib.fg_fft_plan_destroy, self._p)
+                self._p = ctypes.c_void_p()
         except Exception:
             pass
 

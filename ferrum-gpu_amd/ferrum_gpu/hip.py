@@ -11,6 +11,8 @@ device-resident work and for the bench.
 from __future__ import annotations
 
 import ctypes
+import gc
+import threading
 
 import numpy as np
 
@@ -18,6 +20,24 @@ from ferrum_gpu import _native as _n
 
 __all__ = ["Device", "DeviceBuffer", "Event", "EventList", "Stream", "Graph", "Capture", "Module", "Kernel",
            "device_count"]
+
+
+# A finalizer that frees a HIP object (memory, stream, event, graph, plan,
+# module, device) while a Capture block is open on its thread would make a
+# call a stream capture cannot record, and the capture would end invalid.  The
+# garbage collector and dropped references run finalizers at any point, so
+# while a block is open their release calls wait in a list and run when the
+# thread's last block ends.
+_capture_state = threading.local()
+
+
+def _release(fn, *args) -> None:
+    """A finalizer's release call: now, or after the Capture blocks open on
+    this thread have ended."""
+    if getattr(_capture_state, "depth", 0) > 0:
+        _capture_state.deferred.append((fn, args))
+    else:
+        fn(*args)
 
 
 def device_count() -> int:
@@ -73,7 +93,9 @@ class Device:
 
     def __del__(self):  # pragma: no cover - interpreter teardown order
         try:
-            self.close()
+            if getattr(self, "_h", None) is not None:
+                _release(_n.lib.fg_device_close, self._h)
+                self._h = None
         except Exception:
             pass
 
@@ -114,7 +136,10 @@ class DeviceBuffer:
 
     def __del__(self):  # pragma: no cover
         try:
-            self.free()
+            if getattr(self, "_p", None) is not None and self._p.value:
+                # the device object rides along, so it outlives a deferred free
+                _release(lambda dev, p: _n.lib.fg_free(dev.handle, p), self.device, self._p)
+                self._p = ctypes.c_void_p()
         except Exception:
             pass
 
@@ -145,7 +170,9 @@ class Stream:
 
     def __del__(self):  # pragma: no cover
         try:
-            self.destroy()
+            if getattr(self, "_s", None) is not None and self._s.value:
+                _release(lambda dev, st: _n.lib.fg_stream_destroy(dev.handle, st), self.device, self._s)
+                self._s = ctypes.c_void_p()
         except Exception:
             pass
 
@@ -181,7 +208,11 @@ class Graph:
 
     def __del__(self):  # pragma: no cover
         try:
-            self.destroy()
+            if getattr(self, "_g", None) is not None and self._g.value:
+                # the kept plans ride along, so they outlive a deferred destroy
+                _release(lambda g, keep: _n.lib.fg_graph_destroy(g), self._g, self._keep)
+                self._g = ctypes.c_void_p()
+                self._keep = ()
         except Exception:
             pass
 
@@ -196,7 +227,11 @@ class Capture:
         cap.graph.launch()
 
     Calls must come from the capturing thread; the caller keeps the buffers
-    the recorded calls use alive while the graph is launched."""
+    the recorded calls use alive while the graph is launched.  Objects of
+    this package that are garbage-collected inside the block release their
+    HIP resources when the block ends (a release inside it would end the
+    capture invalid); explicit ``free`` / ``destroy`` / ``close`` calls inside
+    the block are the caller's to avoid."""
 
     def __init__(self, device: Device, keep=()):
         self.device = device
@@ -209,13 +244,27 @@ class Capture:
         return self._s.value or 0
 
     def __enter__(self) -> "Capture":
+        gc.collect()  # garbage already unreachable is released before the capture begins
         _n.check(_n.lib.fg_graph_capture_begin(self.device.handle, ctypes.byref(self._s)))
+        if getattr(_capture_state, "depth", 0) == 0:
+            _capture_state.deferred = []
+        _capture_state.depth = getattr(_capture_state, "depth", 0) + 1
         return self
 
     def __exit__(self, exc_type, exc, tb) -> bool:
         g = ctypes.c_void_p()
-        rc = _n.lib.fg_graph_capture_end(self.device.handle, self._s, ctypes.byref(g))
-        self._s = ctypes.c_void_p()
+        try:
+            rc = _n.lib.fg_graph_capture_end(self.device.handle, self._s, ctypes.byref(g))
+        finally:
+            self._s = ctypes.c_void_p()
+            _capture_state.depth -= 1
+            if _capture_state.depth == 0:
+                deferred, _capture_state.deferred = _capture_state.deferred, []
+                for fn, args in deferred:
+                    try:
+                        fn(*args)
+                    except Exception:
+                        pass
         if exc_type is not None:
             if rc == _n.FG_OK and g.value:
                 _n.lib.fg_graph_destroy(g)
@@ -246,7 +295,7 @@ class Event:
 
     def __del__(self):  # pragma: no cover
         try:
-            _n.lib.fg_event_destroy(self._e)
+            _release(_n.lib.fg_event_destroy, self._e)
         except Exception:
             pass
 
@@ -305,6 +354,8 @@ class Module:
 
     def __del__(self):  # pragma: no cover
         try:
-            _n.lib.fg_module_unload(self._m)
+            # the device and the image ride along, so they outlive a deferred unload
+            _release(lambda m, dev, image: _n.lib.fg_module_unload(m), self._m, self.device,
+                     getattr(self, "_image", None))
         except Exception:
             pass
