@@ -212,6 +212,19 @@ bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise) {
     return log_l >= 7 && g == tile_columns(log_l);
 }
 
+bool use_row_halves_tile(uint32_t log_l, uint32_t g, bool rowwise) {
+    // The 1D last pass of 512 / 1024 points in 16-row tiles: every row load
+    // of the tile is issued at once and each half of the positions is
+    // transposed through an LDS tile of L/2 positions, then the exchanges run
+    // in halves -- 35 / 70 KB instead of 70 / 139 KB, so four / two
+    // workgroups per CU instead of two / one.  Measured on gfx950 at 512 MiB
+    // per execution (two alternations, us): 2^20 397.7 / 396.9 -> 368.4 /
+    // 369.9, 2^19 365.4 / 366.3 -> 362.3 / 362.7; at 256 points (2^16 ..
+    // 2^18, already four workgroups per CU) no change (323.5 .. 352.0 either
+    // way), so those keep the 16-element tile.
+    return rowwise && g == 16 && (log_l == 9 || log_l == 10);
+}
+
 bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }
 
 namespace {
@@ -276,7 +289,7 @@ namespace {
 
 uint32_t elems_per_thread_log(uint32_t log_l) { return log_l < 4 ? log_l : 4; }
 
-std::string tile_name(uint32_t log_l, uint32_t g, char kind, const char* policy) {
+std::string tile_name(uint32_t log_l, uint32_t g, const char* kind, const char* policy) {
     return "fg_tile_l" + std::to_string(log_l) + "_g" + std::to_string(g) + "_" + kind + policy;
 }
 
@@ -360,9 +373,10 @@ void FftPlan::add_tile(const HipBackend::Module& mod, uint32_t log_l, uint32_t g
         s.tile_order = halves ? FG_TILE_ORDER_LINE_GROUPS : FG_TILE_ORDER_XCD_RANGES;
         s.order_unit = halves ? 8 * (16 / g) : 8;
     }
-    s.name = tile_name(log_l, g, halves ? 'h' : (rowwise ? 'r' : 'c'), policy);
+    const bool row_halves = use_row_halves_tile(log_l, g, rowwise);
+    s.name = tile_name(log_l, g, halves ? "h" : row_halves ? "rh" : (rowwise ? "r" : "c"), policy);
     s.fn = HipBackend::get_kernel(mod, s.name.c_str());
-    s.block = Dim3(g * ((1u << log_l) >> (halves ? 5 : elems_per_thread_log(log_l))));
+    s.block = Dim3(g * ((1u << log_l) >> ((halves || row_halves) ? 5 : elems_per_thread_log(log_l))));
     s.src = src;
     s.dst = dst;
     s.tw = stage_table(log_l, elems_per_thread_log(log_l));

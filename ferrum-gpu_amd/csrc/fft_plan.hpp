@@ -245,6 +245,9 @@ uint32_t cached_tile_columns(uint32_t log_l, bool rowwise);
 // (fg_tile_l*_g*_h): column passes at the HBM width (tile_columns) of 128 ..
 // 1024 points, and the 8-column passes of 2048 / 4096 points.
 bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise);
+// Whether a 1D last pass (row-wise) runs the 32-element kernel with the
+// exchanges in halves (fg_tile_l*_g16_rh): 16-row tiles of 512 / 1024 points.
+bool use_row_halves_tile(uint32_t log_l, uint32_t g, bool rowwise);
 // Whether the column FFT of an image with 2^log_rows rows runs as two passes.
 bool split_2d_columns(uint32_t log_rows);
 // Largest chunk (bytes of one chunk's array) a multi-launch plan created from

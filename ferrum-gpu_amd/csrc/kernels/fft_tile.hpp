@@ -297,7 +297,7 @@ struct HalvesStages {
     }
 };
 
-template <int LOGL, int G, bool LOAD_CACHED, bool STORE_CACHED, bool CONJ>
+template <int LOGL, int G, bool LOAD_CACHED, bool STORE_CACHED, bool CONJ, bool ROWWISE>
 __device__ __forceinline__ void fft_tile_halves_body(const float2* __restrict__ in, float2* __restrict__ out,
                                                      const float2* __restrict__ tw, const float2* __restrict__ big,
                                                      const TileGeom& g, float2* __restrict__ lds) {
@@ -310,7 +310,39 @@ __device__ __forceinline__ void fft_tile_halves_body(const float2* __restrict__ 
     char* out_tile = reinterpret_cast<char*>(out + tc.ob);
 
     float2 x[H::E], y[H::E];
-    {
+    if constexpr (ROWWISE) {
+        // Rows contiguous (ies == 1): every load of the tile is issued at
+        // once, coalesced along the rows (y[m]: half m / (E/2) of the
+        // positions, linear element li -> row li / HALF, position li % HALF),
+        // then each half is transposed through the LDS tile into the
+        // Stockham positions t + T m of column c.
+        using Lay = TileLayout<LOGL - 1, G>;
+        constexpr int THREADS = G * H::T;
+        static_assert(G * H::HALF == THREADS * (H::E / 2), "one half of the tile per E/2 loads");
+#pragma unroll
+        for (int m = 0; m < H::E; ++m) {
+            const int h = m / (H::E / 2);
+            const int li = tid + THREADS * (m % (H::E / 2));
+            const int cc = li >> (LOGL - 1);
+            const int n = li & (H::HALF - 1);
+            const uint32_t off = (uint32_t)((cc * g.ics + H::HALF * h + n) * sizeof(float2));
+            y[m] = gload<LOAD_CACHED>(reinterpret_cast<const float2*>(in_tile + off));
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (h > 0) __syncthreads();  // the previous half's readers are done
+#pragma unroll
+            for (int m = 0; m < H::E / 2; ++m) {
+                const int li = tid + THREADS * m;
+                lds[Lay::at(li & (H::HALF - 1), li >> (LOGL - 1))] = y[(H::E / 2) * h + m];
+            }
+            __syncthreads();
+            const float2* rbase = lds + Lay::at(t, c);
+#pragma unroll
+            for (int m = 0; m < H::E / 2; ++m) x[(H::E / 2) * h + m] = rbase[m * Lay::template step<H::T>()];
+        }
+        __syncthreads();  // the first exchange writes the LDS tile again
+    } else {
         const uint32_t lane_off = (uint32_t)((c + (uint64_t)t * g.ies) * sizeof(float2));
         const uint64_t row_step = (uint64_t)H::T * g.ies * sizeof(float2);
 #pragma unroll
@@ -345,15 +377,15 @@ __device__ __forceinline__ void fft_tile_halves_body(const float2* __restrict__ 
     }
 }
 
-template <int LOGL, int G, bool LOAD_CACHED, bool STORE_CACHED>
+template <int LOGL, int G, bool LOAD_CACHED, bool STORE_CACHED, bool ROWWISE = false>
 __device__ __forceinline__ void fft_tile_halves_pass(const float2* __restrict__ in, float2* __restrict__ out,
                                                      const float2* __restrict__ tw, const float2* __restrict__ big,
                                                      const TileGeom& g) {
     __shared__ float2 lds[TileLayout<LOGL - 1, G>::ELEMS];
     if (g.flags)
-        fft_tile_halves_body<LOGL, G, LOAD_CACHED, STORE_CACHED, true>(in, out, tw, big, g, lds);
+        fft_tile_halves_body<LOGL, G, LOAD_CACHED, STORE_CACHED, true, ROWWISE>(in, out, tw, big, g, lds);
     else
-        fft_tile_halves_body<LOGL, G, LOAD_CACHED, STORE_CACHED, false>(in, out, tw, big, g, lds);
+        fft_tile_halves_body<LOGL, G, LOAD_CACHED, STORE_CACHED, false, ROWWISE>(in, out, tw, big, g, lds);
 }
 
 // One pass: a forward body and one that applies the inverse's conjugations.

@@ -185,6 +185,13 @@ def use_halves_tile(log_l, g, rowwise):
     return 7 <= log_l and g == tile_columns(log_l)
 
 
+def use_row_halves_tile(log_l, g, rowwise):
+    """use_row_halves_tile in fft_plan.cpp: the 1D last passes of 512 / 1024
+    points in 16-row tiles run the 32-element kernel with the exchanges in
+    halves (fg_tile_l*_g16_rh)."""
+    return rowwise and g == 16 and log_l in (9, 10)
+
+
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
     """The kernel of every pass of a plan of 1D length 2^log_n (one pass up to
     16384 points, several beyond) or of 2D images with 2^log_n rows and
@@ -192,6 +199,7 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
     chunks in flight (the two-stream widths)."""
     def tile(p, pol):
         kind = "h" if use_halves_tile(p["log_l"], p["g"], p["rowwise"]) else \
+            "rh" if use_row_halves_tile(p["log_l"], p["g"], p["rowwise"]) else \
             ("r" if p["rowwise"] else "c")
         return f"fg_tile_l{p['log_l']}_g{p['g']}_{kind}{pol}"
 

@@ -94,6 +94,9 @@ def instantiated_kernels():
     # the 1024-point column pass in 16-column halves tiles, streamed out
     for m in re.finditer(r"^FG_TILE_HALVES_P\((\d+), (\d+), _cs, true, false\)", src, flags=re.M):
         names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_h_cs")
+    # 1D last passes of 512 / 1024 points: rows in, exchanges in halves
+    for m in re.finditer(r"^FG_TILE_ROW_HALVES\((\d+), (\d+), (\w*),", src, flags=re.M):
+        names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_rh{m.group(3)}")
     # row passes over row pairs (2D images of 4096 rows)
     names |= set(re.findall(r"void (fg_fft2d_rowpair_n\d+)\(", src))
     # narrow tiles in halves (2D columns of 2048 / 4096 points): _cc alone

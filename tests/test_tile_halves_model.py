@@ -260,6 +260,85 @@ def test_narrow_halves_kernels_are_instantiated():
     assert "if constexpr (Lay::PADPOS && L == 1) return G;" in hpp
 
 
+def row_tile_load_model(rows, log_l, g):
+    """The row-wise input of fft_tile_halves_body (ROWWISE = true, the 1D last
+    passes fg_tile_l{9,10}_g16_rh): thread tid = c + G t issues all E loads
+    along the rows first -- y[m] is linear element li = tid + THREADS (m mod
+    E/2) of half h = m / (E/2), i.e. row li / HALF at position HALF h + li mod
+    HALF -- then each half goes through the LDS tile (TileLayout<LOGL - 1, G>)
+    into x[E/2 h + m] = position t + T (E/2 h + m) of column c.  Checks every
+    write in bounds and distinct within its half, every read written in the
+    same half, each read address formed as the kernel forms it, and each
+    wave's loads in at most two contiguous runs; returns regs[c, t, m]."""
+    n = 1 << log_l
+    T, half = n // E, n // 2
+    threads = g * T
+    assert g * half == threads * (E // 2)
+    tid = np.arange(threads)
+    y = np.empty((threads, E), np.complex64)
+    for m in range(E):
+        h = m // (E // 2)
+        li = tid + threads * (m % (E // 2))
+        row, pos = li >> (log_l - 1), half * h + (li & (half - 1))
+        assert row.max() < g and pos.max() < n
+        for w in range(0, threads, 64):
+            flat = row[w:w + 64] * n + pos[w:w + 64]
+            assert np.count_nonzero(np.diff(flat) != 1) <= 1   # one row end per wave at most
+        y[:, m] = rows[row, pos]
+    c, t = tid % g, tid // g
+    regs = np.empty((g, T, E), np.complex64)
+    for h in range(2):
+        lds = np.zeros(lds_elems(log_l, g), np.complex64)
+        written = np.zeros(lds.size, dtype=bool)
+        for m in range(E // 2):
+            li = tid + threads * m
+            idx = lds_index(li & (half - 1), li >> (log_l - 1), g)
+            assert idx.max() < lds.size and len(np.unique(idx)) == threads
+            assert not written[idx].any()
+            written[idx] = True
+            lds[idx] = y[:, (E // 2) * h + m]
+        assert written.sum() == half * g
+        for m in range(E // 2):
+            idx = lds_index(t, c, g) + m * layout_step(T, g)
+            assert np.array_equal(idx, lds_index(t + T * m, c, g))
+            assert written[idx].all()
+            regs[c, t, (E // 2) * h + m] = lds[idx]
+    return regs
+
+
+@pytest.mark.parametrize("log_l", [9, 10])
+def test_row_tile_load_transposes_each_half(log_l):
+    # the transposed load hands each thread its Stockham positions t + T m
+    # bit for bit, so the stages are those of the column tile above
+    g, n = 16, 1 << log_l
+    rng = np.random.default_rng(log_l)
+    rows = uniform_c64(rng, g * n).reshape(g, n)
+    T = n // E
+    natural = np.arange(T)[:, None] + T * np.arange(E)[None, :]
+    assert np.array_equal(row_tile_load_model(rows, log_l, g), rows[:, natural])
+    got = halves_model(rows, log_l)
+    assert rel_l2(got, oracle.fft_1d(rows.reshape(-1), log_l).reshape(g, n)) < 1e-5
+
+
+def test_row_halves_tiles_fit_and_are_instantiated():
+    import os
+    import re
+    from test_multipass_model import use_row_halves_tile
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
+    got = set(re.findall(r"^FG_TILE_ROW_HALVES\((\d+), (\d+), (\w*),", src, flags=re.M))
+    assert got == {(l, "16", p) for l in ("9", "10") for p in ("", "_cs")}
+    for log_l in (9, 10):
+        assert use_row_halves_tile(log_l, 16, True)
+        assert not use_row_halves_tile(log_l, 8, True) and not use_row_halves_tile(log_l, 16, False)
+        # four / two workgroups per CU against two / one for the whole 16-row tile
+        lds = lds_elems(log_l, 16) * 8
+        whole = (1 << log_l) * 17 * 8
+        assert 2 * lds == whole and (160 * 1024) // lds == (4 if log_l == 9 else 2)
+        assert (160 * 1024) // whole == (2 if log_l == 9 else 1)
+    assert not use_row_halves_tile(8, 16, True)
+
+
 def test_rowpair_cross_exchange_model():
     # fft2d_rowpair_fused_body (4096-point rows, 128 threads per row): the
     # exchange before the last stage writes each row's stage-1 outputs into
