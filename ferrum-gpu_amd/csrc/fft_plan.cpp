@@ -186,11 +186,16 @@ uint32_t cached_tile_columns(uint32_t log_l, bool rowwise) {
     //    points 47.3 -> 42.3 (32 columns), 512 rows 50.5 -> 47.8 and 1024
     //    rows 58.2 -> 56.2 (16); at 64 points 8 columns lose (47.8 vs 40.2);
     //  * row-wise (the 1D last pass, output streamed in G * 8-byte pieces):
-    //    16 rows at 128 / 256 points (128: 43.1 -> 39.4 from 64), 8 at 512
-    //    (48.4 -> 43.9 from 16), 16 at 1024 (8 lose: 60.6 vs 57.6); at 64
-    //    points 16 rows gain nothing over 64.
+    //    16 rows at 128 points (43.1 -> 39.4 from 64), 8 at 512 (48.4 -> 43.9
+    //    from 16), 16 at 1024 (8 lose: 60.6 vs 57.6); at 64 points 16 rows
+    //    gain nothing over 64.  256 points: 32 rows exchanging in halves
+    //    (use_row_halves_tile), measured at 512 MiB per execution against 16
+    //    rows in the 16-element tile (two alternations, us): 2^16 323.1 /
+    //    324.2 -> 321.4 / 322.0, 2^17 341.3 / 341.2 -> 338.2 / 338.7, 2^18
+    //    353.4 / 353.9 -> 352.9 / 352.7, 2^24 479.5 / 479.7 -> 479.5 / 480.1
+    //    (16 rows in halves: 324.1, 340.2, 354.6, 482.3).
     if (log_l < 7) return tile_columns(log_l);
-    if (rowwise) return log_l == 9 ? 8u : 16u;
+    if (rowwise) return log_l == 9 ? 8u : log_l == 8 ? 32u : 16u;
     return 8u;
 }
 
@@ -219,10 +224,12 @@ bool use_row_halves_tile(uint32_t log_l, uint32_t g, bool rowwise) {
     // in halves -- 35 / 70 KB instead of 70 / 139 KB, so four / two
     // workgroups per CU instead of two / one.  Measured on gfx950 at 512 MiB
     // per execution (two alternations, us): 2^20 397.7 / 396.9 -> 368.4 /
-    // 369.9, 2^19 365.4 / 366.3 -> 362.3 / 362.7; at 256 points (2^16 ..
-    // 2^18, already four workgroups per CU) no change (323.5 .. 352.0 either
-    // way), so those keep the 16-element tile.
-    return rowwise && g == 16 && (log_l == 9 || log_l == 10);
+    // 369.9, 2^19 365.4 / 366.3 -> 362.3 / 362.7.  At 256 points (already
+    // four workgroups per CU at 16 rows) halves of 16 rows gained nothing;
+    // halves of 32 rows (34 KB, 256-byte output pieces) do
+    // (cached_tile_columns).
+    if (!rowwise) return false;
+    return (g == 16 && (log_l == 9 || log_l == 10)) || (g == 32 && log_l == 8);
 }
 
 bool split_2d_columns(uint32_t log_rows) { return log_rows > 12; }

@@ -246,7 +246,8 @@ uint32_t cached_tile_columns(uint32_t log_l, bool rowwise);
 // 1024 points, and the 8-column passes of 2048 / 4096 points.
 bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise);
 // Whether a 1D last pass (row-wise) runs the 32-element kernel with the
-// exchanges in halves (fg_tile_l*_g16_rh): 16-row tiles of 512 / 1024 points.
+// exchanges in halves (fg_tile_l*_g*_rh): 32-row tiles of 256 points, 16-row
+// tiles of 512 / 1024 points.
 bool use_row_halves_tile(uint32_t log_l, uint32_t g, bool rowwise);
 // Whether the column FFT of an image with 2^log_rows rows runs as two passes.
 bool split_2d_columns(uint32_t log_rows);

@@ -407,9 +407,10 @@ FG_TILE_HALVES_P(7, 64, _cs, true, false)
 FG_TILE_HALVES_P(8, 32, _cs, true, false)
 FG_TILE_HALVES_P(9, 16, _cs, true, false)
 FG_TILE_HALVES_P(10, 16, _cs, true, false)
-// 1D last passes of 512 / 1024 points in 16-row tiles: rows in (all loads
-// issued at once, each half transposed through LDS), exchanges in halves,
-// columns out (whole 128-byte lines), streamed out or unchunked.
+// 1D last passes of 256 points in 32-row tiles and of 512 / 1024 points in
+// 16-row tiles: rows in (all loads issued at once, each half transposed
+// through LDS), exchanges in halves, columns out (256- / 128-byte pieces),
+// streamed out or unchunked.
 #define FG_TILE_ROW_HALVES(LOGL, G, TAG, LC, SC)                                                           \
     extern "C" __global__ __launch_bounds__(G * HalvesShape<LOGL>::T) __attribute__((amdgpu_waves_per_eu(4))) \
     void fg_tile_l##LOGL##_g##G##_rh##TAG(const float2* __restrict__ in, float2* __restrict__ out,             \
@@ -417,6 +418,8 @@ FG_TILE_HALVES_P(10, 16, _cs, true, false)
                                           TileGeom g) {                                                       \
         fft_tile_halves_pass<LOGL, G, LC, SC, true>(in, out, tw, big, g);                                     \
     }
+FG_TILE_ROW_HALVES(8, 32, , false, false)
+FG_TILE_ROW_HALVES(8, 32, _cs, true, false)
 FG_TILE_ROW_HALVES(9, 16, , false, false)
 FG_TILE_ROW_HALVES(9, 16, _cs, true, false)
 FG_TILE_ROW_HALVES(10, 16, , false, false)
@@ -424,9 +427,7 @@ FG_TILE_ROW_HALVES(10, 16, _cs, true, false)
 // Row passes (last 1D digit: rows contiguous, transposed store): the widths
 // for HBM-resident input, then those for cache-resident input.
 FG_TILE(7, 64, true, r)
-FG_TILE(8, 32, true, r)
 FG_TILE(7, 16, true, r)
-FG_TILE(8, 16, true, r)
 FG_TILE_NARROW(9, 8, true, r)
 
 // ------------------------------------------------------------- pointwise

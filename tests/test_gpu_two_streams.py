@@ -219,8 +219,8 @@ def test_which_plans_take_two_streams(gpu_device, chunk_limit):
     assert one.describe()["streams"] == 1 and one.kernel_names()[-1] == "fg_tile_l9_g8_r_cc"
     many = ferrum_gpu.fft.Plan1D(19, 128, gpu_device)
     assert many.describe()["streams"] == 2 and many.kernel_names()[-1] == "fg_tile_l9_g16_rh_cs"
-    # 2^18 = 1024 x 256: the 256-point last pass
-    assert ferrum_gpu.fft.Plan1D(18, 256, gpu_device).kernel_names()[:2] == ["fg_tile_l10_g16_h_sc", "fg_tile_l8_g16_r_cs"]
+    # 2^18 = 1024 x 256: the 256-point last pass (32 rows, exchanges in halves)
+    assert ferrum_gpu.fft.Plan1D(18, 256, gpu_device).kernel_names()[:2] == ["fg_tile_l10_g16_h_sc", "fg_tile_l8_g32_rh_cs"]
 
 
 def test_two_stream_plan_behind_the_host_array_path(gpu_device, chunk_limit):

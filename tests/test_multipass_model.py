@@ -42,7 +42,7 @@ def cached_tile_columns(log_l, rowwise):
     if log_l < 7:
         return tile_columns(log_l)
     if rowwise:
-        return 8 if log_l == 9 else 16
+        return {9: 8, 8: 32}.get(log_l, 16)
     return 8
 
 
@@ -186,10 +186,10 @@ def use_halves_tile(log_l, g, rowwise):
 
 
 def use_row_halves_tile(log_l, g, rowwise):
-    """use_row_halves_tile in fft_plan.cpp: the 1D last passes of 512 / 1024
-    points in 16-row tiles run the 32-element kernel with the exchanges in
-    halves (fg_tile_l*_g16_rh)."""
-    return rowwise and g == 16 and log_l in (9, 10)
+    """use_row_halves_tile in fft_plan.cpp: the 1D last passes of 256 points
+    in 32-row tiles and of 512 / 1024 points in 16-row tiles run the
+    32-element kernel with the exchanges in halves (fg_tile_l*_g*_rh)."""
+    return rowwise and ((g == 16 and log_l in (9, 10)) or (g == 32 and log_l == 8))
 
 
 def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):

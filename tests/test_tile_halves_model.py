@@ -306,11 +306,11 @@ def row_tile_load_model(rows, log_l, g):
     return regs
 
 
-@pytest.mark.parametrize("log_l", [9, 10])
-def test_row_tile_load_transposes_each_half(log_l):
+@pytest.mark.parametrize("log_l,g", [(8, 32), (9, 16), (10, 16)])
+def test_row_tile_load_transposes_each_half(log_l, g):
     # the transposed load hands each thread its Stockham positions t + T m
     # bit for bit, so the stages are those of the column tile above
-    g, n = 16, 1 << log_l
+    n = 1 << log_l
     rng = np.random.default_rng(log_l)
     rows = uniform_c64(rng, g * n).reshape(g, n)
     T = n // E
@@ -327,15 +327,16 @@ def test_row_halves_tiles_fit_and_are_instantiated():
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     src = open(os.path.join(root, "ferrum-gpu_amd", "csrc", "kernels", "fft_kernels.hip")).read()
     got = set(re.findall(r"^FG_TILE_ROW_HALVES\((\d+), (\d+), (\w*),", src, flags=re.M))
-    assert got == {(l, "16", p) for l in ("9", "10") for p in ("", "_cs")}
-    for log_l in (9, 10):
-        assert use_row_halves_tile(log_l, 16, True)
-        assert not use_row_halves_tile(log_l, 8, True) and not use_row_halves_tile(log_l, 16, False)
-        # four / two workgroups per CU against two / one for the whole 16-row tile
-        lds = lds_elems(log_l, 16) * 8
-        whole = (1 << log_l) * 17 * 8
-        assert 2 * lds == whole and (160 * 1024) // lds == (4 if log_l == 9 else 2)
-        assert (160 * 1024) // whole == (2 if log_l == 9 else 1)
+    assert got == {(l, g, p) for l, g in (("8", "32"), ("9", "16"), ("10", "16")) for p in ("", "_cs")}
+    for log_l, g in ((8, 32), (9, 16), (10, 16)):
+        assert use_row_halves_tile(log_l, g, True)
+        assert not use_row_halves_tile(log_l, 8, True) and not use_row_halves_tile(log_l, g, False)
+        # four / four / two workgroups per CU; the whole-tile layout of the
+        # 16-element kernel takes twice the LDS
+        lds = lds_elems(log_l, g) * 8
+        whole = (1 << log_l) * (g + 1) * 8
+        assert 2 * lds == whole and (160 * 1024) // lds == (2 if log_l == 10 else 4)
+        assert g * (1 << log_l) // E <= 1024
     assert not use_row_halves_tile(8, 16, True)
 
 
