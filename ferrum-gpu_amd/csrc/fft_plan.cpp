@@ -194,9 +194,16 @@ uint32_t cached_tile_columns(uint32_t log_l, bool rowwise) {
     //    324.2 -> 321.4 / 322.0, 2^17 341.3 / 341.2 -> 338.2 / 338.7, 2^18
     //    353.4 / 353.9 -> 352.9 / 352.7, 2^24 479.5 / 479.7 -> 479.5 / 480.1
     //    (16 rows in halves: 324.1, 340.2, 354.6, 482.3).
+    //  * the 1D middle pass of 256 points (three-pass plans): 16 columns
+    //    exchanging in halves (use_halves_tile; whole 128-byte lines),
+    //    measured at 512 MiB per execution against the 8-column tile (three
+    //    alternations, us): 2^23 478.8 / 479.2 / 477.8 -> 475.7 / 475.5 /
+    //    475.5, 2^24 480.8 / 481.7 / 480.7 -> 480.4 / 479.5 / 479.6; at 128
+    //    points (2^21, 2^22) no gain (483.1 .. 484.5 -> 484.0 .. 485.1 at
+    //    2^21), so those keep 8 columns.
     if (log_l < 7) return tile_columns(log_l);
     if (rowwise) return log_l == 9 ? 8u : log_l == 8 ? 32u : 16u;
-    return 8u;
+    return log_l == 8 ? 16u : 8u;
 }
 
 bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise) {
@@ -212,8 +219,11 @@ bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise) {
     // the same LDS (add_tile gives the timings).  The cache-resident
     // 8-column passes of 128 .. 1024 points keep the 16-element tile: at 512
     // points halves lost (41.5 .. 46.7 -> 45.8 .. 47.3 us per 128 MiB pass).
+    // The 1D middle pass of 256 points runs 16 columns in halves instead.
     if (rowwise) return false;
     if (log_l > 10) return true;
+    // the cache-resident 1D middle pass of 256 points (cached_tile_columns)
+    if (log_l == 8 && g == 16) return true;
     return log_l >= 7 && g == tile_columns(log_l);
 }
 

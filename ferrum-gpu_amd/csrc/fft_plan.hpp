@@ -243,7 +243,8 @@ uint32_t tile_columns(uint32_t log_l);
 uint32_t cached_tile_columns(uint32_t log_l, bool rowwise);
 // Whether a tile pass runs the 32-element kernel with the exchanges in halves
 // (fg_tile_l*_g*_h): column passes at the HBM width (tile_columns) of 128 ..
-// 1024 points, and the 8-column passes of 2048 / 4096 points.
+// 1024 points, the 16-column 1D middle pass of 256 points, and the 8-column
+// passes of 2048 / 4096 points.
 bool use_halves_tile(uint32_t log_l, uint32_t g, bool rowwise);
 // Whether a 1D last pass (row-wise) runs the 32-element kernel with the
 // exchanges in halves (fg_tile_l*_g*_rh): 32-row tiles of 256 points, 16-row

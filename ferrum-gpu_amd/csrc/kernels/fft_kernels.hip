@@ -372,10 +372,9 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 FG_TILE(4, 64, false, c)
 FG_TILE(5, 64, false, c)
 FG_TILE(6, 64, false, c)
-// Column passes over cache-resident data of 1D middle digits (128 / 256
-// points): 8 columns per tile.
+// Column passes over cache-resident data of 1D middle digits of 128 points:
+// 8 columns per tile (256 points: the 16-column halves tile below).
 FG_TILE_NARROW(7, 8, false, c)
-FG_TILE_NARROW(8, 8, false, c)
 // Column passes at the HBM width from 128 points up (the first 1D pass, 1D
 // middle passes of unchunked plans, 2D column passes of 128 .. 1024 rows):
 // the column DFTs and four-step twiddle with 32 elements per thread and the
@@ -401,6 +400,9 @@ FG_TILE_HALVES(10, 16)
 #define FG_TILE_HALVES_NARROW(LOGL, G) FG_TILE_HALVES_P(LOGL, G, _cc, true, true)
 FG_TILE_HALVES_NARROW(11, 8)
 FG_TILE_HALVES_NARROW(12, 8)
+// The 1D middle pass of 256 points over cache-resident data: 16 columns
+// (whole 128-byte lines), 128 threads, 17 KB of LDS, cached in and out.
+FG_TILE_HALVES_P(8, 16, _cc, true, true)
 // 2D column passes of chunked plans at the HBM width: 128 .. 1024 rows,
 // cached in, streamed out.
 FG_TILE_HALVES_P(7, 64, _cs, true, false)

@@ -43,7 +43,7 @@ def cached_tile_columns(log_l, rowwise):
         return tile_columns(log_l)
     if rowwise:
         return {9: 8, 8: 32}.get(log_l, 16)
-    return 8
+    return 16 if log_l == 8 else 8
 
 
 def split_1d(log_n):
@@ -181,6 +181,8 @@ def use_halves_tile(log_l, g, rowwise):
     if rowwise:
         return False
     if log_l > 10:
+        return True
+    if log_l == 8 and g == 16:      # the cache-resident 1D middle pass
         return True
     return 7 <= log_l and g == tile_columns(log_l)
 

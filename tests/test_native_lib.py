@@ -94,6 +94,9 @@ def instantiated_kernels():
     # the 1024-point column pass in 16-column halves tiles, streamed out
     for m in re.finditer(r"^FG_TILE_HALVES_P\((\d+), (\d+), _cs, true, false\)", src, flags=re.M):
         names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_h_cs")
+    # the 1D middle pass of 256 points in halves, cached in and out
+    for m in re.finditer(r"^FG_TILE_HALVES_P\((\d+), (\d+), _cc, true, true\)", src, flags=re.M):
+        names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_h_cc")
     # 1D last passes of 512 / 1024 points: rows in, exchanges in halves
     for m in re.finditer(r"^FG_TILE_ROW_HALVES\((\d+), (\d+), (\w*),", src, flags=re.M):
         names.add(f"fg_tile_l{m.group(1)}_g{m.group(2)}_rh{m.group(3)}")

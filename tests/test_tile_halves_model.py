@@ -214,9 +214,9 @@ def test_row_halves_fit_the_hardware(log_n):
 
 
 # (log_l, G): the instantiated kernels, FG_TILE_HALVES (the widths of the
-# passes that read HBM) and FG_TILE_HALVES_NARROW (2D columns of 1024 .. 4096
-# points)
-CASES = [(7, 64), (8, 32), (9, 16), (10, 16), (10, 8), (11, 8), (12, 8)]
+# passes that read HBM), the 1D middle pass of 256 points (16 columns) and
+# FG_TILE_HALVES_NARROW (2D columns of 1024 .. 4096 points)
+CASES = [(7, 64), (8, 32), (8, 16), (9, 16), (10, 16), (10, 8), (11, 8), (12, 8)]
 
 
 @pytest.mark.parametrize("log_l,g", CASES)
