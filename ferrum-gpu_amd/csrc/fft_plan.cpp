@@ -231,12 +231,12 @@ bool use_row_halves_tile(uint32_t log_l, uint32_t g, bool rowwise) {
     // The 1D last pass of 512 / 1024 points in 16-row tiles: every row load
     // of the tile is issued at once and each half of the positions is
     // transposed through an LDS tile of L/2 positions, then the exchanges run
-    // in halves -- 35 / 70 KB instead of 70 / 139 KB, so four / two
+    // in halves -- 34 / 68 KB instead of 68 / 136 KB, so four / two
     // workgroups per CU instead of two / one.  Measured on gfx950 at 512 MiB
     // per execution (two alternations, us): 2^20 397.7 / 396.9 -> 368.4 /
     // 369.9, 2^19 365.4 / 366.3 -> 362.3 / 362.7.  At 256 points (already
     // four workgroups per CU at 16 rows) halves of 16 rows gained nothing;
-    // halves of 32 rows (34 KB, 256-byte output pieces) do
+    // halves of 32 rows (33 KB, 256-byte output pieces) do
     // (cached_tile_columns).
     if (!rowwise) return false;
     return (g == 16 && (log_l == 9 || log_l == 10)) || (g == 32 && log_l == 8);

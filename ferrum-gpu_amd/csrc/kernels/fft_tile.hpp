@@ -249,8 +249,8 @@ __device__ __forceinline__ void fft_tile_body(const float2* __restrict__ in, flo
 //  * 1D last passes (ROWWISE: rows in, transposed store) of 256 points in
 //    32-row tiles and of 512 / 1024 points in 16-row tiles: every row load
 //    is issued at once and each half of the positions is transposed through
-//    the same L/2-position LDS tile, so 34 / 35 / 70 KB instead of the
-//    16-element tile's 69 / 70 / 139 KB.
+//    the same L/2-position LDS tile, so 33 / 34 / 68 KB instead of the
+//    16-element tile's 66 / 68 / 136 KB.
 //  * 2D column passes of 1024 .. 4096 points, narrow tiles (8 columns, the
 //    position-padded layout): twice the columns of the 16-element tile in the
 //    same LDS (136 KB at 4096 points), so 64-byte row pieces instead of 32.
