@@ -148,14 +148,20 @@ std::vector<uint32_t> split_1d(uint32_t log_n) {
     // 16384 complex of LDS), three passes beyond 2^20.  Narrow tiles (2048 /
     // 4096-point digits) are for cache-resident data only: reading the input
     // from HBM in 32-byte pieces measured 2.9x slower than 256-byte ones.
-    // Two digits: the last (the row-wise pass that streams the output out)
-    // of at least 256 points, the first of at most 1024.  Measured on gfx950
-    // at 512 MiB per execution, us: 2^18 as 512 * 512 366.9 / 368.1, as
-    // 1024 * 256 356.0, as 256 * 1024 379.2; 2^16 as 256 * 256 326.7 /
-    // 327.9, as 128 * 512 345.8, 512 * 128 345.5, 64 * 1024 380.9.
+    // Two digits: the first (the column pass that reads HBM) of at least 256
+    // points, the last (the row-wise pass that streams the output out) of
+    // at most 1024.  Measured on gfx950 at 512 MiB per execution, us, with
+    // the last passes exchanging in halves (three alternations): 2^17 as 256
+    // * 512 330.0 .. 330.9, 512 * 256 338.4 .. 338.9, 128 * 1024 342.0 ..
+    // 343.3; 2^18 as 256 * 1024 339.7 .. 341.0, 1024 * 256 351.4 .. 352.2,
+    // 512 * 512 351.3 .. 352.0; 2^19 as 512 * 1024 358.1 .. 359.8, 1024 *
+    // 512 360.3 .. 361.9; earlier, 2^16 as 256 * 256 326.7 / 327.9, 128 *
+    // 512 345.8, 512 * 128 345.5, 64 * 1024 380.9.  (Before those last
+    // passes, with one 139 KB workgroup per CU at 1024 points, the split
+    // was the other way round: 2^18 as 1024 * 256 356.0, 256 * 1024 379.2.)
     if (log_n <= 20) {
-        const uint32_t a = log_n >= 16 ? std::min<uint32_t>(10, log_n - 8) : log_n - log_n / 2;
-        return {a, log_n - a};
+        const uint32_t b = log_n >= 16 ? std::min<uint32_t>(10, log_n - 8) : log_n / 2;
+        return {log_n - b, b};
     }
     const uint32_t base = log_n / 3, rest = log_n - 3 * base;
     return {base + (rest > 0 ? 1u : 0u), base + (rest > 1 ? 1u : 0u), base};

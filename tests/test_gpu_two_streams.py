@@ -213,14 +213,14 @@ def test_which_plans_take_two_streams(gpu_device, chunk_limit):
     assert d2["streams"] == 1 and d2["chunks"] == 2 and p2.kernel_names()[1] == "fg_tile_l8_g32_h_cs"
     assert ferrum_gpu.fft.Plan2D(9, 2048, gpu_device, log_cols=6).describe()["streams"] == 1
     assert ferrum_gpu.fft.Plan2D(4, 2048, gpu_device, log_cols=11).describe()["streams"] == 1
-    # 2^19 = 1024 x 512: one chunk keeps the 8-row last pass on one stream,
-    # two or more take 16-row tiles and two streams
-    one = ferrum_gpu.fft.Plan1D(19, 1, gpu_device)
+    # 2^17 = 256 x 512: one chunk keeps the 8-row last pass on one stream,
+    # two or more take 16-row tiles (exchanging in halves) and two streams
+    one = ferrum_gpu.fft.Plan1D(17, 1, gpu_device)
     assert one.describe()["streams"] == 1 and one.kernel_names()[-1] == "fg_tile_l9_g8_r_cc"
-    many = ferrum_gpu.fft.Plan1D(19, 128, gpu_device)
+    many = ferrum_gpu.fft.Plan1D(17, 512, gpu_device)
     assert many.describe()["streams"] == 2 and many.kernel_names()[-1] == "fg_tile_l9_g16_rh_cs"
-    # 2^18 = 1024 x 256: the 256-point last pass (32 rows, exchanges in halves)
-    assert ferrum_gpu.fft.Plan1D(18, 256, gpu_device).kernel_names()[:2] == ["fg_tile_l10_g16_h_sc", "fg_tile_l8_g32_rh_cs"]
+    # 2^18 = 256 x 1024: the 1024-point last pass (16 rows, exchanges in halves)
+    assert ferrum_gpu.fft.Plan1D(18, 256, gpu_device).kernel_names()[:2] == ["fg_tile_l8_g32_h_sc", "fg_tile_l10_g16_rh_cs"]
 
 
 def test_two_stream_plan_behind_the_host_array_path(gpu_device, chunk_limit):

@@ -49,8 +49,8 @@ def cached_tile_columns(log_l, rowwise):
 def split_1d(log_n):
     """Digit sizes (log2) for N = 2^log_n, slowest first (split_1d in fft_plan.cpp)."""
     if log_n <= 20:
-        a = min(10, log_n - 8) if log_n >= 16 else log_n - log_n // 2
-        return [a, log_n - a]
+        b = min(10, log_n - 8) if log_n >= 16 else log_n // 2
+        return [log_n - b, b]
     base = log_n // 3
     rest = log_n - 3 * base
     return [base + (1 if rest > 0 else 0), base + (1 if rest > 1 else 0), base]
