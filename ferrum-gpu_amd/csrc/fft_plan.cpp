@@ -514,10 +514,10 @@ std::unique_ptr<FftPlan> FftPlan::make_1d(HipDevice& dev, const HipBackend::Modu
         const uint64_t L = 1ull << log_l, n1 = 1ull << logs[0];
         uint32_t g = p->cached_ ? cached_tile_columns(log_l, true) : tile_columns(log_l);
         // With two chunks in flight (below) the 16-row tile wins at 512
-        // points too (measured with the 512-point last digit of the earlier
-        // 1024 * 512 splits: 2^18 / 2^19 at 512 MiB 397 / 406 us with 8 rows
-        // on one stream -> 370 / 376 us with 16 rows on two); 2^17 = 256 *
-        // 512 takes it now, in halves (use_row_halves_tile).
+        // points too (measured with the 512-point last digits of earlier
+        // splits, 2^18 = 512 * 512 and 2^19 = 1024 * 512: 397 / 406 us at 512
+        // MiB with 8 rows on one stream -> 370 / 376 us with 16 rows on two);
+        // 2^17 = 256 * 512 takes it now, in halves (use_row_halves_tile).
         if (two && g < 16) g = 16;
         if (n1 < g) fail(FG_ERR_INTERNAL, "digit split leaves fewer rows than a tile");
         TileGeom t{};
