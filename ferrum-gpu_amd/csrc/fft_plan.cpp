@@ -656,20 +656,22 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         b.oes = R1 * C;
         p->add_tile(mod, l2, g, false, b, (uint64_t)b.t0n * b.t1n, Buf::Work, Buf::Out, p->policy(2, npass));
     }
-    if (log_rows >= 11 && log_cols >= 10) {
-        // 2048 / 4096 rows of 1024 .. 4096 points, out of place: the column
+    if (log_rows >= 10 && log_cols >= 10) {
+        // 1024 .. 4096 rows of 1024 .. 4096 points, out of place: the column
         // DFT split radix-2 over the row index.  The row pass transforms rows
         // r and r + R/2 of an image in one workgroup and stores A + B and
         // (A - B) W_R^r to output rows 2r and 2r + 1
         // (kernels/fft_2d_rowpair.hpp); the column pass takes R/2-point DFTs
-        // over the rows of each parity in place, in halves (68 KB, two
-        // workgroups per CU): 8 columns at 4096 rows (where a 4096-row tile
-        // takes the CU's LDS), 16 at 2048 rows (whole 128-byte lines).
+        // over the rows of each parity in place, in halves: 8 columns at 4096
+        // rows (68 KB, where a 4096-row tile takes the CU's LDS), 16 at 2048
+        // rows (68 KB) and at 1024 rows (34 KB), whole 128-byte lines.
         // Measured on gfx950 at 512 MiB per execution against the two passes
         // above, us: 4096 x 4096 398 -> 388, 2048 x 4096 373 -> 348, 2048 x
         // 2048 363 -> 359, 2048 x 1024 365 -> 352, 4096 x 1024 375 -> 367
-        // (even in another A/B).  In-place executions keep the two passes
-        // above.
+        // (even in another A/B); 1024 rows (three alternations) x 2048
+        // 340.0 .. 341.0 -> 333.3 .. 334.2, x 4096 340.8 .. 341.9 -> 335.8 ..
+        // 336.3, x 1024 335.2 .. 341.1 -> 331.1 .. 340.2.  In-place executions
+        // keep the two passes above.
         p->steps_in_place_ = std::move(p->steps_);
         p->steps_.clear();
         Step s;
@@ -687,8 +689,9 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         p->big_table();
         p->steps_.push_back(s);
         TileGeom t{};
-        // 2048 rows: 1024-row tiles of 16 columns in halves (whole lines, 68 KB)
-        const uint32_t gw = log_rows == 11 ? 16u : 8u;
+        // 1024 / 2048 rows: 512- / 1024-row tiles of 16 columns in halves
+        // (whole lines, 34 / 68 KB)
+        const uint32_t gw = log_rows <= 11 ? 16u : 8u;
         t.t0n = (uint32_t)(C / gw);
         t.t1n = 2;  // row parity
         t.is0 = t.os0 = gw;

@@ -36,28 +36,28 @@ def _read(dev, buf, nbytes, off, dtype):
     return raw[off:off + nbytes].view(dtype).copy()
 
 
-# (dims, log_n, batch, expected first kernel): the 1024-point kernel in 1D
-# (an even and an odd batch) and as the 2D row pass, and the 4096-point one
+# (dims, log_n (2D: rows), log_cols, batch, expected first kernel): the
+# 1024-point kernel in 1D (an even and an odd batch) and as the 2D row pass
+# (512 x 1024 images), the row pairs of 1024 x 1024 images, and the
+# 4096-point kernel
 CASES = [
-    (1, 10, 1536, "fg_fft_n10"),
-    (1, 10, 2049, "fg_fft_n10"),
-    (2, 10, 1, None),
-    (1, 12, 600, "fg_fft_n12"),
+    (1, 10, None, 1536, "fg_fft_n10"),
+    (1, 10, None, 2049, "fg_fft_n10"),
+    (2, 9, 10, 2, "fg_fft_n10"),
+    (2, 10, 10, 1, "fg_fft2d_rowpair_n10"),
+    (1, 12, None, 600, "fg_fft_n12"),
 ]
 
 
-@pytest.mark.parametrize("dims,log_n,batch,first", CASES)
+@pytest.mark.parametrize("dims,log_n,log_cols,batch,first", CASES)
 @pytest.mark.parametrize("direction", ["forward", "inverse"])
-def test_interleaved_offset_by_8_bytes(gpu_device, dims, log_n, batch, first, direction):
+def test_interleaved_offset_by_8_bytes(gpu_device, dims, log_n, log_cols, batch, first, direction):
     import ferrum_gpu
 
     plan = (ferrum_gpu.fft.Plan1D(log_n, batch, gpu_device) if dims == 1
-            else ferrum_gpu.fft.Plan2D(log_n, batch, gpu_device))
+            else ferrum_gpu.fft.Plan2D(log_n, batch, gpu_device, log_cols=log_cols))
     names = plan.kernel_names()
-    if first:
-        assert names[0] == first
-    else:
-        assert any(n.startswith("fg_fft_n10") for n in names), names
+    assert names[0].startswith(first), names
     nb = plan.nbytes
     rng = np.random.default_rng(log_n * 1000 + batch)
     x = uniform_c64(rng, nb // 8)
@@ -74,7 +74,10 @@ def test_interleaved_offset_by_8_bytes(gpu_device, dims, log_n, batch, first, di
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
     if dims == 1:
         want = oracle.fft_1d(x, log_n, direction, direction == "inverse", threads=8)
-        assert rel_l2(outs[0], want) <= TOL
+    else:
+        from test_gpu_extras import oracle_2d_rect
+        want = oracle_2d_rect(x, log_n, log_cols, direction, direction == "inverse")
+    assert rel_l2(outs[0], want) <= TOL
     plan.destroy()
 
 

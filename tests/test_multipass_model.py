@@ -99,10 +99,11 @@ def tile_geometry_1d(log_n, batch, cached=True, streams=1):
 
 
 def rowpair_2d(log_rows, log_cols):
-    """FftPlan::make_2d: images of 2048 / 4096 rows of 1024 .. 4096 points split
-    their column DFT radix-2 over the row index (kernels/fft_2d_rowpair.hpp)
-    when run out of place; in place they keep the row pass + R-row columns."""
-    return log_rows >= 11 and log_cols >= 10
+    """FftPlan::make_2d: images of 1024 .. 4096 rows of 1024 .. 4096 points
+    split their column DFT radix-2 over the row index
+    (kernels/fft_2d_rowpair.hpp) when run out of place; in place they keep the
+    row pass + R-row columns."""
+    return log_rows >= 10 and log_cols >= 10
 
 
 def rowpair_model(x):
@@ -219,10 +220,10 @@ def plan_kernel_names(two_d, log_n, cached=True, log_cols=None, streams=1):
         return [f"fg_fft2d_l{log_n}_{lc}"]
     if rowpair_2d(log_n, lc):
         # row pairs, then R/2-row halves tiles over each row parity: 8
-        # columns at 4096 rows (narrow: always _cc), 16 at 2048 rows
+        # columns at 4096 rows (narrow: always _cc), 16 at 1024 / 2048 rows
         if log_n == 12:
             return [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l11_g8_h_cc"]
-        return [f"fg_fft2d_rowpair_n{lc}", "fg_tile_l10_g16_h" + ("_cs" if cached else "")]
+        return [f"fg_fft2d_rowpair_n{lc}", f"fg_tile_l{log_n - 1}_g16_h" + ("_cs" if cached else "")]
     passes = tile_geometry_2d(log_n, 1, lc, cached)
     n = len(passes) + 1
     return [f"fg_fft_n{lc}" + ("_sc" if cached else "")] + \
@@ -429,7 +430,8 @@ def test_rowpair_geometry_stays_in_bounds():
     # write the image's elements, each exactly once and each in its own tile
     # (so the pass runs in place); the row pass's workgroups write rows 2r and
     # 2r + 1 of what they read from rows r and r + R/2, every row once
-    for R, C in ((4096, 4096), (4096, 2048), (4096, 1024), (2048, 2048), (2048, 4096), (2048, 1024)):
+    for R, C in ((4096, 4096), (4096, 2048), (4096, 1024), (2048, 2048), (2048, 4096), (2048, 1024),
+                 (1024, 1024), (1024, 4096)):
         g = 8 if R == 4096 else 16
         t0n, t1n, L = C // g, 2, R // 2
         t0 = np.arange(t0n)[:, None, None, None]
