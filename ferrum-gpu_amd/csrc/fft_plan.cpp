@@ -656,8 +656,9 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         b.oes = R1 * C;
         p->add_tile(mod, l2, g, false, b, (uint64_t)b.t0n * b.t1n, Buf::Work, Buf::Out, p->policy(2, npass));
     }
-    if (log_rows >= 10 && log_cols >= 10) {
-        // 1024 .. 4096 rows of 1024 .. 4096 points, out of place: the column
+    if ((log_rows >= 11 && log_cols >= 10) || (log_rows == 10 && log_cols >= 11)) {
+        // 2048 / 4096 rows of 1024 .. 4096 points and 1024 rows of 2048 /
+        // 4096 points, out of place: the column
         // DFT split radix-2 over the row index.  The row pass transforms rows
         // r and r + R/2 of an image in one workgroup and stores A + B and
         // (A - B) W_R^r to output rows 2r and 2r + 1
@@ -670,8 +671,9 @@ std::unique_ptr<FftPlan> FftPlan::make_2d(HipDevice& dev, const HipBackend::Modu
         // 2048 363 -> 359, 2048 x 1024 365 -> 352, 4096 x 1024 375 -> 367
         // (even in another A/B); 1024 rows (three alternations) x 2048
         // 340.0 .. 341.0 -> 333.3 .. 334.2, x 4096 340.8 .. 341.9 -> 335.8 ..
-        // 336.3, x 1024 335.2 .. 341.1 -> 331.1 .. 340.2.  In-place executions
-        // keep the two passes above.
+        // 336.3.  1024 x 1024 measured mixed (335.2 .. 341.1 -> 331.1 ..
+        // 340.2, and 333 -> 342 in an earlier A/B), so it keeps the two
+        // passes above, as every in-place execution does.
         p->steps_in_place_ = std::move(p->steps_);
         p->steps_.clear();
         Step s;

@@ -11,8 +11,9 @@
 // column tile holds twice the columns of an R-point one in the same LDS, so
 // the column pass of 4096-row images runs 2048-row tiles of 8 columns (two
 // workgroups per CU where a 4096-row tile takes the CU's LDS) and those of
-// 2048- / 1024-row images 1024- / 512-row tiles of 16 columns (whole
-// 128-byte lines; four workgroups per CU at 512 rows).  Rows
+// 2048- / 1024-row images (1024 rows: of 2048 / 4096 columns) 1024- /
+// 512-row tiles of 16 columns (whole 128-byte lines; four workgroups per CU
+// at 512 rows).  Rows
 // 2r, 2r + 1 are not the rows r, r + R/2 read, so the pass is out of place
 // only.
 #pragma once

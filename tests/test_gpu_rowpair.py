@@ -1,4 +1,5 @@
-"""2D images of 1024 .. 4096 rows of 1024 .. 4096 points out of place: the row
+"""2D images of 2048 / 4096 rows of 1024 .. 4096 points and of 1024 rows of 2048
+/ 4096 points out of place: the row
 pass over row pairs (fg_fft2d_rowpair_n{10,11,12}: rows r and r + R/2, stored as
 A + B to row 2r and (A - B) W_R^r to row 2r + 1), then R/2-point column DFTs
 over the rows of each parity in place (element stride 2C; fg_tile_l11_g8_h_cc
@@ -57,7 +58,7 @@ def _run(dev, x, lr, lc, direction="forward", normalize=False, in_place=False):
 
 # (log rows, log cols, batch, images per chunk)
 CASES = [(12, 11, 3, 2), (12, 12, 2, 1), (12, 12, 1, 1), (11, 11, 5, 2), (11, 12, 3, 2), (11, 10, 5, 2), (12, 10, 3, 2),
-         (10, 10, 7, 3), (10, 12, 3, 2)]
+         (10, 11, 7, 3), (10, 12, 3, 2)]
 
 
 @pytest.mark.parametrize("lr,lc,batch,per_chunk", CASES)
@@ -85,7 +86,7 @@ def test_rowpair_out_of_place(gpu_device, chunk_limit, lr, lc, batch, per_chunk)
     assert np.array_equal(one.view(np.uint32), fwd.view(np.uint32))
 
 
-@pytest.mark.parametrize("lr,lc", [(12, 10), (12, 11), (12, 12), (11, 10), (11, 11), (11, 12), (10, 10), (10, 11)])
+@pytest.mark.parametrize("lr,lc", [(12, 10), (12, 11), (12, 12), (11, 10), (11, 11), (11, 12), (10, 11), (10, 12)])
 def test_rowpair_in_place_takes_the_row_column_passes(gpu_device, lr, lc):
     batch = 2
     x = uniform_c64(np.random.default_rng(950 + lc), batch << (lr + lc)).reshape(batch, 1 << lr, 1 << lc)

@@ -170,12 +170,12 @@ def test_in_place_kernel_names(gpu_device):
     assert p.kernel_names() == ["fg_fft2d_rowpair_n12", "fg_tile_l11_g8_h_cc"]
     assert p.kernel_names(in_place=True) == ["fg_fft_n12_sc", "fg_tile_l12_g8_h_cc"]
     p.destroy()
-    # 1024 x 1024: 512-row column tiles after the row pairs, 1024-row ones in place
-    p = ferrum_gpu.fft.Plan2D(10, 4, gpu_device)
-    assert p.kernel_names() == ["fg_fft2d_rowpair_n10", "fg_tile_l9_g16_h_cs"]
-    assert p.kernel_names(in_place=True) == ["fg_fft_n10_sc", "fg_tile_l10_g16_h_cs"]
+    # 1024 x 2048: 512-row column tiles after the row pairs, 1024-row ones in place
+    p = ferrum_gpu.fft.Plan2D(10, 2, gpu_device, log_cols=11)
+    assert p.kernel_names() == ["fg_fft2d_rowpair_n11", "fg_tile_l9_g16_h_cs"]
+    assert p.kernel_names(in_place=True) == ["fg_fft_n11_sc", "fg_tile_l10_g16_h_cs"]
     p.destroy()
-    for plan in (ferrum_gpu.fft.Plan1D(24, 4, gpu_device), ferrum_gpu.fft.Plan2D(9, 16, gpu_device),
+    for plan in (ferrum_gpu.fft.Plan1D(24, 4, gpu_device), ferrum_gpu.fft.Plan2D(10, 4, gpu_device),
                  ferrum_gpu.fft.Plan1D(10, 4096, gpu_device)):
         assert plan.kernel_names(in_place=True) == plan.kernel_names()
         plan.destroy()

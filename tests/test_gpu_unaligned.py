@@ -38,13 +38,14 @@ def _read(dev, buf, nbytes, off, dtype):
 
 # (dims, log_n (2D: rows), log_cols, batch, expected first kernel): the
 # 1024-point kernel in 1D (an even and an odd batch) and as the 2D row pass
-# (512 x 1024 images), the row pairs of 1024 x 1024 images, and the
-# 4096-point kernel
+# (512 x 1024 and 1024 x 1024 images), the row pairs of 1024 x 2048 images,
+# and the 4096-point kernel
 CASES = [
     (1, 10, None, 1536, "fg_fft_n10"),
     (1, 10, None, 2049, "fg_fft_n10"),
     (2, 9, 10, 2, "fg_fft_n10"),
-    (2, 10, 10, 1, "fg_fft2d_rowpair_n10"),
+    (2, 10, 10, 1, "fg_fft_n10"),
+    (2, 10, 11, 1, "fg_fft2d_rowpair_n11"),
     (1, 12, None, 600, "fg_fft_n12"),
 ]
 

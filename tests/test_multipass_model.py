@@ -99,11 +99,11 @@ def tile_geometry_1d(log_n, batch, cached=True, streams=1):
 
 
 def rowpair_2d(log_rows, log_cols):
-    """FftPlan::make_2d: images of 1024 .. 4096 rows of 1024 .. 4096 points
-    split their column DFT radix-2 over the row index
-    (kernels/fft_2d_rowpair.hpp) when run out of place; in place they keep the
-    row pass + R-row columns."""
-    return log_rows >= 10 and log_cols >= 10
+    """FftPlan::make_2d: images of 2048 / 4096 rows of 1024 .. 4096 points and
+    of 1024 rows of 2048 / 4096 points split their column DFT radix-2 over the
+    row index (kernels/fft_2d_rowpair.hpp) when run out of place; in place
+    they keep the row pass + R-row columns."""
+    return (log_rows >= 11 and log_cols >= 10) or (log_rows == 10 and log_cols >= 11)
 
 
 def rowpair_model(x):
@@ -431,7 +431,7 @@ def test_rowpair_geometry_stays_in_bounds():
     # (so the pass runs in place); the row pass's workgroups write rows 2r and
     # 2r + 1 of what they read from rows r and r + R/2, every row once
     for R, C in ((4096, 4096), (4096, 2048), (4096, 1024), (2048, 2048), (2048, 4096), (2048, 1024),
-                 (1024, 1024), (1024, 4096)):
+                 (1024, 2048), (1024, 4096)):
         g = 8 if R == 4096 else 16
         t0n, t1n, L = C // g, 2, R // 2
         t0 = np.arange(t0n)[:, None, None, None]
